@@ -1,0 +1,165 @@
+/*
+ * inferno_hip.h -- C ABI of the MI355X (gfx950) K-quant matvec library.
+ *
+ * This is the whole boundary: plain pointers, sizes and status codes, no
+ * HIP or torch types.  It replaces the native library behind Inferno.jl's
+ * QuantizedKernels / FusedKernels / Dequant call surface (paths relative to
+ * the Inferno.jl checkout):
+ *
+ *   src/QuantizedKernels.jl:84-148  ccall((:q4_k_gemv,...)), q5_k, q6_k, q8_0
+ *   src/kernels/quant_kernels.c:602-697  the C functions those ccalls bind
+ *   src/Dequant.jl:304-601          dequantize_q8_0/_q4_k/_q5_k/_q6_k
+ *   src/FusedKernels.jl:203-311     fused_mlp_gate_mul!, fused_silu_gate_mul!,
+ *                                   gpu_argmax!
+ *   src/ModelCPU.jl:482-508         mlp_forward (gate/up/SwiGLU/down)
+ *   src/ModelCPU.jl:1091-1123 + src/CommonOps.jl:142-163
+ *                                   lm_head_project! + greedy argmax
+ *   src/ModelCPU.jl:1001-1017       per-token prefill loop
+ *
+ * Conventions
+ *   - Every function returns int: IHIP_OK (0) or a negative IHIP_ERR_*.
+ *     ihip_last_error() returns a message for the calling thread's last
+ *     failure.  (The reference C returns void and only asserts.)
+ *   - Weights are GGML blocks, row-major: output row r owns blocks
+ *     [r*nb, (r+1)*nb) with nb = inner/256 (K-quants) or inner/32 (Q8_0);
+ *     `inner` is GGUF ne0 = length of x (src/ModelCPU.jl:296-297).
+ *   - Functions without a suffix take HOST pointers and are synchronous,
+ *     like the reference.  Weights passed by host pointer are uploaded once
+ *     and cached by address (they are immutable after load in the
+ *     reference); call ihip_weight_release before freeing or changing one.
+ *   - *_dev functions take DEVICE pointers and an `ihip_stream` (a
+ *     hipStream_t passed as void*, NULL = the null stream) and are
+ *     asynchronous.  Device weight pointers must be 16-byte aligned.
+ *   - Token ids are 0-based (Julia callers add 1).
+ *   - Calls from several threads are serialized inside the library; two
+ *     *_dev calls that share a workspace must not overlap on the GPU.
+ */
+#ifndef INFERNO_HIP_H
+#define INFERNO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IHIP_OK 0
+#define IHIP_ERR_INVALID (-1)     /* bad argument: type, shape, pointer, alignment */
+#define IHIP_ERR_HIP (-2)         /* a HIP runtime call failed */
+#define IHIP_ERR_NO_DEVICE (-3)   /* no usable gfx950 device */
+#define IHIP_ERR_NONFINITE (-4)   /* argmax saw NaN or +Inf (CommonOps.jl:149-152) */
+#define IHIP_ERR_DISABLED (-5)    /* IHIP_DISABLE is set in the environment */
+#define IHIP_ERR_NOMEM (-6)
+#define IHIP_ERR_EMPTY (-7)       /* argmax of an empty vector (CommonOps.jl:177) */
+
+/* GGML type ids (src/GGUF.jl:25-60) */
+#define IHIP_Q8_0 8
+#define IHIP_Q4_K 12
+#define IHIP_Q5_K 13
+#define IHIP_Q6_K 14
+
+/* argmax flag bits written to *flags */
+#define IHIP_FLAG_NAN 1u
+#define IHIP_FLAG_POSINF 2u
+#define IHIP_FLAG_ALL_NEGINF 4u
+
+typedef void *ihip_stream;
+
+/* ---- status / lifecycle ------------------------------------------------ */
+const char *ihip_last_error(void);
+int ihip_version(void);
+/* 1 when a gfx950 device is usable and IHIP_DISABLE is unset, else 0.
+ * Replaces quant_kernels_available (src/QuantizedKernels.jl:50-51). */
+int ihip_available(void);
+/* Select the device and create the library's stream (optional: the host
+ * entry points initialise device 0 on first use). */
+int ihip_init(int device);
+/* Free every cached weight and buffer. */
+int ihip_shutdown(void);
+/* Performance knobs (no effect on results): "rows_direct" (rows per wave of
+ * the Q4_K/Q5_K GEMV: 1, 2, 4, 8), "rows_staged" (Q6_K/Q8_0 GEMV: 1, 2, 4). */
+int ihip_set_tuning(const char *name, int value);
+
+/* ---- weight registry (host entry points use it implicitly) ------------ */
+/* Upload `bytes` of GGML blocks once; *handle names the device copy. */
+int ihip_weight_register(const void *host, size_t bytes, int ggml_type, int inner,
+                         int outer, uint64_t *handle);
+int ihip_weight_release(uint64_t handle);
+/* Release the cache entry of a host pointer (no-op if not cached). */
+int ihip_weight_forget(const void *host);
+/* Device address of a registered weight (for the *_dev entry points). */
+int ihip_weight_device_ptr(uint64_t handle, const void **dev);
+
+/* ---- drop-in mirrors of src/kernels/quant_kernels.c ------------------- */
+/* Same arguments as q{4,5,6}_k_gemv (quant_kernels.c:602, 620, 638); the
+ * Q8_K scratch argument is accepted and ignored (activations stay fp32). */
+int ihip_q4_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf_unused,
+                   int inner_dim, int outer_dim);
+int ihip_q5_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf_unused,
+                   int inner_dim, int outer_dim);
+int ihip_q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf_unused,
+                   int inner_dim, int outer_dim);
+/* Same arguments as q8_0_gemv (quant_kernels.c:657). */
+int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
+                   int outer_dim);
+
+/* ---- Dequant (src/Dequant.jl:304-601): bit-exact blocks -> fp32 -------- */
+/* n = number of elements; src holds n/256 (or n/32) blocks. */
+int ihip_dequantize(int ggml_type, const uint8_t *src, float *dst, int64_t n);
+
+/* ---- fused calls (host pointers, synchronous) ---------------------------- */
+/* mlp_forward, src/ModelCPU.jl:482-508: h = silu(Wg x) .* (Wu x), y = Wd h.
+ * wg, wu: inter x hidden; wd: hidden x inter. h may be NULL. */
+int ihip_ffn_swiglu(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
+                    int down_type, const uint8_t *wd, const float *x, float *h, float *y,
+                    int hidden, int inter);
+/* lm_head_project! + greedy token (ModelCPU.jl:1091-1123, CommonOps.jl:142-163):
+ * logits = W x (W: vocab x hidden), *token = lowest index of the max.
+ * logits may be NULL.  Returns IHIP_ERR_NONFINITE on NaN/+Inf logits. */
+int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *logits,
+                        int32_t *token, int hidden, int vocab);
+/* Batched prefill: Y[t,:] = W X[t,:] for t < T (W: outer x inner Q4_K);
+ * the activations are rounded to fp16 for the matrix cores. */
+int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inner,
+                      int outer);
+
+/* ---- device-pointer entry points (asynchronous on `stream`) -------------- */
+int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int inner,
+                  int outer, ihip_stream stream);
+int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n,
+                        ihip_stream stream);
+/* h = silu(Wg x) .* (Wu x), one pass over both weights (h: inter floats). */
+int ihip_gate_up_swiglu_dev(int gate_type, const void *wg, int up_type, const void *wu,
+                            const float *x, float *h, int hidden, int inter,
+                            ihip_stream stream);
+/* gate/up/SwiGLU then down: y = Wd h; h is caller-provided (inter floats). */
+int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *wu,
+                        int down_type, const void *wd, const float *x, float *h, float *y,
+                        int hidden, int inter, ihip_stream stream);
+/* Workspace for the argmax entry points: IHIP_ARGMAX_WS_BYTES of device
+ * memory, zeroed once before first use; every call leaves it zeroed. */
+#define IHIP_ARGMAX_WS_BYTES 256
+/* GEMV + fused greedy argmax.  logits may be NULL.  *token and *flags are
+ * device int32s (flags: IHIP_FLAG_* bits; the token is meaningless when
+ * NAN or POSINF is set). */
+int ihip_lm_head_argmax_dev(int ggml_type, const void *w, const float *x, float *logits,
+                            int32_t *token, uint32_t *flags, int hidden, int vocab,
+                            void *workspace, ihip_stream stream);
+/* gpu_argmax! (FusedKernels.jl:271-311) with _validate_logits semantics. */
+int ihip_argmax_dev(const float *logits, int64_t n, int32_t *token, uint32_t *flags,
+                    void *workspace, ihip_stream stream);
+/* fused_mlp_gate_mul! (FusedKernels.jl:203-214): gate = gate/(1+exp(-gate))*up */
+int ihip_fused_mlp_gate_mul_dev(float *gate, const float *up, int64_t n, ihip_stream stream);
+/* fused_silu_gate_mul! (FusedKernels.jl:219-230): out = x/(1+exp(-x))*gate */
+int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, int64_t n,
+                                 ihip_stream stream);
+/* X: T x inner fp32 (row-major), Y: T x outer fp32.  `xh` is caller scratch
+ * of T*inner fp16 values (2 bytes each) for the rounded activations. */
+int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
+                          int inner, int outer, ihip_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INFERNO_HIP_H */

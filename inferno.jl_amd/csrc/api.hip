@@ -1,0 +1,710 @@
+// api.hip -- the C ABI (include/inferno_hip.h): argument checks, the device
+// weight cache, host<->device staging for the host-pointer entry points,
+// and dispatch to the gfx950 kernels.
+//
+// Host-pointer entry points mirror the reference's synchronous C functions
+// (src/kernels/quant_kernels.c:602-697 behind src/QuantizedKernels.jl:84-148
+// of Inferno.jl).  Unlike the reference they report failures through a
+// status code and ihip_last_error() instead of returning void.
+#include "../../include/inferno_hip.h"
+#include "kq_common.h"
+#include "kq_launch.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+using namespace ihip;
+
+namespace {
+
+thread_local std::string t_err;
+
+int fail(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+#define HIPCHK(expr)                                                                          \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return fail(IHIP_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));          \
+    } while (0)
+
+#define RET_IF(expr)                                                                          \
+    do {                                                                                      \
+        int rc_ = (expr);                                                                     \
+        if (rc_ != IHIP_OK)                                                                   \
+            return rc_;                                                                       \
+    } while (0)
+
+struct Weight {
+    void *dev = nullptr;
+    size_t bytes = 0;
+    int type = 0, inner = 0, outer = 0;
+    const void *host = nullptr;
+};
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct Ctx {
+    std::recursive_mutex mu;
+    bool ready = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    std::unordered_map<uint64_t, Weight> by_handle;
+    std::unordered_map<const void *, uint64_t> by_host;
+    uint64_t next_handle = 1;
+    DevBuf x, y, h, t, src; // staging and scratch, grown on demand
+    void *argmax_ws = nullptr; // IHIP_ARGMAX_WS_BYTES, left zeroed by the kernels
+    int32_t *d_token = nullptr;
+    uint32_t *d_flags = nullptr;
+};
+
+Ctx &ctx()
+{
+    static Ctx c;
+    return c;
+}
+
+bool disabled()
+{
+    const char *e = getenv("IHIP_DISABLE");
+    return e && e[0] && strcmp(e, "0") != 0;
+}
+
+bool known_type(int t) { return block_elems(t) != 0; }
+
+size_t weight_bytes(int type, int inner, int outer)
+{
+    return (size_t)outer * (size_t)(inner / block_elems(type)) * (size_t)block_bytes(type);
+}
+
+int check_shape(int type, int inner, int outer)
+{
+    if (!known_type(type))
+        return fail(IHIP_ERR_INVALID, "unknown ggml type %d", type);
+    if (inner <= 0 || outer <= 0)
+        return fail(IHIP_ERR_INVALID, "inner=%d outer=%d must be positive", inner, outer);
+    if (inner % block_elems(type))
+        return fail(IHIP_ERR_INVALID, "inner=%d is not a multiple of %d for type %d", inner,
+                    block_elems(type), type);
+    return IHIP_OK;
+}
+
+bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int ensure(DevBuf &b, size_t need)
+{
+    if (b.cap >= need)
+        return IHIP_OK;
+    if (b.p)
+        HIPCHK(hipFree(b.p));
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t cap = need < 4096 ? 4096 : need;
+    HIPCHK(hipMalloc(&b.p, cap));
+    b.cap = cap;
+    return IHIP_OK;
+}
+
+int init_locked(int device)
+{
+    Ctx &c = ctx();
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (c.ready) {
+        if (device == c.device)
+            return IHIP_OK;
+        return fail(IHIP_ERR_INVALID, "already initialised on device %d", c.device);
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || n <= device)
+        return fail(IHIP_ERR_NO_DEVICE, "no HIP device %d (count %d)", device, n);
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(IHIP_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
+                    device, prop.gcnArchName);
+    HIPCHK(hipSetDevice(device));
+    HIPCHK(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    HIPCHK(hipMalloc(&c.argmax_ws, IHIP_ARGMAX_WS_BYTES + 64));
+    HIPCHK(hipMemset(c.argmax_ws, 0, IHIP_ARGMAX_WS_BYTES + 64));
+    c.d_token = (int32_t *)((char *)c.argmax_ws + IHIP_ARGMAX_WS_BYTES);
+    c.d_flags = (uint32_t *)((char *)c.argmax_ws + IHIP_ARGMAX_WS_BYTES + 32);
+    c.device = device;
+    c.ready = true;
+    return IHIP_OK;
+}
+
+int ready_locked()
+{
+    Ctx &c = ctx();
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (!c.ready)
+        return init_locked(0);
+    HIPCHK(hipSetDevice(c.device));
+    return IHIP_OK;
+}
+
+int release_handle_locked(uint64_t h)
+{
+    Ctx &c = ctx();
+    auto it = c.by_handle.find(h);
+    if (it == c.by_handle.end())
+        return fail(IHIP_ERR_INVALID, "unknown weight handle %llu", (unsigned long long)h);
+    if (it->second.host) {
+        auto hi = c.by_host.find(it->second.host);
+        if (hi != c.by_host.end() && hi->second == h)
+            c.by_host.erase(hi);
+    }
+    HIPCHK(hipFree(it->second.dev));
+    c.by_handle.erase(it);
+    return IHIP_OK;
+}
+
+int upload_locked(const void *host, size_t bytes, int type, int inner, int outer,
+                  bool cache_by_host, uint64_t *handle)
+{
+    Ctx &c = ctx();
+    Weight w;
+    w.bytes = bytes;
+    w.type = type;
+    w.inner = inner;
+    w.outer = outer;
+    w.host = cache_by_host ? host : nullptr;
+    HIPCHK(hipMalloc(&w.dev, bytes));
+    hipError_t e = hipMemcpy(w.dev, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(w.dev);
+        return fail(IHIP_ERR_HIP, "weight upload failed: %s", hipGetErrorString(e));
+    }
+    const uint64_t h = c.next_handle++;
+    c.by_handle[h] = w;
+    if (cache_by_host)
+        c.by_host[host] = h;
+    *handle = h;
+    return IHIP_OK;
+}
+
+// Device copy of a host weight, uploaded on first sight and cached by its
+// host address (weights are immutable after load in the reference).
+int resolve_locked(const void *host, int type, int inner, int outer, const void **dev)
+{
+    Ctx &c = ctx();
+    const size_t bytes = weight_bytes(type, inner, outer);
+    auto hi = c.by_host.find(host);
+    if (hi != c.by_host.end()) {
+        const Weight &w = c.by_handle[hi->second];
+        if (w.bytes == bytes && w.type == type && w.inner == inner && w.outer == outer) {
+            *dev = w.dev;
+            return IHIP_OK;
+        }
+        RET_IF(release_handle_locked(hi->second)); // same address, new shape: re-upload
+    }
+    uint64_t h = 0;
+    RET_IF(upload_locked(host, bytes, type, inner, outer, true, &h));
+    *dev = c.by_handle[h].dev;
+    return IHIP_OK;
+}
+
+// Fast kernels need 16-byte aligned weights and x, and (staged formats)
+// 16-byte aligned rows: Q6_K rows of a multiple of 8 blocks, Q8_0 rows of a
+// multiple of 8 blocks.
+bool fast_ok(int type, const void *w, const float *x, int inner)
+{
+    if (!al16(w) || !al16(x))
+        return false;
+    if (type == kQ6_K)
+        return inner % 2048 == 0;
+    if (type == kQ8_0)
+        return inner % 256 == 0;
+    return true;
+}
+
+int gemv_dev_locked(int type, const void *w, const float *x, float *out, int inner, int outer,
+                    hipStream_t s)
+{
+    RET_IF(check_shape(type, inner, outer));
+    if (!w || !x || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    hipError_t e = fast_ok(type, w, x, inner) ? launch_gemv(type, w, x, out, inner, outer, s)
+                                              : launch_gemv_generic(type, w, x, out, inner, outer, s);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "gemv launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int gate_up_dev_locked(int gt, const void *wg, int ut, const void *wu, const float *x, float *h,
+                       int hidden, int inter, hipStream_t s)
+{
+    RET_IF(check_shape(gt, hidden, inter));
+    RET_IF(check_shape(ut, hidden, inter));
+    if (!wg || !wu || !x || !h)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (gate_up_fusable(gt, ut) && fast_ok(gt, wg, x, hidden) && al16(wu)) {
+        hipError_t e = launch_gate_up_swiglu(gt, wg, wu, x, h, hidden, inter, s);
+        if (e != hipSuccess)
+            return fail(IHIP_ERR_HIP, "gate/up launch failed: %s", hipGetErrorString(e));
+        return IHIP_OK;
+    }
+    // unfused: g -> h, u -> scratch, then h = silu(h) * u
+    Ctx &c = ctx();
+    RET_IF(ensure(c.t, sizeof(float) * (size_t)inter));
+    RET_IF(gemv_dev_locked(gt, wg, x, h, hidden, inter, s));
+    RET_IF(gemv_dev_locked(ut, wu, x, (float *)c.t.p, hidden, inter, s));
+    hipError_t e = launch_mlp_gate_mul(h, (const float *)c.t.p, inter, s);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "swiglu launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, int32_t *token,
+                       uint32_t *flags, int hidden, int vocab, void *ws, hipStream_t s)
+{
+    RET_IF(check_shape(type, hidden, vocab));
+    if (!w || !x || !token || !flags || !ws)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if ((type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden)) {
+        hipError_t e = launch_lm_head_argmax(type, w, x, logits, token, flags, hidden, vocab, ws, s);
+        if (e != hipSuccess)
+            return fail(IHIP_ERR_HIP, "lm_head launch failed: %s", hipGetErrorString(e));
+        return IHIP_OK;
+    }
+    float *lg = logits;
+    if (!lg) {
+        RET_IF(ensure(ctx().t, sizeof(float) * (size_t)vocab));
+        lg = (float *)ctx().t.p;
+    }
+    RET_IF(gemv_dev_locked(type, w, x, lg, hidden, vocab, s));
+    hipError_t e = launch_argmax(lg, vocab, token, flags, ws, s);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "argmax launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int copy_in(DevBuf &b, const void *host, size_t bytes)
+{
+    RET_IF(ensure(b, bytes));
+    HIPCHK(hipMemcpyAsync(b.p, host, bytes, hipMemcpyHostToDevice, ctx().stream));
+    return IHIP_OK;
+}
+
+int host_gemv(int type, const uint8_t *w, const float *x, float *out, int inner, int outer)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(type, inner, outer));
+    if (!w || !x || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const void *dw = nullptr;
+    RET_IF(resolve_locked(w, type, inner, outer, &dw));
+    RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)inner));
+    RET_IF(ensure(c.y, sizeof(float) * (size_t)outer));
+    RET_IF(gemv_dev_locked(type, dw, (const float *)c.x.p, (float *)c.y.p, inner, outer, c.stream));
+    HIPCHK(hipMemcpyAsync(out, c.y.p, sizeof(float) * (size_t)outer, hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *ihip_last_error(void) { return t_err.c_str(); }
+
+int ihip_version(void) { return 10000; }
+
+int ihip_available(void)
+{
+    if (disabled())
+        return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess)
+        return 0;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int ihip_init(int device)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    return init_locked(device);
+}
+
+int ihip_shutdown(void)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    if (!c.ready)
+        return IHIP_OK;
+    (void)hipSetDevice(c.device);
+    (void)hipStreamSynchronize(c.stream);
+    for (auto &kv : c.by_handle)
+        (void)hipFree(kv.second.dev);
+    c.by_handle.clear();
+    c.by_host.clear();
+    for (DevBuf *b : {&c.x, &c.y, &c.h, &c.t, &c.src}) {
+        if (b->p)
+            (void)hipFree(b->p);
+        b->p = nullptr;
+        b->cap = 0;
+    }
+    (void)hipFree(c.argmax_ws);
+    c.argmax_ws = nullptr;
+    (void)hipStreamDestroy(c.stream);
+    c.stream = nullptr;
+    c.ready = false;
+    c.device = -1;
+    return IHIP_OK;
+}
+
+int ihip_set_tuning(const char *name, int value)
+{
+    if (!name)
+        return fail(IHIP_ERR_INVALID, "null name");
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    set_tuning(name, value);
+    set_prefill_tuning(name, value);
+    return IHIP_OK;
+}
+
+int ihip_weight_register(const void *host, size_t bytes, int ggml_type, int inner, int outer,
+                         uint64_t *handle)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(ggml_type, inner, outer));
+    if (!host || !handle)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (bytes < weight_bytes(ggml_type, inner, outer))
+        return fail(IHIP_ERR_INVALID, "%zu bytes < %zu needed for %dx%d type %d", bytes,
+                    weight_bytes(ggml_type, inner, outer), outer, inner, ggml_type);
+    return upload_locked(host, weight_bytes(ggml_type, inner, outer), ggml_type, inner, outer,
+                         false, handle);
+}
+
+int ihip_weight_release(uint64_t handle)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    return release_handle_locked(handle);
+}
+
+int ihip_weight_forget(const void *host)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    auto it = c.by_host.find(host);
+    if (it == c.by_host.end())
+        return IHIP_OK;
+    return release_handle_locked(it->second);
+}
+
+int ihip_weight_device_ptr(uint64_t handle, const void **dev)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    auto it = c.by_handle.find(handle);
+    if (it == c.by_handle.end() || !dev)
+        return fail(IHIP_ERR_INVALID, "unknown weight handle %llu", (unsigned long long)handle);
+    *dev = it->second.dev;
+    return IHIP_OK;
+}
+
+int ihip_q4_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf_unused,
+                   int inner_dim, int outer_dim)
+{
+    (void)q8_buf_unused;
+    return host_gemv(kQ4_K, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_q5_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf_unused,
+                   int inner_dim, int outer_dim)
+{
+    (void)q8_buf_unused;
+    return host_gemv(kQ5_K, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf_unused,
+                   int inner_dim, int outer_dim)
+{
+    (void)q8_buf_unused;
+    return host_gemv(kQ6_K, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
+                   int outer_dim)
+{
+    return host_gemv(kQ8_0, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_dequantize(int ggml_type, const uint8_t *src, float *dst, int64_t n)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    if (!known_type(ggml_type))
+        return fail(IHIP_ERR_INVALID, "unknown ggml type %d", ggml_type);
+    if (n < 0 || n % block_elems(ggml_type))
+        return fail(IHIP_ERR_INVALID, "n=%lld is not a multiple of %d", (long long)n,
+                    block_elems(ggml_type));
+    if (n == 0)
+        return IHIP_OK;
+    if (!src || !dst)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const size_t in_bytes = (size_t)(n / block_elems(ggml_type)) * block_bytes(ggml_type);
+    RET_IF(copy_in(c.src, src, in_bytes));
+    RET_IF(ensure(c.y, sizeof(float) * (size_t)n));
+    hipError_t e = launch_dequant(ggml_type, c.src.p, (float *)c.y.p, n, true, c.stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "dequant launch failed: %s", hipGetErrorString(e));
+    HIPCHK(hipMemcpyAsync(dst, c.y.p, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+int ihip_ffn_swiglu(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
+                    int down_type, const uint8_t *wd, const float *x, float *h, float *y,
+                    int hidden, int inter)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(gate_type, hidden, inter));
+    RET_IF(check_shape(up_type, hidden, inter));
+    RET_IF(check_shape(down_type, inter, hidden));
+    if (!wg || !wu || !wd || !x || !y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const void *dg, *du, *dd;
+    RET_IF(resolve_locked(wg, gate_type, hidden, inter, &dg));
+    RET_IF(resolve_locked(wu, up_type, hidden, inter, &du));
+    RET_IF(resolve_locked(wd, down_type, inter, hidden, &dd));
+    RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)hidden));
+    RET_IF(ensure(c.h, sizeof(float) * (size_t)inter));
+    RET_IF(ensure(c.y, sizeof(float) * (size_t)hidden));
+    RET_IF(gate_up_dev_locked(gate_type, dg, up_type, du, (const float *)c.x.p, (float *)c.h.p,
+                              hidden, inter, c.stream));
+    RET_IF(gemv_dev_locked(down_type, dd, (const float *)c.h.p, (float *)c.y.p, inter, hidden,
+                           c.stream));
+    if (h)
+        HIPCHK(hipMemcpyAsync(h, c.h.p, sizeof(float) * (size_t)inter, hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipMemcpyAsync(y, c.y.p, sizeof(float) * (size_t)hidden, hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *logits,
+                        int32_t *token, int hidden, int vocab)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(ggml_type, hidden, vocab));
+    if (!w || !x || !token)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const void *dw;
+    RET_IF(resolve_locked(w, ggml_type, hidden, vocab, &dw));
+    RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)hidden));
+    float *dlog = nullptr;
+    if (logits) {
+        RET_IF(ensure(c.y, sizeof(float) * (size_t)vocab));
+        dlog = (float *)c.y.p;
+    }
+    RET_IF(lm_head_dev_locked(ggml_type, dw, (const float *)c.x.p, dlog, c.d_token, c.d_flags,
+                              hidden, vocab, c.argmax_ws, c.stream));
+    int32_t tok = 0;
+    uint32_t fl = 0;
+    HIPCHK(hipMemcpyAsync(&tok, c.d_token, 4, hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipMemcpyAsync(&fl, c.d_flags, 4, hipMemcpyDeviceToHost, c.stream));
+    if (logits)
+        HIPCHK(hipMemcpyAsync(logits, dlog, sizeof(float) * (size_t)vocab, hipMemcpyDeviceToHost,
+                              c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    if (fl & IHIP_FLAG_NAN)
+        return fail(IHIP_ERR_NONFINITE, "logits must not contain NaN");
+    if (fl & IHIP_FLAG_POSINF)
+        return fail(IHIP_ERR_NONFINITE, "logits must not contain +Inf");
+    *token = tok;
+    return IHIP_OK;
+}
+
+int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inner, int outer)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(kQ4_K, inner, outer));
+    if (T <= 0)
+        return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if (!w || !X || !Y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const void *dw;
+    RET_IF(resolve_locked(w, kQ4_K, inner, outer, &dw));
+    RET_IF(copy_in(c.x, X, sizeof(float) * (size_t)T * inner));
+    RET_IF(ensure(c.h, 2 * (size_t)T * inner));
+    RET_IF(ensure(c.y, sizeof(float) * (size_t)T * outer));
+    hipError_t e = launch_prefill_q4k(dw, (const float *)c.x.p, c.h.p, (float *)c.y.p, T, inner,
+                                      outer, c.stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
+    HIPCHK(hipMemcpyAsync(Y, c.y.p, sizeof(float) * (size_t)T * outer, hipMemcpyDeviceToHost,
+                          c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+// ---- device-pointer entry points ----------------------------------------
+
+int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int inner, int outer,
+                  ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream);
+}
+
+int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (!known_type(ggml_type))
+        return fail(IHIP_ERR_INVALID, "unknown ggml type %d", ggml_type);
+    if (n < 0 || n % block_elems(ggml_type))
+        return fail(IHIP_ERR_INVALID, "n=%lld is not a multiple of %d", (long long)n,
+                    block_elems(ggml_type));
+    if (n == 0)
+        return IHIP_OK;
+    if (!src || !dst)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    hipError_t e = launch_dequant(ggml_type, src, dst, n, al16(src) && al16(dst), (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "dequant launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_gate_up_swiglu_dev(int gate_type, const void *wg, int up_type, const void *wu,
+                            const float *x, float *h, int hidden, int inter, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    return gate_up_dev_locked(gate_type, wg, up_type, wu, x, h, hidden, inter, (hipStream_t)stream);
+}
+
+int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *wu,
+                        int down_type, const void *wd, const float *x, float *h, float *y,
+                        int hidden, int inter, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(down_type, inter, hidden));
+    if (!wd || !y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    RET_IF(gate_up_dev_locked(gate_type, wg, up_type, wu, x, h, hidden, inter, (hipStream_t)stream));
+    return gemv_dev_locked(down_type, wd, h, y, inter, hidden, (hipStream_t)stream);
+}
+
+int ihip_lm_head_argmax_dev(int ggml_type, const void *w, const float *x, float *logits,
+                            int32_t *token, uint32_t *flags, int hidden, int vocab, void *workspace,
+                            ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    return lm_head_dev_locked(ggml_type, w, x, logits, token, flags, hidden, vocab, workspace,
+                              (hipStream_t)stream);
+}
+
+int ihip_argmax_dev(const float *logits, int64_t n, int32_t *token, uint32_t *flags,
+                    void *workspace, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (n == 0)
+        return fail(IHIP_ERR_EMPTY, "logits must not be empty");
+    if (n < 0 || n >= 0xffffffffll)
+        return fail(IHIP_ERR_INVALID, "n=%lld out of range", (long long)n);
+    if (!logits || !token || !flags || !workspace)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    hipError_t e = launch_argmax(logits, n, token, flags, workspace, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "argmax launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_fused_mlp_gate_mul_dev(float *gate, const float *up, int64_t n, ihip_stream stream)
+{
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (n < 0)
+        return fail(IHIP_ERR_INVALID, "n < 0");
+    if (n == 0)
+        return IHIP_OK;
+    if (!gate || !up)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    hipError_t e = launch_mlp_gate_mul(gate, up, n, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, int64_t n,
+                                 ihip_stream stream)
+{
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (n < 0)
+        return fail(IHIP_ERR_INVALID, "n < 0");
+    if (n == 0)
+        return IHIP_OK;
+    if (!out || !x || !gate)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    hipError_t e = launch_silu_gate_mul(out, x, gate, n, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T, int inner,
+                          int outer, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(kQ4_K, inner, outer));
+    if (T <= 0)
+        return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if (!w || !X || !xh || !Y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (!al16(w) || !al16(X) || !al16(xh) || !al16(Y))
+        return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    hipError_t e = launch_prefill_q4k(w, X, xh, Y, T, inner, outer, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,95 @@
+// kq_common.h -- shared definitions for the gfx950 K-quant kernels.
+//
+// Block layouts (src/kernels/quant_kernels.c:24-62, src/Dequant.jl:311-316,
+// 336-341, 392-400, 570-574 of Inferno.jl), little-endian:
+//   Q4_K 144 B: d f16 @0, dmin f16 @2, scales[12] @4, qs[128] @16
+//   Q5_K 176 B: d @0, dmin @2, scales[12] @4, qh[32] @16, qs[128] @48
+//   Q6_K 210 B: ql[128] @0, qh[64] @128, scales int8[16] @192, d f16 @208
+//   Q8_0  34 B: d f16 @0, qs int8[32] @2
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ihip {
+
+constexpr int kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14;
+
+constexpr int kBytesQ4K = 144, kBytesQ5K = 176, kBytesQ6K = 210, kBytesQ80 = 34;
+
+__host__ __device__ constexpr int block_bytes(int t)
+{
+    return t == kQ4_K ? 144 : t == kQ5_K ? 176 : t == kQ6_K ? 210 : t == kQ8_0 ? 34 : 0;
+}
+__host__ __device__ constexpr int block_elems(int t)
+{
+    return (t == kQ4_K || t == kQ5_K || t == kQ6_K) ? 256 : t == kQ8_0 ? 32 : 0;
+}
+
+// fp16 bits -> fp32.  v_cvt_f32_f16 widens exactly, fp16 subnormals
+// included (the kernels run with fp16/fp64 denormals enabled, the HIP
+// default; the exhaustive dequant test checks all 65536 patterns).
+__device__ __forceinline__ float h2f(uint32_t bits16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// The 6-bit scale (sc) and min (m) of sub-block i of a Q4_K/Q5_K block,
+// from the 12 packed bytes held as three dwords s0 (bytes 0-3), s1 (4-7)
+// and s2 (8-11): src/Dequant.jl:345-362.
+//   i < 4:  sc = s[i] & 63,                        m = s[i+4] & 63
+//   i >= 4: sc = (s[i+4] & 15) | (s[i-4] >> 6) << 4, m = (s[i+4] >> 4) | (s[i] >> 6) << 4
+__device__ __forceinline__ void k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int i,
+                                            uint32_t &sc, uint32_t &m)
+{
+    if (i < 4) {
+        sc = (s0 >> (8 * i)) & 63u;
+        m = (s1 >> (8 * i)) & 63u;
+    } else {
+        const int k = 8 * (i - 4);
+        sc = ((s2 >> k) & 15u) | (((s0 >> (k + 6)) & 3u) << 4);
+        m = ((s2 >> (k + 4)) & 15u) | (((s1 >> (k + 6)) & 3u) << 4);
+    }
+}
+
+// Sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Read 8 bytes starting at byte `off` of a 4-byte-aligned LDS array as two
+// dwords.  The dword reads stay 4-byte aligned; the byte phase (off & 3) is
+// taken out with v_alignbyte.  `off` must be relative to the aligned array
+// base, not to a block inside it (Q6_K blocks are 210 bytes, so odd blocks
+// start 2 bytes past a dword boundary).
+__device__ __forceinline__ void lds_read8_even(const uint8_t *lds, uint32_t off, uint32_t &a,
+                                               uint32_t &b)
+{
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(lds + (off & ~3u));
+    const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+    const uint32_t sh = off & 3u;
+    a = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    b = __builtin_amdgcn_alignbyte(w2, w1, sh);
+}
+
+__device__ __forceinline__ uint32_t lds_read_u16(const uint8_t *lds, uint32_t off)
+{
+    return *reinterpret_cast<const uint16_t *>(lds + off);
+}
+
+// Signed byte k (0..3) of a dword, as float.
+__device__ __forceinline__ float sbyte_f(uint32_t w, int k)
+{
+    return (float)(int32_t)(int8_t)(w >> (8 * k));
+}
+// Unsigned byte k of a dword, as float (v_cvt_f32_ubyte{k}).
+__device__ __forceinline__ float ubyte_f(uint32_t w, int k)
+{
+    return (float)((w >> (8 * k)) & 0xffu);
+}
+
+} // namespace ihip

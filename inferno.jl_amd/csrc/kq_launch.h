@@ -1,0 +1,36 @@
+// kq_launch.h -- internal launchers shared by the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ihip {
+
+// kq_gemv.hip
+hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
+                       hipStream_t s);
+bool gate_up_fusable(int gate_type, int up_type);
+hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,
+                                 float *h, int hidden, int inter, hipStream_t s);
+hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
+                                 int32_t *token, uint32_t *flags, int hidden, int vocab,
+                                 void *ws, hipStream_t s);
+hipError_t launch_argmax(const float *v, int64_t n, int32_t *token, uint32_t *flags, void *ws,
+                         hipStream_t s);
+void set_tuning(const char *name, int value);
+
+// kq_dequant.hip
+hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y, int inner,
+                               int outer, hipStream_t s);
+hipError_t launch_dequant(int type, const void *src, float *dst, int64_t n, bool aligned,
+                          hipStream_t s);
+hipError_t launch_mlp_gate_mul(float *gate, const float *up, int64_t n, hipStream_t s);
+hipError_t launch_silu_gate_mul(float *out, const float *x, const float *gate, int64_t n,
+                                hipStream_t s);
+
+// kq_prefill.hip
+hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
+                              int inner, int outer, hipStream_t s);
+void set_prefill_tuning(const char *name, int value);
+
+} // namespace ihip

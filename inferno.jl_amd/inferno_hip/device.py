@@ -1,0 +1,143 @@
+"""Device-resident entry points over torch CUDA(HIP) tensors.
+
+torch only provides device memory and the stream here; all computation runs
+in libinferno_hip.so.  Each function takes device tensors, launches on
+torch's current stream (or ``stream``) and returns without synchronizing.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import Q4_K, IHIPArgumentError, check, lib
+from .synth import BLOCK_BYTES, BLOCK_ELEMS
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _ptr(t: torch.Tensor, dtype=None, what="tensor") -> int:
+    if not t.is_cuda:
+        raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, f"{what} must be a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, f"{what} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, f"{what} must be contiguous")
+    return t.data_ptr()
+
+
+@dataclass
+class DeviceWeight:
+    """GGML blocks of an ``outer x inner`` row-major matrix in device memory."""
+    data: torch.Tensor        # uint8, device
+    ggml_type: int
+    inner: int
+    outer: int
+
+    @classmethod
+    def upload(cls, host_bytes, ggml_type: int, inner: int, outer: int, device="cuda"):
+        t = torch.as_tensor(host_bytes, dtype=torch.uint8).to(device)
+        w = cls(t, ggml_type, inner, outer)
+        w.validate()
+        return w
+
+    def validate(self):
+        be = BLOCK_ELEMS[self.ggml_type]
+        need = self.outer * (self.inner // be) * BLOCK_BYTES[self.ggml_type]
+        if self.inner % be or self.data.numel() < need:
+            raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, "weight bytes do not match the shape")
+
+    @property
+    def nbytes(self) -> int:
+        return self.outer * (self.inner // BLOCK_ELEMS[self.ggml_type]) * BLOCK_BYTES[self.ggml_type]
+
+
+class ArgmaxWorkspace:
+    """IHIP_ARGMAX_WS_BYTES of zeroed device memory plus the token/flags
+    outputs; the kernels leave the workspace zeroed after every call."""
+
+    def __init__(self, device="cuda"):
+        self.ws = torch.zeros(_lib.ARGMAX_WS_BYTES, dtype=torch.uint8, device=device)
+        self.token = torch.zeros(1, dtype=torch.int32, device=device)
+        self.flags = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def result(self) -> int:
+        """Synchronize and return the 0-based token, raising like
+        src/CommonOps.jl:149-152 on NaN/+Inf."""
+        torch.cuda.synchronize()
+        fl = int(self.flags.item())
+        if fl & _lib.FLAG_NAN:
+            raise IHIPArgumentError(_lib.IHIP_ERR_NONFINITE, "logits must not contain NaN")
+        if fl & _lib.FLAG_POSINF:
+            raise IHIPArgumentError(_lib.IHIP_ERR_NONFINITE, "logits must not contain +Inf")
+        return int(self.token.item())
+
+
+def gemv(w: DeviceWeight, x: torch.Tensor, out: torch.Tensor = None, stream=None):
+    if out is None:
+        out = torch.empty(w.outer, dtype=torch.float32, device=x.device)
+    check(lib().ihip_gemv_dev(w.ggml_type, _ptr(w.data, torch.uint8, "w"), _ptr(x, torch.float32, "x"),
+                              _ptr(out, torch.float32, "out"), w.inner, w.outer, _stream(stream)))
+    return out
+
+
+def dequantize(w: DeviceWeight, out: torch.Tensor = None, stream=None):
+    n = w.inner * w.outer
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=w.data.device)
+    check(lib().ihip_dequantize_dev(w.ggml_type, _ptr(w.data, torch.uint8, "w"),
+                                    _ptr(out, torch.float32, "out"), n, _stream(stream)))
+    return out
+
+
+def gate_up_swiglu(wg: DeviceWeight, wu: DeviceWeight, x, h=None, stream=None):
+    if h is None:
+        h = torch.empty(wg.outer, dtype=torch.float32, device=x.device)
+    check(lib().ihip_gate_up_swiglu_dev(wg.ggml_type, _ptr(wg.data), wu.ggml_type, _ptr(wu.data),
+                                        _ptr(x, torch.float32, "x"), _ptr(h, torch.float32, "h"),
+                                        wg.inner, wg.outer, _stream(stream)))
+    return h
+
+
+def ffn_swiglu(wg: DeviceWeight, wu: DeviceWeight, wd: DeviceWeight, x, h=None, y=None, stream=None):
+    if h is None:
+        h = torch.empty(wg.outer, dtype=torch.float32, device=x.device)
+    if y is None:
+        y = torch.empty(wd.outer, dtype=torch.float32, device=x.device)
+    check(lib().ihip_ffn_swiglu_dev(wg.ggml_type, _ptr(wg.data), wu.ggml_type, _ptr(wu.data),
+                                    wd.ggml_type, _ptr(wd.data), _ptr(x, torch.float32, "x"),
+                                    _ptr(h, torch.float32, "h"), _ptr(y, torch.float32, "y"),
+                                    wg.inner, wg.outer, _stream(stream)))
+    return y
+
+
+def lm_head_argmax(w: DeviceWeight, x, ws: ArgmaxWorkspace, logits=None, stream=None):
+    lp = _ptr(logits, torch.float32, "logits") if logits is not None else None
+    check(lib().ihip_lm_head_argmax_dev(w.ggml_type, _ptr(w.data), _ptr(x, torch.float32, "x"), lp,
+                                        ws.token.data_ptr(), ws.flags.data_ptr(), w.inner, w.outer,
+                                        ws.ws.data_ptr(), _stream(stream)))
+    return logits
+
+
+def argmax(logits: torch.Tensor, ws: ArgmaxWorkspace, stream=None):
+    check(lib().ihip_argmax_dev(_ptr(logits, torch.float32, "logits"), logits.numel(),
+                                ws.token.data_ptr(), ws.flags.data_ptr(), ws.ws.data_ptr(),
+                                _stream(stream)))
+
+
+def prefill_q4_k(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, xh: torch.Tensor = None,
+                 stream=None):
+    if w.ggml_type != Q4_K:
+        raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, "prefill takes a Q4_K weight")
+    T = X.shape[0]
+    if xh is None:
+        xh = torch.empty(T * w.inner, dtype=torch.float16, device=X.device)
+    if Y is None:
+        Y = torch.empty(T, w.outer, dtype=torch.float32, device=X.device)
+    check(lib().ihip_prefill_q4_k_dev(_ptr(w.data), _ptr(X, torch.float32, "X"), _ptr(xh), _ptr(Y, torch.float32, "Y"),
+                                      T, w.inner, w.outer, _stream(stream)))
+    return Y

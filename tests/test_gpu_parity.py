@@ -1,0 +1,383 @@
+"""GPU parity: the gfx950 kernels against the CPU oracle on seeded inputs.
+
+Bars (the reference CPU semantics restated in oracle/):
+* standalone dequant: bit-exact;
+* fp32-accumulated GEMV / GEMM: |y - y_ref| <= 1e-4 * ||w_row||_2 * ||x||_2,
+  y_ref accumulated in fp64 over the exact dequantized weights;
+* argmax token ids: bit-exact (lowest index of the maximum).
+Every call goes through the C ABI (libinferno_hip.so).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from inferno_hip import _lib
+    assert _lib.available(), "libinferno_hip.so reports no usable gfx950 device"
+    yield
+    torch.cuda.synchronize()
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.to("cuda") if dtype is None else t.to("cuda", dtype)
+
+
+def dweight(w, t, inner, outer):
+    from inferno_hip.device import DeviceWeight
+    return DeviceWeight(dev(w), t, inner, outer)
+
+
+def assert_within(y, ref, tol, what):
+    err = np.abs(np.asarray(y, np.float64) - ref)
+    ratio = float(np.max(err / tol))
+    say(f"{what}: max err/tol = {ratio:.3e}")
+    assert np.all(err <= tol), f"{what}: {np.sum(err > tol)} outputs over tolerance (max ratio {ratio})"
+
+
+# ------------------------------------------------------------- dequant ----
+
+def test_dequant_all_half_patterns_bit_exact():
+    say("dequant Q8_0: all 65536 fp16 scale patterns")
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    blocks = np.zeros((65536, 34), dtype=np.uint8)
+    blocks[:, 0:2] = h.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:34] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    n = 65536 * 32
+    from inferno_hip import device as D
+    got = D.dequantize(dweight(blocks.reshape(-1), synth.Q8_0, n, 1)).cpu().numpy()
+    want = oracle.dequant(synth.Q8_0, blocks.reshape(-1), n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,outer,inner", [
+    (synth.Q8_0, 4096, 4096),   # the standalone-dequant workload, full size
+    (synth.Q4_K, 1024, 4096),
+    (synth.Q5_K, 512, 4096),
+    (synth.Q6_K, 512, 2048),
+    (synth.Q6_K, 3, 768),       # 9 blocks: not a multiple of 8 -> generic path
+    (synth.Q8_0, 5, 96),        # 15 blocks -> generic path
+    (synth.Q4_K, 1, 256),
+])
+def test_dequant_bit_exact(t, outer, inner):
+    say(f"dequant type={t} {outer}x{inner}")
+    rng = synth.rng_for(1000 + t + inner)
+    w = synth.weight(rng, t, outer, inner)
+    from inferno_hip import device as D
+    got = D.dequantize(dweight(w, t, inner, outer)).cpu().numpy()
+    want = oracle.dequant(t, w, outer * inner)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0])
+def test_dequant_host_entry_point_and_misaligned_source(t):
+    say(f"Dequant host mirror type={t}")
+    from inferno_hip import Dequant, device as D
+    rng = synth.rng_for(77 + t)
+    inner = 2048
+    w = synth.weight(rng, t, 4, inner)
+    want = oracle.dequant(t, w, 4 * inner)
+    got = Dequant.dequantize(t, w, 4 * inner)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a source that starts 2 bytes past a 16-byte boundary takes the generic kernel
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    buf[2:2 + w.size] = dev(w)
+    dw = D.DeviceWeight(buf[2:2 + w.size], t, inner, 4)
+    got2 = D.dequantize(dw).cpu().numpy()
+    assert np.array_equal(got2.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMV ----
+
+GEMV_CASES = [
+    (synth.Q4_K, 4096, 4096),     # the headline decode GEMV
+    (synth.Q4_K, 12288, 4096),    # FFN gate/up shape
+    (synth.Q4_K, 37, 2304),       # ragged rows, partial 2048-column segment
+    (synth.Q4_K, 1, 256),
+    (synth.Q5_K, 4096, 4096),
+    (synth.Q5_K, 9, 768),
+    (synth.Q6_K, 4096, 12288),    # FFN down shape
+    (synth.Q6_K, 300, 2048),
+    (synth.Q6_K, 7, 768),         # row stride not 16-byte aligned -> generic kernel
+    (synth.Q8_0, 4096, 4096),
+    (synth.Q8_0, 11, 2304),       # partial 64-block segment
+    (synth.Q8_0, 6, 96),          # generic kernel
+]
+
+
+@pytest.mark.parametrize("t,outer,inner", GEMV_CASES)
+def test_gemv_device(t, outer, inner):
+    say(f"gemv_dev type={t} {outer}x{inner}")
+    rng = synth.rng_for(0xC0 + t * 7 + inner + outer)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner)
+    from inferno_hip import device as D
+    y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
+    assert_within(y, ref, tol, f"type {t} {outer}x{inner}")
+
+
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0])
+def test_gemv_host_mirror_and_weight_cache(t):
+    from inferno_hip import QuantizedKernels as QK
+    fn = {synth.Q4_K: QK.q4_k_gemv_, synth.Q5_K: QK.q5_k_gemv_, synth.Q6_K: QK.q6_k_gemv_,
+          synth.Q8_0: QK.q8_0_gemv_}[t]
+    rng = synth.rng_for(5 + t)
+    outer, inner = 256, 4096
+    w = synth.weight(rng, t, outer, inner)
+    tol_n = oracle.row_norms(t, w, inner, outer)
+    for rep in range(3):  # same weight buffer, new x: the cached device copy is reused
+        say(f"host mirror type={t} rep={rep}")
+        x = synth.activations(rng, inner) * np.float32(10.0 ** (rep - 1))
+        out = np.zeros(outer, np.float32)
+        fn(out, w, x, inner, outer)
+        assert_within(out, oracle.gemv_f64(t, w, x, inner, outer), oracle.tolerance(tol_n, x),
+                      f"host type {t} rep {rep}")
+    # new bytes in the same host buffer: forget() drops the stale device copy
+    w[:] = synth.weight(rng, t, outer, inner)
+    QK.forget(w)
+    x = synth.activations(rng, inner)
+    out = np.zeros(outer, np.float32)
+    fn(out, w, x, inner, outer)
+    assert_within(out, oracle.gemv_f64(t, w, x, inner, outer),
+                  oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), "after forget")
+
+
+def test_gemv_special_inputs():
+    from inferno_hip import device as D
+    rng = synth.rng_for(4242)
+    outer, inner = 64, 4096
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    dw = dweight(w, synth.Q4_K, inner, outer)
+    say("gemv zero x")
+    y = D.gemv(dw, torch.zeros(inner, device="cuda")).cpu().numpy()
+    assert np.all(y == 0)
+    say("gemv one-hot x pins columns")
+    W = oracle.dequant(synth.Q4_K, w, outer * inner).reshape(outer, inner)
+    for c in (0, 31, 32, 63, 64, 255, 256, 2047, 2048, 4095):
+        e = np.zeros(inner, np.float32)
+        e[c] = 1.0
+        y = D.gemv(dw, dev(e)).cpu().numpy()
+        assert np.allclose(y, W[:, c], rtol=2e-6, atol=1e-9), c
+
+
+# ---------------------------------------------------- SwiGLU / FFN block ----
+
+def _ffn_case(hidden, inter, gt=synth.Q4_K, dt=synth.Q6_K, seed=0xC3):
+    rng = synth.rng_for(seed)
+    wg = synth.weight(rng, gt, inter, hidden)
+    wu = synth.weight(rng, gt, inter, hidden)
+    wd = synth.weight(rng, dt, hidden, inter)
+    x = synth.activations(rng, hidden)
+    return wg, wu, wd, x
+
+
+def _h_bound(g, u, ng, nu, x):
+    tg = oracle.tolerance(ng, x)
+    tu = oracle.tolerance(nu, x)
+    s = 1 / (1 + np.exp(-g))
+    silu = g * s
+    dsilu = s * (1 + g * (1 - s))
+    return np.abs(dsilu * u) * tg + np.abs(silu) * tu + 1e-6 * np.abs(silu * u) + 1e-30
+
+
+@pytest.mark.parametrize("hidden,inter,gt,dt", [
+    (4096, 12288, synth.Q4_K, synth.Q6_K),   # the decode FFN block, full size
+    (2048, 5632, synth.Q5_K, synth.Q6_K),
+    (1024, 2816, synth.Q4_K, synth.Q8_0),
+    (512, 768, synth.Q8_0, synth.Q4_K),      # unfused gate/up path
+])
+def test_ffn_block(hidden, inter, gt, dt):
+    say(f"ffn hidden={hidden} inter={inter} gate/up={gt} down={dt}")
+    wg, wu, wd, x = _ffn_case(hidden, inter, gt, dt)
+    from inferno_hip import device as D
+    h = torch.empty(inter, device="cuda")
+    y = D.ffn_swiglu(dweight(wg, gt, hidden, inter), dweight(wu, gt, hidden, inter),
+                     dweight(wd, dt, inter, hidden), dev(x), h=h).cpu().numpy()
+    h = h.cpu().numpy()
+    g, u, h_ref, y_ref = oracle.ffn_swiglu_f64(gt, wg, gt, wu, dt, wd, x, hidden, inter)
+    hb = _h_bound(g, u, oracle.row_norms(gt, wg, hidden, inter),
+                  oracle.row_norms(gt, wu, hidden, inter), x)
+    assert_within(h, h_ref, hb, "h = silu(g)*u")
+    nd = oracle.row_norms(dt, wd, inter, hidden)
+    dh = np.linalg.norm(h.astype(np.float64) - h_ref)
+    assert_within(y, y_ref, 1e-4 * nd * np.linalg.norm(h_ref) + nd * dh, "ffn y")
+
+
+def test_ffn_host_entry_point():
+    from inferno_hip import _lib
+    import ctypes as C
+    hidden, inter = 1024, 2816
+    wg, wu, wd, x = _ffn_case(hidden, inter, seed=11)
+    y = np.zeros(hidden, np.float32)
+    h = np.zeros(inter, np.float32)
+    say("ihip_ffn_swiglu host")
+    _lib.check(_lib.lib().ihip_ffn_swiglu(synth.Q4_K, wg.ctypes.data, synth.Q4_K, wu.ctypes.data,
+                                          synth.Q6_K, wd.ctypes.data, x.ctypes.data, h.ctypes.data,
+                                          y.ctypes.data, hidden, inter))
+    g, u, h_ref, y_ref = oracle.ffn_swiglu_f64(synth.Q4_K, wg, synth.Q4_K, wu, synth.Q6_K, wd, x,
+                                               hidden, inter)
+    nd = oracle.row_norms(synth.Q6_K, wd, inter, hidden)
+    dh = np.linalg.norm(h.astype(np.float64) - h_ref)
+    assert_within(y, y_ref, 1e-4 * nd * np.linalg.norm(h_ref) + nd * dh, "host ffn y")
+
+
+def test_fused_elementwise_kernels():
+    from inferno_hip import FusedKernels as FK
+    rng = np.random.default_rng(3)
+    g = (rng.standard_normal(10007) * 4).astype(np.float32)
+    u = rng.standard_normal(10007).astype(np.float32)
+    say("fused_mlp_gate_mul_ / fused_silu_gate_mul_")
+    gd = dev(g)
+    FK.fused_mlp_gate_mul_(gd, dev(u))
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.allclose(gd.cpu().numpy(), ref, rtol=2e-6, atol=1e-7)
+    out = torch.empty(10007, device="cuda")
+    FK.fused_silu_gate_mul_(out, dev(g), dev(u))
+    assert np.allclose(out.cpu().numpy(), ref, rtol=2e-6, atol=1e-7)
+
+
+# ------------------------------------------------------ lm_head + argmax ----
+
+@pytest.mark.parametrize("t,vocab,hidden,seed", [
+    (synth.Q6_K, 151936, 2048, 0xC2),   # the lm_head workload, full size
+    (synth.Q6_K, 151936, 2048, 0xC2 + 1),
+    (synth.Q6_K, 1000, 2048, 5),
+    (synth.Q8_0, 32000, 2048, 6),
+    (synth.Q4_K, 5003, 1024, 7),       # GEMV + standalone argmax path
+])
+def test_lm_head_argmax(t, vocab, hidden, seed):
+    say(f"lm_head type={t} vocab={vocab} hidden={hidden} seed={seed}")
+    rng = synth.rng_for(seed)
+    w = synth.weight(rng, t, vocab, hidden)
+    x = synth.activations(rng, hidden)
+    from inferno_hip import device as D
+    ws = D.ArgmaxWorkspace()
+    logits = torch.empty(vocab, device="cuda")
+    dw = dweight(w, t, hidden, vocab)
+    D.lm_head_argmax(dw, dev(x), ws, logits=logits)
+    tok = ws.result()
+    ref = oracle.gemv_f64(t, w, x, hidden, vocab)
+    tol = oracle.tolerance(oracle.row_norms(t, w, hidden, vocab), x)
+    assert_within(logits.cpu().numpy(), ref, tol, "logits")
+    best = int(np.argmax(ref))
+    gap = ref[best] - np.max(np.delete(ref, best))
+    say(f"top-2 gap {gap:.4g} vs bound {2 * tol.max():.4g}")
+    assert gap > 2 * tol.max(), "seed gives an ambiguous maximum"
+    assert tok == best
+    # without logits, twice in a row (the workspace must come back zeroed)
+    for _ in range(2):
+        D.lm_head_argmax(dw, dev(x), ws, logits=None)
+        assert ws.result() == best
+
+
+def test_lm_head_host_entry_point_and_nonfinite():
+    from inferno_hip import _lib
+    import ctypes as C
+    rng = synth.rng_for(99)
+    vocab, hidden = 4096, 2048
+    w = synth.weight(rng, synth.Q6_K, vocab, hidden)
+    x = synth.activations(rng, hidden)
+    tok = C.c_int32(-1)
+    logits = np.zeros(vocab, np.float32)
+    say("ihip_lm_head_argmax host")
+    _lib.check(_lib.lib().ihip_lm_head_argmax(synth.Q6_K, w.ctypes.data, x.ctypes.data,
+                                              logits.ctypes.data, C.byref(tok), hidden, vocab))
+    ref = oracle.gemv_f64(synth.Q6_K, w, x, hidden, vocab)
+    assert tok.value == int(np.argmax(ref))
+    # a NaN scale in one block makes that logit NaN: an error, like CommonOps.jl:149-150
+    w2 = w.copy()
+    w2[208:210] = np.array([0x7E00], np.uint16).view(np.uint8)
+    say("ihip_lm_head_argmax with a NaN logit")
+    rc = _lib.lib().ihip_lm_head_argmax(synth.Q6_K, w2.ctypes.data, x.ctypes.data, None,
+                                        C.byref(tok), hidden, vocab)
+    assert rc == _lib.IHIP_ERR_NONFINITE
+    assert b"NaN" in _lib.lib().ihip_last_error()
+    # +Inf scale -> +Inf or NaN logit: still an error
+    w3 = w.copy()
+    w3[208:210] = np.array([0x7C00], np.uint16).view(np.uint8)
+    rc = _lib.lib().ihip_lm_head_argmax(synth.Q6_K, w3.ctypes.data, x.ctypes.data, None,
+                                        C.byref(tok), hidden, vocab)
+    assert rc == _lib.IHIP_ERR_NONFINITE
+
+
+ARGMAX_CASES = {
+    # tests/unit/test_common_ops.jl:85-93 and :61-62 (0-based here)
+    "all -inf": (np.array([-np.inf, -np.inf], np.float32), 0),
+    "greedy 0..5": (np.arange(6, dtype=np.float32), 5),
+    "skip -inf": (np.array([-np.inf, 0, -np.inf, 1], np.float32), 3),
+    "tie lowest index": (np.array([3, 7, 7, 1], np.float32), 1),
+    "signed zeros tie": (np.array([-0.0, 0.0, -1.0], np.float32), 0),
+    "single": (np.array([-3.5], np.float32), 0),
+}
+
+
+@pytest.mark.parametrize("name", sorted(ARGMAX_CASES))
+def test_argmax_reference_cases(name):
+    from inferno_hip import FusedKernels as FK
+    v, want = ARGMAX_CASES[name]
+    say(f"argmax {name}")
+    assert FK.gpu_argmax(dev(v)) == want
+    assert oracle.argmax(v)[0] == want
+
+
+def test_argmax_errors_and_large_ties():
+    from inferno_hip import FusedKernels as FK, _lib
+    for bad in ([1, np.inf], [1, np.nan], [np.nan, np.nan]):
+        say(f"argmax error case {bad}")
+        with pytest.raises(_lib.IHIPArgumentError):
+            FK.gpu_argmax(dev(np.array(bad, np.float32)))
+    with pytest.raises(_lib.IHIPArgumentError):
+        FK.gpu_argmax(torch.empty(0, device="cuda"))
+    rng = np.random.default_rng(8)
+    for n in (151936, 1 << 20, 257, 65):
+        v = rng.integers(-1000, 1000, size=n).astype(np.float32)
+        v[rng.integers(0, n, size=5)] = 5000.0  # several equal maxima
+        say(f"argmax ties n={n}")
+        assert FK.gpu_argmax(dev(v)) == int(np.argmax(v))
+
+
+# ------------------------------------------------------------- prefill ----
+
+@pytest.mark.parametrize("T,outer,inner,check_rows", [
+    (512, 4096, 4096, 24),   # the batched prefill workload, sampled tokens
+    (70, 300, 2048, None),   # ragged tiles, every token checked
+    (1, 128, 256, None),
+])
+def test_prefill_q4k(T, outer, inner, check_rows):
+    say(f"prefill T={T} {outer}x{inner}")
+    rng = synth.rng_for(0xC4 + T)
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    X = rng.standard_normal((T, inner)).astype(np.float32)
+    from inferno_hip import device as D
+    Y = D.prefill_q4_k(dweight(w, synth.Q4_K, inner, outer), dev(X)).cpu().numpy()
+    Xh = X.astype(np.float16).astype(np.float32)  # the matrix-core operand rounding
+    nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+    rows = range(T) if check_rows is None else sorted(set(
+        [0, T - 1] + list(rng.integers(0, T, size=check_rows))))
+    worst = 0.0
+    for t in rows:
+        ref = oracle.gemv_f64(synth.Q4_K, w, Xh[t], inner, outer)
+        tol = oracle.tolerance(nrm, Xh[t])
+        err = np.abs(Y[t].astype(np.float64) - ref)
+        worst = max(worst, float(np.max(err / tol)))
+        assert np.all(err <= tol), f"token {t}"
+        # and against the fp32-x oracle (fp16 rounding of x included)
+        ref32 = oracle.gemv_f64(synth.Q4_K, w, X[t], inner, outer)
+        assert np.all(np.abs(Y[t] - ref32) <= oracle.tolerance(nrm, X[t]))
+    say(f"prefill max err/tol = {worst:.3e}")
