@@ -77,8 +77,9 @@ int ihip_available(void);
 int ihip_init(int device);
 /* Free every cached weight and buffer. */
 int ihip_shutdown(void);
-/* Performance knobs (no effect on results): "rows_direct" (rows per wave of
- * the Q4_K/Q5_K GEMV: 1, 2, 4, 8), "rows_staged" (Q6_K/Q8_0 GEMV: 1, 2, 4). */
+/* Performance knobs (no effect on results beyond fp32 summation order):
+ * "rows_wide" (rows per wave of the Q4_K/Q5_K GEMV: 1, 2, 4), "rows_gateup"
+ * (the fused gate/up GEMV: 1, 2, 4), "rows_staged" (Q6_K/Q8_0 GEMV: 1, 2). */
 int ihip_set_tuning(const char *name, int value);
 
 /* ---- weight registry (host entry points use it implicitly) ------------ */
@@ -138,8 +139,9 @@ int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *
                         int down_type, const void *wd, const float *x, float *h, float *y,
                         int hidden, int inter, ihip_stream stream);
 /* Workspace for the argmax entry points: IHIP_ARGMAX_WS_BYTES of device
- * memory, zeroed once before first use; every call leaves it zeroed. */
-#define IHIP_ARGMAX_WS_BYTES 256
+ * memory (per-workgroup partial maxima; no initialisation needed).  Calls
+ * that share a workspace must not overlap on the GPU. */
+#define IHIP_ARGMAX_WS_BYTES 65536
 /* GEMV + fused greedy argmax.  logits may be NULL.  *token and *flags are
  * device int32s (flags: IHIP_FLAG_* bits; the token is meaningless when
  * NAN or POSINF is set). */

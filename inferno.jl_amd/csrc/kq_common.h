@@ -39,17 +39,16 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
 // and s2 (8-11): src/Dequant.jl:345-362.
 //   i < 4:  sc = s[i] & 63,                        m = s[i+4] & 63
 //   i >= 4: sc = (s[i+4] & 15) | (s[i-4] >> 6) << 4, m = (s[i+4] >> 4) | (s[i] >> 6) << 4
+// Branch-free: `i` may differ between lanes.
 __device__ __forceinline__ void k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int i,
                                             uint32_t &sc, uint32_t &m)
 {
-    if (i < 4) {
-        sc = (s0 >> (8 * i)) & 63u;
-        m = (s1 >> (8 * i)) & 63u;
-    } else {
-        const int k = 8 * (i - 4);
-        sc = ((s2 >> k) & 15u) | (((s0 >> (k + 6)) & 3u) << 4);
-        m = ((s2 >> (k + 4)) & 15u) | (((s1 >> (k + 6)) & 3u) << 4);
-    }
+    const uint32_t k = 8u * (uint32_t)(i & 3);
+    const uint32_t sc_lo = __builtin_amdgcn_ubfe(s0, k, 6), m_lo = __builtin_amdgcn_ubfe(s1, k, 6);
+    const uint32_t sc_hi = __builtin_amdgcn_ubfe(s2, k, 4) | (__builtin_amdgcn_ubfe(s0, k + 6, 2) << 4);
+    const uint32_t m_hi = __builtin_amdgcn_ubfe(s2, k + 4, 4) | (__builtin_amdgcn_ubfe(s1, k + 6, 2) << 4);
+    sc = i < 4 ? sc_lo : sc_hi;
+    m = i < 4 ? m_lo : m_hi;
 }
 
 // Sum over the 64 lanes of a wavefront; every lane gets the total.
@@ -79,6 +78,15 @@ __device__ __forceinline__ void lds_read8_even(const uint8_t *lds, uint32_t off,
 __device__ __forceinline__ uint32_t lds_read_u16(const uint8_t *lds, uint32_t off)
 {
     return *reinterpret_cast<const uint16_t *>(lds + off);
+}
+
+// Hide a value from the optimizer (no instruction is emitted).  Used on
+// nibble-masked dwords so that the byte converts stay v_cvt_f32_ubyte{0..3}
+// instead of being refolded into a bit-field extract plus convert.
+__device__ __forceinline__ uint32_t opaque(uint32_t v)
+{
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
 // Signed byte k (0..3) of a dword, as float.

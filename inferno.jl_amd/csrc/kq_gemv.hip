@@ -7,164 +7,256 @@
 // src/kernels/quant_kernels.c:166-194, is not used: it breaks the
 // 1e-4*||w_row||*||x|| bound).
 //
-// Work decomposition (wave64):
-//   * the K axis is cut into 2048-column segments; within a segment each of
-//     the 64 lanes owns 32 columns for the whole kernel, keeps those 32 x
-//     values in registers and reuses them across the R rows its wave owns;
-//   * per row, a lane reduces its 32 weights against its 32 x values; a
-//     wave-wide butterfly gives the row total.
-//   * Q4_K / Q5_K blocks are 16-byte multiples, so lanes load their bytes
-//     straight from HBM with 128-bit loads ("direct" kernels): 8 lanes per
-//     block, one 16-byte qs chunk (32 weights) each, plus the block header.
-//   * Q6_K (210 B) and Q8_0 (34 B) blocks are not 16-byte aligned; the
-//     workgroup streams its rows' bytes into LDS with coalesced 128-bit
-//     loads and lanes re-slice blocks from LDS ("staged" kernels).
-// Per-sub-block sums of x (shared by all rows) absorb the `dmin*m` term of
-// Q4_K/Q5_K and the -32 offset of Q6_K, so the inner loop is one convert and
-// one FMA per weight.
+// A decode GEMV is a single pass over the weight bytes, so every kernel here
+// is built to put all of a wave's weight loads in flight before it waits on
+// any of them, to reuse each lane's x registers over several rows, and to
+// keep the per-weight ALU work at one byte convert plus one FMA (the
+// `dmin*m` term of Q4_K/Q5_K and the -32 offset of Q6_K are folded into
+// per-sub-block sums of x, which all rows share).
+//
+//   * Q4_K / Q5_K ("wide" kernels): blocks are 16-byte multiples, so lanes
+//     load straight from HBM with 128-bit loads.  A wave covers 16 blocks
+//     (4096 columns) of R rows per pass: lane = (block, sub-block pair), 64
+//     weights per lane per row.
+//   * Q6_K (210 B) and Q8_0 (34 B) blocks are not 16-byte aligned, but 8 of
+//     them are (1680 B / 272 B).  Each wave copies its own rows into a
+//     private LDS region with gfx950's direct-to-LDS 128-bit loads (no
+//     registers, no workgroup barrier), every segment of the row in flight
+//     at once, then re-slices blocks from LDS ("staged" kernels).
+//   * Greedy argmax (lm_head) is fused into the staged kernel's epilogue:
+//     each workgroup writes one (value, index) partial to its own slot and a
+//     one-workgroup kernel reduces the partials, so no two workgroups touch
+//     the same address.
 #include "kq_common.h"
 #include "kq_launch.h"
 
 namespace ihip {
 
 // ------------------------------------------------------------------------
-// Q4_K / Q5_K direct kernels
+// Q4_K / Q5_K wide kernels
 // ------------------------------------------------------------------------
 template <int FMT>
-struct KDirect;
+struct KFmt;
 template <>
-struct KDirect<kQ4_K> {
+struct KFmt<kQ4_K> {
     static constexpr int BYTES = 144, QS = 16;
 };
 template <>
-struct KDirect<kQ5_K> {
-    static constexpr int BYTES = 176, QS = 48, QH = 16;
+struct KFmt<kQ5_K> {
+    static constexpr int BYTES = 176, QS = 48;
 };
 
-// Lane geometry inside a 2048-column segment: block bs = lane>>3 (8 blocks),
-// qs chunk k = lane&7 covering qs[16k, 16k+16) = sub-block pair j = k>>1,
-// positions l0..l0+15 (l0 = 16*(k&1)); low nibbles are elements 64j+l0+i
-// (sub-block 2j), high nibbles 64j+32+l0+i (sub-block 2j+1).
-struct KLane {
-    int bs, k, j, l0;
-    __device__ KLane(int lane) : bs(lane >> 3), k(lane & 7), j((lane & 7) >> 1), l0(16 * (lane & 1)) {}
-};
-
-struct XSlice {
-    float a[16], b[16];
+// Lane geometry inside a 16-block (4096-column) pass: block b = lane >> 2,
+// sub-block pair j = lane & 3.  The lane's weights are qs[32j, 32j+32) of
+// block b: low nibbles are elements 64j + l (sub-block 2j), high nibbles
+// 64j + 32 + l (sub-block 2j+1), l = 0..31 (src/Dequant.jl:364-371).
+//
+// Both operands are staged in LDS so that every global load is a fully
+// contiguous 1 KB wave access: the rows' bytes with direct-to-LDS loads, x
+// with plain loads into a padded layout (4 floats of padding after every 64)
+// under which a lane's 16-byte x reads hit distinct banks across the wave.
+struct XWide {
+    float a[32], b[32];
     float sa, sb;
 };
 
-__device__ __forceinline__ void load_x_slice(const float *__restrict__ xblk, const KLane &L,
-                                             bool active, XSlice &X)
+constexpr int kXPadFloats = 4096 + 4096 / 64 * 4;
+__device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
+
+__device__ __forceinline__ void x_from_lds(const float *xs, int b, int j, XWide &X)
 {
-    if (active) {
-        const float4 *pa = reinterpret_cast<const float4 *>(xblk + 64 * L.j + L.l0);
-        const float4 *pb = reinterpret_cast<const float4 *>(xblk + 64 * L.j + 32 + L.l0);
+    const int base = 256 * b + 64 * j;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float4 va = pa[t], vb = pb[t];
-            X.a[4 * t + 0] = va.x; X.a[4 * t + 1] = va.y; X.a[4 * t + 2] = va.z; X.a[4 * t + 3] = va.w;
-            X.b[4 * t + 0] = vb.x; X.b[4 * t + 1] = vb.y; X.b[4 * t + 2] = vb.z; X.b[4 * t + 3] = vb.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) X.a[i] = X.b[i] = 0.0f;
+    for (int t = 0; t < 8; ++t) {
+        const float4 va = *reinterpret_cast<const float4 *>(xs + xpad(base + 4 * t));
+        const float4 vb = *reinterpret_cast<const float4 *>(xs + xpad(base + 32 + 4 * t));
+        X.a[4 * t + 0] = va.x; X.a[4 * t + 1] = va.y; X.a[4 * t + 2] = va.z; X.a[4 * t + 3] = va.w;
+        X.b[4 * t + 0] = vb.x; X.b[4 * t + 1] = vb.y; X.b[4 * t + 2] = vb.z; X.b[4 * t + 3] = vb.w;
     }
-    float sa = 0.0f, sb = 0.0f;
+    float sa0 = 0.0f, sa1 = 0.0f, sb0 = 0.0f, sb1 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { sa += X.a[i]; sb += X.b[i]; }
-    X.sa = sa;
-    X.sb = sb;
+    for (int i = 0; i < 32; i += 2) {
+        sa0 += X.a[i]; sa1 += X.a[i + 1];
+        sb0 += X.b[i]; sb1 += X.b[i + 1];
+    }
+    X.sa = sa0 + sa1;
+    X.sb = sb0 + sb1;
 }
 
-// One lane's contribution for one row: header h, qs chunk q, (Q5_K) qh chunk.
+// The block bytes one lane needs for one row: header (d, dmin, scales), its
+// 32 qs bytes and (Q5_K) the 32 qh bytes.
+struct KBytes {
+    uint4 h, q0, q1, e0, e1;
+};
+
 template <int FMT>
-__device__ __forceinline__ float kdot(const uint4 &h, const uint4 &q, const uint4 &qh,
-                                      const KLane &L, const XSlice &X)
+__device__ __forceinline__ void kbytes_from_lds(const uint8_t *blk, int j, KBytes &B)
 {
-    float sa = 0.0f, sb = 0.0f;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        uint32_t lo = qw[t] & 0x0f0f0f0fu;
-        uint32_t hi = (qw[t] >> 4) & 0x0f0f0f0fu;
-        if (FMT == kQ5_K) {
-            lo |= ((hw[t] >> (2 * L.j)) & 0x01010101u) << 4;
-            hi |= ((hw[t] >> (2 * L.j + 1)) & 0x01010101u) << 4;
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            sa = fmaf(ubyte_f(lo, b), X.a[4 * t + b], sa);
-            sb = fmaf(ubyte_f(hi, b), X.b[4 * t + b], sb);
-        }
+    using F = KFmt<FMT>;
+    B.h = *reinterpret_cast<const uint4 *>(blk);
+    B.q0 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j);
+    B.q1 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j + 16);
+    if constexpr (FMT == kQ5_K) {
+        B.e0 = *reinterpret_cast<const uint4 *>(blk + 16);
+        B.e1 = *reinterpret_cast<const uint4 *>(blk + 32);
     }
-    const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// One lane's contribution to one row.
+//
+// Q4_K converts nibbles with v_cvt_pk_f32_fp8, two per instruction: a byte
+// 0000qqqq is the OCP e4m3 encoding of q * 2^-9 exactly (q3 becomes the
+// exponent's low bit, q2..q0 the mantissa; 0..7 are e4m3 subnormals, which
+// gfx950 converts exactly), so the sums are formed in units of 2^-9 and the
+// exact power-of-two factor 512 is applied once per sub-block.  Q5_K's 5-bit
+// values are not linear in e4m3 and use v_cvt_f32_ubyte.
+template <int FMT>
+__device__ __forceinline__ float kwide_dot(const KBytes &B, int j, const XWide &X)
+{
+    const uint32_t qw[8] = {B.q0.x, B.q0.y, B.q0.z, B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w};
+    float sa0 = 0.0f, sa1 = 0.0f, sb0 = 0.0f, sb1 = 0.0f;
+    if constexpr (FMT == kQ4_K) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t lo = qw[t] & 0x0f0f0f0fu;
+            const uint32_t hi = (qw[t] >> 4) & 0x0f0f0f0fu;
+            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+            const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+            const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+            sa0 = fmaf(l01[0], X.a[4 * t + 0], sa0);
+            sa1 = fmaf(l01[1], X.a[4 * t + 1], sa1);
+            sa0 = fmaf(l23[0], X.a[4 * t + 2], sa0);
+            sa1 = fmaf(l23[1], X.a[4 * t + 3], sa1);
+            sb0 = fmaf(h01[0], X.b[4 * t + 0], sb0);
+            sb1 = fmaf(h01[1], X.b[4 * t + 1], sb1);
+            sb0 = fmaf(h23[0], X.b[4 * t + 2], sb0);
+            sb1 = fmaf(h23[1], X.b[4 * t + 3], sb1);
+        }
+        sa0 = (sa0 + sa1) * 512.0f;
+        sb0 = (sb0 + sb1) * 512.0f;
+    } else {
+        // qh[l] bit 2j lifts element 64j + l, bit 2j+1 element 64j + 32 + l;
+        // shift both bits down to bit positions 0 and 1 of each byte once
+        const uint32_t sh = 2 * j;
+        const uint32_t ew[8] = {B.e0.x >> sh, B.e0.y >> sh, B.e0.z >> sh, B.e0.w >> sh,
+                                B.e1.x >> sh, B.e1.y >> sh, B.e1.z >> sh, B.e1.w >> sh};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t lo = (qw[t] & 0x0f0f0f0fu) | ((ew[t] & 0x01010101u) << 4);
+            uint32_t hi = ((qw[t] >> 4) & 0x0f0f0f0fu) | ((ew[t] & 0x02020202u) << 3);
+            lo = opaque(lo);
+            hi = opaque(hi);
+            sa0 = fmaf(ubyte_f(lo, 0), X.a[4 * t + 0], sa0);
+            sa1 = fmaf(ubyte_f(lo, 1), X.a[4 * t + 1], sa1);
+            sa0 = fmaf(ubyte_f(lo, 2), X.a[4 * t + 2], sa0);
+            sa1 = fmaf(ubyte_f(lo, 3), X.a[4 * t + 3], sa1);
+            sb0 = fmaf(ubyte_f(hi, 0), X.b[4 * t + 0], sb0);
+            sb1 = fmaf(ubyte_f(hi, 1), X.b[4 * t + 1], sb1);
+            sb0 = fmaf(ubyte_f(hi, 2), X.b[4 * t + 2], sb0);
+            sb1 = fmaf(ubyte_f(hi, 3), X.b[4 * t + 3], sb1);
+        }
+        sa0 += sa1;
+        sb0 += sb1;
+    }
+    const float d = h2f(B.h.x & 0xffffu), dmin = h2f(B.h.x >> 16);
     uint32_t scA, mA, scB, mB;
-    k_scale_min(h.y, h.z, h.w, 2 * L.j, scA, mA);
-    k_scale_min(h.y, h.z, h.w, 2 * L.j + 1, scB, mB);
-    float r = (d * (float)scA) * sa;
-    r = fmaf(d * (float)scB, sb, r);
+    k_scale_min(B.h.y, B.h.z, B.h.w, 2 * j, scA, mA);
+    k_scale_min(B.h.y, B.h.z, B.h.w, 2 * j + 1, scB, mB);
+    float r = (d * (float)scA) * sa0;
+    r = fmaf(d * (float)scB, sb0, r);
     r = fmaf(-(dmin * (float)mA), X.sa, r);
     r = fmaf(-(dmin * (float)mB), X.sb, r);
     return r;
 }
 
 // Plain GEMV (GATEUP == false) or fused gate/up + SwiGLU (GATEUP == true:
-// W2 is the up weight, y[r] = silu(g[r]) * u[r]).
+// W2 is the up weight, y[r] = silu(g[r]) * u[r]).  Wave w of workgroup g
+// owns rows [(4g + w) R, (4g + w + 1) R).  Per 4096-column pass: each wave
+// copies its rows' bytes into its LDS region, the workgroup stages x, one
+// barrier, then every wave reduces its rows from LDS.
 template <int FMT, int R, bool GATEUP>
-__global__ __launch_bounds__(256) void k_gemv_kdirect(const uint8_t *__restrict__ W,
-                                                      const uint8_t *__restrict__ W2,
-                                                      const float *__restrict__ x,
-                                                      float *__restrict__ y, int outer, int nblk)
+__global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ W,
+                                                    const uint8_t *__restrict__ W2,
+                                                    const float *__restrict__ x,
+                                                    float *__restrict__ y, int outer, int nblk)
 {
-    using F = KDirect<FMT>;
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (row0 >= outer)
-        return; // wave-uniform
-    const KLane L(lane);
-    const size_t row_bytes = (size_t)nblk * F::BYTES;
+    using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
+    constexpr int PASS_BYTES = 16 * F::BYTES; // one row's bytes of a 16-block pass
+    constexpr int WAVE_BYTES = NW * R * PASS_BYTES;
+    __shared__ __attribute__((aligned(16))) float xs[kXPadFloats];
+    __shared__ __attribute__((aligned(16))) uint8_t wb[4 * WAVE_BYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const bool live = row0 < outer; // wave-uniform; dead waves still join the barriers
+    const int b = lane >> 2, j = lane & 3;
+    const int inner = nblk * 256;
+    const size_t row_bytes = (size_t)nblk * F::BYTES;
+    uint8_t *mine = wb + wave * WAVE_BYTES;
+
     float acc[NW][R];
 #pragma unroll
     for (int m = 0; m < NW; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
-    const int nseg = (nblk + 7) >> 3;
-    for (int seg = 0; seg < nseg; ++seg) {
-        const int blk = seg * 8 + L.bs;
-        const bool active = blk < nblk;
-        uint4 hh[NW][R], qq[NW][R], qh[NW][R];
+    const int npass = (nblk + 15) >> 4;
+    for (int pass = 0; pass < npass; ++pass) {
+        const int nb = min(16, nblk - pass * 16);
+        if (live) {
+            const int chunks = nb * (F::BYTES / 16);
 #pragma unroll
-        for (int m = 0; m < NW; ++m) {
-            const uint8_t *Wm = m == 0 ? W : W2;
+            for (int m = 0; m < NW; ++m) {
+                const uint8_t *Wm = m == 0 ? W : W2;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = row0 + r;
-                if (active && row < outer) {
-                    const uint8_t *bp = Wm + (size_t)row * row_bytes + (size_t)blk * F::BYTES;
-                    hh[m][r] = *reinterpret_cast<const uint4 *>(bp);
-                    qq[m][r] = *reinterpret_cast<const uint4 *>(bp + F::QS + 16 * L.k);
-                    if constexpr (FMT == kQ5_K)
-                        qh[m][r] = *reinterpret_cast<const uint4 *>(bp + 16 + L.l0);
-                    else
-                        qh[m][r] = make_uint4(0, 0, 0, 0);
-                } else {
-                    hh[m][r] = qq[m][r] = qh[m][r] = make_uint4(0, 0, 0, 0);
+                for (int r = 0; r < R; ++r) {
+                    const int row = min(row0 + r, outer - 1); // rows past the end re-read the last
+                    const uint8_t *src = Wm + (size_t)row * row_bytes + (size_t)pass * PASS_BYTES;
+                    uint8_t *dst = mine + (m * R + r) * PASS_BYTES;
+                    for (int c0 = 0; c0 < chunks; c0 += 64) {
+                        const int c = c0 + lane;
+                        if (c < chunks)
+                            __builtin_amdgcn_global_load_lds(
+                                (const void *)(src + 16 * (size_t)c),
+                                (__attribute__((address_space(3))) void *)(dst + 16 * c0), 16, 0, 0);
+                    }
                 }
             }
         }
-        XSlice X;
-        load_x_slice(x + (size_t)blk * 256, L, active, X);
 #pragma unroll
-        for (int m = 0; m < NW; ++m)
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * (tid + 256 * k); // float index inside the pass
+            const int col = pass * 4096 + i;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (col < inner)
+                v = *reinterpret_cast<const float4 *>(x + col);
+            *reinterpret_cast<float4 *>(xs + xpad(i)) = v;
+        }
+        __builtin_amdgcn_s_waitcnt(0); // this wave's LDS copies have landed
+        __syncthreads();
+        if (live) {
+            XWide X;
+            x_from_lds(xs, b, j, X);
+            const bool active = b < nb;
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                acc[m][r] += kdot<FMT>(hh[m][r], qq[m][r], qh[m][r], L, X);
+            for (int m = 0; m < NW; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    KBytes B;
+                    kbytes_from_lds<FMT>(mine + (m * R + r) * PASS_BYTES + b * F::BYTES, j, B);
+                    const float c = kwide_dot<FMT>(B, j, X);
+                    acc[m][r] += active ? c : 0.0f;
+                }
+        }
+        if (pass + 1 < npass)
+            __syncthreads(); // the next pass overwrites xs and wb
     }
+    if (!live)
+        return;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float g = wave_sum(acc[0][r]);
@@ -181,56 +273,84 @@ __global__ __launch_bounds__(256) void k_gemv_kdirect(const uint8_t *__restrict_
 }
 
 // ------------------------------------------------------------------------
-// Staged kernels (Q6_K, Q8_0): WG = 4 waves x R rows; each 2048-column
-// segment of the WG's rows is copied to LDS with 128-bit loads first.
+// Staged kernels (Q6_K, Q8_0)
 // ------------------------------------------------------------------------
+// A segment is 8 Q6_K blocks (2048 columns, 1680 B) or 64 Q8_0 blocks (2048
+// columns, 2176 B); rows of a whole number of 8-block groups are 16-byte
+// aligned, which the host checks before choosing these kernels.
 template <int FMT>
-struct KStaged;
+struct SFmt;
 template <>
-struct KStaged<kQ6_K> {
-    static constexpr int SEG_BLOCKS = 8, SEG_BYTES = 8 * 210, CHUNKS = SEG_BYTES / 16;
+struct SFmt<kQ6_K> {
+    static constexpr int SEG_BLOCKS = 8, SEG_BYTES = 8 * 210;
 };
 template <>
-struct KStaged<kQ8_0> {
-    static constexpr int SEG_BLOCKS = 64, SEG_BYTES = 64 * 34, CHUNKS = SEG_BYTES / 16;
+struct SFmt<kQ8_0> {
+    static constexpr int SEG_BLOCKS = 64, SEG_BYTES = 64 * 34;
 };
-static_assert(KStaged<kQ6_K>::SEG_BYTES % 16 == 0, "Q6_K segment must be 16-byte aligned");
-static_assert(KStaged<kQ8_0>::SEG_BYTES % 16 == 0, "Q8_0 segment must be 16-byte aligned");
+static_assert(SFmt<kQ6_K>::SEG_BYTES % 16 == 0, "Q6_K segment must be 16-byte aligned");
+static_assert(SFmt<kQ8_0>::SEG_BYTES % 16 == 0, "Q8_0 segment must be 16-byte aligned");
 
 // Q6_K lane geometry: block bs = lane>>3; unit u = lane&7: half n = u>>2,
 // positions l0 = 8*(u&3) .. +7.  Group g (0..3) of the unit holds the
 // elements 128n + 32g + l0 + i (src/Dequant.jl:584-597): g=0 low nibble of
 // ql[64n+l0+i], g=1 low nibble of ql[64n+32+l0+i], g=2/3 the high nibbles,
 // with qh[32n+l0+i] bits 2g..2g+1 on top and scale sc[8n + 2g + (l0>>4)].
-struct Q6Slice {
+// Q8_0 lane geometry: lane = block of the 64-block segment, 32 weights.
+template <int FMT>
+struct SX;
+template <>
+struct SX<kQ6_K> {
     float x[4][8];
     float s[4];
 };
+template <>
+struct SX<kQ8_0> {
+    float x[32];
+};
 
-__device__ __forceinline__ void q6_load_x(const float *__restrict__ xblk, int n, int l0,
-                                          bool active, Q6Slice &X)
+template <int FMT>
+__device__ __forceinline__ void staged_load_x(const float *__restrict__ xseg, int lane,
+                                              int seg_blocks, SX<FMT> &X)
 {
+    if constexpr (FMT == kQ6_K) {
+        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+        const bool active = bs < seg_blocks;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        if (active) {
-            const float4 *p = reinterpret_cast<const float4 *>(xblk + 128 * n + 32 * g + l0);
-            const float4 v0 = p[0], v1 = p[1];
-            X.x[g][0] = v0.x; X.x[g][1] = v0.y; X.x[g][2] = v0.z; X.x[g][3] = v0.w;
-            X.x[g][4] = v1.x; X.x[g][5] = v1.y; X.x[g][6] = v1.z; X.x[g][7] = v1.w;
+        for (int g = 0; g < 4; ++g) {
+            if (active) {
+                const float4 *p =
+                    reinterpret_cast<const float4 *>(xseg + 256 * bs + 128 * n + 32 * g + l0);
+                const float4 v0 = p[0], v1 = p[1];
+                X.x[g][0] = v0.x; X.x[g][1] = v0.y; X.x[g][2] = v0.z; X.x[g][3] = v0.w;
+                X.x[g][4] = v1.x; X.x[g][5] = v1.y; X.x[g][6] = v1.z; X.x[g][7] = v1.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) X.x[g][i] = 0.0f;
+            }
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += X.x[g][i];
+            X.s[g] = sum;
+        }
+    } else {
+        if (lane < seg_blocks) {
+            const float4 *p = reinterpret_cast<const float4 *>(xseg + 32 * lane);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float4 v = p[t];
+                X.x[4 * t] = v.x; X.x[4 * t + 1] = v.y; X.x[4 * t + 2] = v.z; X.x[4 * t + 3] = v.w;
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) X.x[g][i] = 0.0f;
+            for (int i = 0; i < 32; ++i) X.x[i] = 0.0f;
         }
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s += X.x[g][i];
-        X.s[g] = s;
     }
 }
 
 // `tile` is the 16-byte-aligned LDS array, `bo` the block's byte offset in it.
 __device__ __forceinline__ float q6_dot(const uint8_t *tile, uint32_t bo, int n, int l0,
-                                        const Q6Slice &X)
+                                        const SX<kQ6_K> &X)
 {
     uint32_t A[2], B[2], H[2], S[2];
     lds_read8_even(tile, bo + 64 * n + l0, A[0], A[1]);
@@ -259,48 +379,54 @@ __device__ __forceinline__ float q6_dot(const uint8_t *tile, uint32_t bo, int n,
     for (int g = 0; g < 4; ++g) {
         const int si = 2 * g + c; // byte of the 8 scales sc[8n..8n+7]
         const float ds = d * sbyte_f(S[si >> 2], si & 3);
-        r = fmaf(ds, acc[g] - 32.0f * X.s[g], r);
+        r = fmaf(ds, fmaf(-32.0f, X.s[g], acc[g]), r);
     }
     return r;
 }
 
-// Q8_0: lane = block within the 64-block segment, 32 weights.
-__device__ __forceinline__ float q80_dot(const uint8_t *blk_lds, uint32_t off, const float *xr)
+// Q8_0 block at byte `off` of the 16-byte-aligned LDS row `row_lds`.
+__device__ __forceinline__ float q80_dot(const uint8_t *row_lds, uint32_t off, const float *xr)
 {
-    const float d = h2f(lds_read_u16(blk_lds, off));
+    const float d = h2f(lds_read_u16(row_lds, off));
     const uint32_t o = off + 2;
-    const uint32_t *p = reinterpret_cast<const uint32_t *>(blk_lds + (o & ~3u));
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
     const uint32_t sh = o & 3u;
     uint32_t w[9];
 #pragma unroll
     for (int i = 0; i < 9; ++i) w[i] = p[i];
-    float acc = 0.0f;
+    float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-            acc = fmaf(sbyte_f(q, b), xr[4 * t + b], acc);
+        a0 = fmaf(sbyte_f(q, 0), xr[4 * t + 0], a0);
+        a1 = fmaf(sbyte_f(q, 1), xr[4 * t + 1], a1);
+        a0 = fmaf(sbyte_f(q, 2), xr[4 * t + 2], a0);
+        a1 = fmaf(sbyte_f(q, 3), xr[4 * t + 3], a1);
     }
-    return d * acc;
+    return d * (a0 + a1);
 }
 
-struct ArgmaxWS {
-    unsigned long long key; // (ordered value << 32) | (0xffffffff - index)
-    unsigned int count;     // workgroups finished
-    unsigned int flags;     // bit0 NaN, bit1 +Inf, bit2 a value other than -Inf seen
+// ---- greedy argmax partials ----------------------------------------------
+// key = (order-preserving bits of the value << 32) | (0xffffffff - index), so
+// the larger key is the larger value and, among equal values, the lower index
+// (the strict `>` scan of src/CommonOps.jl:155-158).
+struct ArgPart {
+    unsigned long long key;
+    uint32_t flags; // bit0 NaN, bit1 +Inf, bit2 a value other than -Inf seen
+    uint32_t pad;
 };
+static_assert(sizeof(ArgPart) == 16, "ArgPart layout");
+constexpr int kArgMaxParts = 4096;
 
 __device__ __forceinline__ uint32_t ordered_bits(float v)
 {
     if (v == 0.0f)
-        v = 0.0f; // -0 == +0 for the strict `>` scan of src/CommonOps.jl:155-158
+        v = 0.0f; // -0 == +0 for the strict `>` scan
     const uint32_t b = __float_as_uint(v);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Fold value v at index i into a (key, flags) pair: NaN and +Inf raise a
-// flag and never win; ties keep the lower index.
+// Fold value v at index i: NaN and +Inf raise a flag and never win.
 __device__ __forceinline__ void argmax_fold(float v, uint32_t i, unsigned long long &key,
                                             uint32_t &flags)
 {
@@ -319,150 +445,58 @@ __device__ __forceinline__ void argmax_fold(float v, uint32_t i, unsigned long l
     key = k > key ? k : key;
 }
 
-// Workgroup-level result -> global workspace; the last workgroup writes the
-// token and flags and returns the workspace to zero for the next call.
-__device__ void argmax_commit(ArgmaxWS *ws, unsigned long long key, uint32_t flags,
-                              int32_t *token, uint32_t *flags_out)
+__device__ __forceinline__ void argmax_wave_reduce(unsigned long long &key, uint32_t &flags)
 {
-    // called by one thread per workgroup
-    if (flags)
-        atomicOr(&ws->flags, flags);
-    if (key)
-        atomicMax(&ws->key, key);
-    __threadfence();
-    const unsigned int done = atomicAdd(&ws->count, 1u);
-    if (done == gridDim.x - 1) {
-        __threadfence();
-        const unsigned long long k = atomicAdd(&ws->key, 0ull);
-        const uint32_t f = atomicOr(&ws->flags, 0u);
-        *token = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
-        uint32_t out = 0;
-        if (f & 1u) out |= 1u;
-        if (f & 2u) out |= 2u;
-        if (!(f & 4u)) out |= 4u; // every logit was -Inf: index 0 (CommonOps.jl:143-161)
-        if (!(f & 4u)) *token = 0;
-        *flags_out = out;
-        atomicExch(&ws->key, 0ull);
-        atomicExch(&ws->flags, 0u);
-        atomicExch(&ws->count, 0u);
-    }
-}
-
-template <int FMT, int R, bool ARGMAX>
-__global__ __launch_bounds__(256) void k_gemv_staged(const uint8_t *__restrict__ W,
-                                                     const float *__restrict__ x,
-                                                     float *__restrict__ y, int outer, int nblk,
-                                                     ArgmaxWS *ws, int32_t *token,
-                                                     uint32_t *flags_out)
-{
-    using F = KStaged<FMT>;
-    constexpr int ROWS = 4 * R;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[ROWS * F::SEG_BYTES + 16];
-    __shared__ unsigned long long wkey[4];
-    __shared__ uint32_t wflag[4];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wg_row0 = blockIdx.x * ROWS;
-    const size_t row_bytes = (size_t)nblk * block_bytes(FMT);
-    const int nseg = (nblk + F::SEG_BLOCKS - 1) / F::SEG_BLOCKS;
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-    for (int seg = 0; seg < nseg; ++seg) {
-        const int seg_blocks = min(F::SEG_BLOCKS, nblk - seg * F::SEG_BLOCKS);
-        const int seg_chunks = (seg_blocks * block_bytes(FMT) + 15) / 16;
-        // cooperative 128-bit copy of the WG's rows' segment into LDS
-        for (int c = tid; c < ROWS * F::CHUNKS; c += 256) {
-            const int rr = c / F::CHUNKS, cc = c - rr * F::CHUNKS;
-            const int row = wg_row0 + rr;
-            if (row < outer && cc < seg_chunks) {
-                const uint8_t *src = W + (size_t)row * row_bytes +
-                                     (size_t)seg * F::SEG_BYTES + 16 * (size_t)cc;
-                *reinterpret_cast<uint4 *>(tile + rr * F::SEG_BYTES + 16 * cc) =
-                    *reinterpret_cast<const uint4 *>(src);
-            }
-        }
-        __syncthreads();
-        const float *xs = x + (size_t)seg * 2048;
-        if constexpr (FMT == kQ6_K) {
-            const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-            const bool active = bs < seg_blocks;
-            Q6Slice X;
-            q6_load_x(xs + 256 * bs, n, l0, active, X);
-            if (active) {
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    acc[r] += q6_dot(tile, (wave * R + r) * F::SEG_BYTES + 210 * bs, n, l0, X);
-            }
-        } else {
-            const bool active = lane < seg_blocks;
-            float xr[32];
-            if (active) {
-                const float4 *p = reinterpret_cast<const float4 *>(xs + 32 * lane);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const float4 v = p[t];
-                    xr[4 * t] = v.x; xr[4 * t + 1] = v.y; xr[4 * t + 2] = v.z; xr[4 * t + 3] = v.w;
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    acc[r] += q80_dot(tile + (wave * R + r) * F::SEG_BYTES, 34u * lane, xr);
-            }
-        }
-        __syncthreads();
-    }
-
-    unsigned long long key = 0;
-    uint32_t fl = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float v = wave_sum(acc[r]);
-        const int row = wg_row0 + wave * R + r;
-        if (row < outer) {
-            if (y && lane == 0)
-                y[row] = v;
-            if (ARGMAX)
-                argmax_fold(v, (uint32_t)row, key, fl);
-        }
-    }
-    if constexpr (ARGMAX) {
-        if (lane == 0) {
-            wkey[wave] = key;
-            wflag[wave] = fl;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            unsigned long long k = wkey[0];
-            uint32_t f = wflag[0];
-#pragma unroll
-            for (int w = 1; w < 4; ++w) {
-                k = wkey[w] > k ? wkey[w] : k;
-                f |= wflag[w];
-            }
-            argmax_commit(ws, k, f, token, flags_out);
-        }
-    }
-}
-
-// Standalone argmax over a logits vector (gpu_argmax!, FusedKernels.jl:271-311,
-// with the _validate_logits checks of CommonOps.jl:142-163).
-__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ v, int64_t n,
-                                                ArgmaxWS *ws, int32_t *token, uint32_t *flags_out)
-{
-    __shared__ unsigned long long wkey[4];
-    __shared__ uint32_t wflag[4];
-    unsigned long long key = 0;
-    uint32_t fl = 0;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-        argmax_fold(v[i], (uint32_t)i, key, fl);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const unsigned long long ok = __shfl_xor(key, o, 64);
         key = ok > key ? ok : key;
-        fl |= __shfl_xor(fl, o, 64);
+        flags |= __shfl_xor(flags, o, 64);
     }
+}
+
+// Workgroup (4 waves) reduction; thread 0 stores the partial.
+__device__ __forceinline__ void argmax_store_partial(unsigned long long key, uint32_t flags,
+                                                     ArgPart *part)
+{
+    __shared__ unsigned long long wkey[4];
+    __shared__ uint32_t wflag[4];
+    argmax_wave_reduce(key, flags);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        wkey[wave] = key;
+        wflag[wave] = flags;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long k = wkey[0];
+        uint32_t f = wflag[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            k = wkey[w] > k ? wkey[w] : k;
+            f |= wflag[w];
+        }
+        part->key = k;
+        part->flags = f;
+        part->pad = 0;
+    }
+}
+
+// Reduce `nparts` partials; writes the 0-based token and the IHIP_FLAG_* bits.
+__global__ __launch_bounds__(256) void k_argmax_finalize(const ArgPart *__restrict__ parts,
+                                                         int nparts, int32_t *token,
+                                                         uint32_t *flags_out)
+{
+    __shared__ unsigned long long wkey[4];
+    __shared__ uint32_t wflag[4];
+    unsigned long long key = 0;
+    uint32_t fl = 0;
+    for (int i = threadIdx.x; i < nparts; i += 256) {
+        const unsigned long long k = parts[i].key;
+        key = k > key ? k : key;
+        fl |= parts[i].flags;
+    }
+    argmax_wave_reduce(key, fl);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
         wkey[wave] = key;
@@ -476,76 +510,204 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ v, int
             k = wkey[w] > k ? wkey[w] : k;
             f |= wflag[w];
         }
-        argmax_commit(ws, k, f, token, flags_out);
+        uint32_t out = f & 3u;
+        int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+        if (!(f & 4u)) { // every logit was -Inf: index 0 (src/CommonOps.jl:143-161)
+            out |= 4u;
+            tok = 0;
+        }
+        *token = tok;
+        *flags_out = out;
     }
+}
+
+// Standalone argmax over a vector (gpu_argmax!, src/FusedKernels.jl:271-311,
+// with the _validate_logits checks of src/CommonOps.jl:142-163).
+__global__ __launch_bounds__(256) void k_argmax_partials(const float *__restrict__ v, int64_t n,
+                                                         ArgPart *__restrict__ parts)
+{
+    unsigned long long key = 0;
+    uint32_t fl = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        argmax_fold(v[i], (uint32_t)i, key, fl);
+    argmax_store_partial(key, fl, parts + blockIdx.x);
+}
+
+// ---- the staged GEMV ------------------------------------------------------
+// Workgroup = 4 waves; wave w of row group g owns rows [(4g + w) R, +R).
+// Each wave stages up to S segments of its R rows into its own LDS region
+// (R * S * SEG_BYTES bytes) with direct-to-LDS loads, waits, then computes;
+// the x slice of the next segment is loaded while the current one is
+// reduced.  ARGMAX: the workgroup walks row groups grid-stride and stores
+// one argmax partial; `y` may then be null.
+template <int FMT, int R, int S, bool ARGMAX>
+__global__ __launch_bounds__(256) void k_gemv_staged(const uint8_t *__restrict__ W,
+                                                     const float *__restrict__ x,
+                                                     float *__restrict__ y, int outer, int nblk,
+                                                     ArgPart *__restrict__ parts)
+{
+    using F = SFmt<FMT>;
+    constexpr int WAVE_BYTES = R * S * F::SEG_BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[4 * WAVE_BYTES + 16];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t row_bytes = (size_t)nblk * block_bytes(FMT);
+    const int nseg = (nblk + F::SEG_BLOCKS - 1) / F::SEG_BLOCKS;
+    const int nrg = (outer + 4 * R - 1) / (4 * R);
+    uint8_t *wt = tile + wave * WAVE_BYTES; // this wave's LDS region
+    const uint32_t wt_off = (uint32_t)(wave * WAVE_BYTES);
+
+    unsigned long long key = 0;
+    uint32_t fl = 0;
+
+    for (int rg = blockIdx.x; rg < nrg; rg += (ARGMAX ? gridDim.x : nrg)) {
+        const int row0 = (rg * 4 + wave) * R;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+        if (row0 < outer) { // wave-uniform
+            for (int st = 0; st < nseg; st += S) {
+                const int ns = min(S, nseg - st);
+                // bytes of this stage in one row: whole segments except a
+                // short last one, always a multiple of 16 (checked on the host)
+                const int last_blocks = min(F::SEG_BLOCKS, nblk - (st + ns - 1) * F::SEG_BLOCKS);
+                const int stage_bytes = (ns - 1) * F::SEG_BYTES + last_blocks * block_bytes(FMT);
+                const int chunks = stage_bytes >> 4;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int row = min(row0 + r, outer - 1); // rows past the end re-read the last row
+                    const uint8_t *src = W + (size_t)row * row_bytes + (size_t)st * F::SEG_BYTES;
+                    uint8_t *dst = wt + r * S * F::SEG_BYTES;
+                    for (int c0 = 0; c0 < chunks; c0 += 64) {
+                        const int c = c0 + lane;
+                        if (c < chunks)
+                            __builtin_amdgcn_global_load_lds(
+                                (const void *)(src + 16 * (size_t)c),
+                                (__attribute__((address_space(3))) void *)(dst + 16 * c0), 16, 0, 0);
+                    }
+                }
+                SX<FMT> X;
+                staged_load_x<FMT>(x + (size_t)st * 2048, lane,
+                                   min(F::SEG_BLOCKS, nblk - st * F::SEG_BLOCKS), X);
+                __builtin_amdgcn_s_waitcnt(0); // LDS copies (and x) have landed
+                for (int s = 0; s < ns; ++s) {
+                    const int seg = st + s;
+                    const int seg_blocks = min(F::SEG_BLOCKS, nblk - seg * F::SEG_BLOCKS);
+                    SX<FMT> Xn;
+                    if (s + 1 < ns)
+                        staged_load_x<FMT>(x + (size_t)(seg + 1) * 2048, lane,
+                                           min(F::SEG_BLOCKS, nblk - (seg + 1) * F::SEG_BLOCKS), Xn);
+                    if constexpr (FMT == kQ6_K) {
+                        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+                        if (bs < seg_blocks) {
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                acc[r] += q6_dot(tile,
+                                                 wt_off + (uint32_t)((r * S + s) * F::SEG_BYTES + 210 * bs),
+                                                 n, l0, X);
+                        }
+                    } else {
+                        if (lane < seg_blocks) {
+#pragma unroll
+                            for (int r = 0; r < R; ++r)
+                                acc[r] += q80_dot(wt + (r * S + s) * F::SEG_BYTES, 34u * lane, X.x);
+                        }
+                    }
+                    if (s + 1 < ns)
+                        X = Xn;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[r]);
+            const int row = row0 + r;
+            if (row < outer) {
+                if (y && lane == 0)
+                    y[row] = v;
+                if constexpr (ARGMAX)
+                    argmax_fold(v, (uint32_t)row, key, fl);
+            }
+        }
+        if constexpr (!ARGMAX)
+            break;
+    }
+    if constexpr (ARGMAX)
+        argmax_store_partial(key, fl, parts + blockIdx.x);
 }
 
 // ------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------
-static int g_rows_direct = 4; // rows per wave, direct kernels
-static int g_rows_staged = 2; // rows per wave, staged kernels
+static int g_rows_wide = 2;   // rows per wave, Q4_K/Q5_K GEMV
+static int g_rows_gateup = 2; // rows per wave, fused gate/up
+static int g_rows_staged = 2; // rows per wave, Q6_K/Q8_0 GEMV
 
 void set_tuning(const char *name, int value)
 {
-    if (!__builtin_strcmp(name, "rows_direct")) g_rows_direct = value;
+    if (!__builtin_strcmp(name, "rows_wide")) g_rows_wide = value;
+    if (!__builtin_strcmp(name, "rows_gateup")) g_rows_gateup = value;
     if (!__builtin_strcmp(name, "rows_staged")) g_rows_staged = value;
 }
 
 template <int FMT, bool GATEUP>
-static hipError_t launch_kdirect(const void *w, const void *w2, const float *x, float *y,
-                                 int inner, int outer, hipStream_t s)
+static hipError_t launch_kwide(const void *w, const void *w2, const float *x, float *y,
+                               int inner, int outer, hipStream_t s)
 {
     const int nblk = inner / 256;
-    const int R = g_rows_direct;
-#define IHIP_KD(RR)                                                                          \
+    int R = GATEUP ? g_rows_gateup : g_rows_wide;
+    if (FMT == kQ5_K && GATEUP && R > 2)
+        R = 2; // register budget
+#define IHIP_KW(RR)                                                                          \
     case RR:                                                                                 \
-        hipLaunchKernelGGL((k_gemv_kdirect<FMT, RR, GATEUP>),                                \
+        hipLaunchKernelGGL((k_gemv_kwide<FMT, RR, GATEUP>),                                  \
                            dim3((outer + 4 * RR - 1) / (4 * RR)), dim3(256), 0, s,            \
                            (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk);      \
         break;
     switch (R) {
-        IHIP_KD(1)
-        IHIP_KD(2)
-        IHIP_KD(8)
+        IHIP_KW(1)
+        IHIP_KW(4)
     default:
-        IHIP_KD(4)
+        IHIP_KW(2)
     }
-#undef IHIP_KD
+#undef IHIP_KW
     return hipGetLastError();
 }
 
+// Segments staged per LDS fill: enough to cover the row when it is short.
+static int stage_segments(int nseg) { return nseg <= 1 ? 1 : nseg == 2 ? 2 : nseg <= 3 ? 3 : 6; }
+
 template <int FMT, bool ARGMAX>
 static hipError_t launch_staged(const void *w, const float *x, float *y, int inner, int outer,
-                                void *ws, int32_t *token, uint32_t *flags, hipStream_t s)
+                                void *parts, hipStream_t s)
 {
     const int nblk = inner / block_elems(FMT);
-    const int R = g_rows_staged;
-#define IHIP_KS(RR)                                                                          \
-    case RR:                                                                                 \
-        hipLaunchKernelGGL((k_gemv_staged<FMT, RR, ARGMAX>),                                 \
-                           dim3((outer + 4 * RR - 1) / (4 * RR)), dim3(256), 0, s,            \
-                           (const uint8_t *)w, x, y, outer, nblk, (ArgmaxWS *)ws, token,      \
-                           flags);                                                           \
-        break;
-    switch (R) {
-        IHIP_KS(1)
-        IHIP_KS(4)
-    default:
-        IHIP_KS(2)
+    const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
+    const int S = stage_segments(nseg);
+    const int R = g_rows_staged == 1 ? 1 : 2;
+    const int nrg = (outer + 4 * R - 1) / (4 * R);
+    const int grid = ARGMAX ? min(nrg, kArgMaxParts) : nrg;
+#define IHIP_KS(RR, SS)                                                                      \
+    if (R == RR && S == SS) {                                                                \
+        hipLaunchKernelGGL((k_gemv_staged<FMT, RR, SS, ARGMAX>), dim3(grid), dim3(256), 0, s, \
+                           (const uint8_t *)w, x, y, outer, nblk, (ArgPart *)parts);          \
+        return hipGetLastError();                                                            \
     }
+    IHIP_KS(1, 1) IHIP_KS(1, 2) IHIP_KS(1, 3) IHIP_KS(1, 6)
+    IHIP_KS(2, 1) IHIP_KS(2, 2) IHIP_KS(2, 3) IHIP_KS(2, 6)
 #undef IHIP_KS
-    return hipGetLastError();
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
                        hipStream_t s)
 {
     switch (type) {
-    case kQ4_K: return launch_kdirect<kQ4_K, false>(w, nullptr, x, y, inner, outer, s);
-    case kQ5_K: return launch_kdirect<kQ5_K, false>(w, nullptr, x, y, inner, outer, s);
-    case kQ6_K: return launch_staged<kQ6_K, false>(w, x, y, inner, outer, nullptr, nullptr, nullptr, s);
-    case kQ8_0: return launch_staged<kQ8_0, false>(w, x, y, inner, outer, nullptr, nullptr, nullptr, s);
+    case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s);
+    case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s);
+    case kQ6_K: return launch_staged<kQ6_K, false>(w, x, y, inner, outer, nullptr, s);
+    case kQ8_0: return launch_staged<kQ8_0, false>(w, x, y, inner, outer, nullptr, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -559,8 +721,8 @@ hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const
                                  float *h, int hidden, int inter, hipStream_t s)
 {
     switch (type) {
-    case kQ4_K: return launch_kdirect<kQ4_K, true>(wg, wu, x, h, hidden, inter, s);
-    case kQ5_K: return launch_kdirect<kQ5_K, true>(wg, wu, x, h, hidden, inter, s);
+    case kQ4_K: return launch_kwide<kQ4_K, true>(wg, wu, x, h, hidden, inter, s);
+    case kQ5_K: return launch_kwide<kQ5_K, true>(wg, wu, x, h, hidden, inter, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -569,21 +731,31 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s)
 {
+    hipError_t e;
     switch (type) {
-    case kQ6_K: return launch_staged<kQ6_K, true>(w, x, logits, hidden, vocab, ws, token, flags, s);
-    case kQ8_0: return launch_staged<kQ8_0, true>(w, x, logits, hidden, vocab, ws, token, flags, s);
+    case kQ6_K: e = launch_staged<kQ6_K, true>(w, x, logits, hidden, vocab, ws, s); break;
+    case kQ8_0: e = launch_staged<kQ8_0, true>(w, x, logits, hidden, vocab, ws, s); break;
     default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess)
+        return e;
+    const int R = g_rows_staged == 1 ? 1 : 2;
+    const int nparts = min((vocab + 4 * R - 1) / (4 * R), kArgMaxParts);
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws, nparts,
+                       token, flags);
+    return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float *v, int64_t n, int32_t *token, uint32_t *flags, void *ws,
                          hipStream_t s)
 {
     int64_t blocks = (n + 255) / 256;
-    if (blocks > 1024) blocks = 1024;
+    if (blocks > kArgMaxParts) blocks = kArgMaxParts;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)blocks), dim3(256), 0, s, v, n, (ArgmaxWS *)ws,
-                       token, flags);
+    hipLaunchKernelGGL(k_argmax_partials, dim3((unsigned)blocks), dim3(256), 0, s, v, n,
+                       (ArgPart *)ws);
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws,
+                       (int)blocks, token, flags);
     return hipGetLastError();
 }
 

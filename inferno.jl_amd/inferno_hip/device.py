@@ -57,8 +57,9 @@ class DeviceWeight:
 
 
 class ArgmaxWorkspace:
-    """IHIP_ARGMAX_WS_BYTES of zeroed device memory plus the token/flags
-    outputs; the kernels leave the workspace zeroed after every call."""
+    """IHIP_ARGMAX_WS_BYTES of device memory for the per-workgroup partial
+    maxima, plus the token/flags outputs.  Calls sharing one workspace must
+    not overlap on the GPU."""
 
     def __init__(self, device="cuda"):
         self.ws = torch.zeros(_lib.ARGMAX_WS_BYTES, dtype=torch.uint8, device=device)

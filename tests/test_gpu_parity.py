@@ -158,6 +158,55 @@ def test_gemv_host_mirror_and_weight_cache(t):
                   oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), "after forget")
 
 
+TUNING_CASES = [
+    ("rows_wide", r, t, outer, inner)
+    for r in (1, 2, 4) for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608))
+] + [
+    ("rows_staged", r, t, outer, inner)
+    for r in (1, 2) for t, outer, inner in ((synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144),
+                                            (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304))
+]
+
+
+@pytest.mark.parametrize("knob,value,t,outer,inner", TUNING_CASES)
+def test_gemv_every_kernel_variant(knob, value, t, outer, inner):
+    from inferno_hip import _lib, device as D
+    say(f"gemv {knob}={value} type={t} {outer}x{inner}")
+    rng = synth.rng_for(value * 131 + t + inner + outer)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner)
+    _lib.set_tuning(knob, value)
+    try:
+        y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
+    finally:
+        _lib.set_tuning(knob, 2)
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
+    assert_within(y, ref, tol, f"{knob}={value} type {t} {outer}x{inner}")
+
+
+@pytest.mark.parametrize("value", [1, 2, 4])
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K])
+def test_gate_up_every_kernel_variant(value, t):
+    from inferno_hip import _lib, device as D
+    hidden, inter = 4096, 1030
+    say(f"gate/up rows_gateup={value} type={t}")
+    rng = synth.rng_for(value + 17 * t)
+    wg = synth.weight(rng, t, inter, hidden)
+    wu = synth.weight(rng, t, inter, hidden)
+    x = synth.activations(rng, hidden)
+    _lib.set_tuning("rows_gateup", value)
+    try:
+        h = D.gate_up_swiglu(dweight(wg, t, hidden, inter), dweight(wu, t, hidden, inter),
+                             dev(x)).cpu().numpy()
+    finally:
+        _lib.set_tuning("rows_gateup", 2)
+    g = oracle.gemv_f64(t, wg, x, hidden, inter)
+    u = oracle.gemv_f64(t, wu, x, hidden, inter)
+    hb = _h_bound(g, u, oracle.row_norms(t, wg, hidden, inter), oracle.row_norms(t, wu, hidden, inter), x)
+    assert_within(h, g / (1 + np.exp(-g)) * u, hb, "h")
+
+
 def test_gemv_special_inputs():
     from inferno_hip import device as D
     rng = synth.rng_for(4242)
