@@ -60,7 +60,39 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="gemv: the headline GEMV only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run the short program the rocprofv3 --pmc traffic runs profile")
     return ap.parse_args()
+
+
+def traffic_bytes():
+    """HBM bytes per Q4_K GEMV launch from the committed FETCH_SIZE / WRITE_SIZE
+    measurement (each counter scaled by what it reads for a plain copy of
+    known size), or None when that record is absent."""
+    p = ROOT / "profiles" / "q4k_gemv_4096x4096_traffic.json"
+    if not p.exists():
+        return None
+    d = json.loads(p.read_text())
+    g = d["gemv_per_dispatch"]
+    return int(round((g["FETCH_SIZE_KiB"] * d["fetch_factor"] + g["WRITE_SIZE_KiB"] * d["write_factor"]) * 1024))
+
+
+def pmc_workload(torch, synth, D):
+    src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    w = synth.weight(synth.rng_for(0xC0), synth.Q4_K, 4096, 4096)
+    base = torch.from_numpy(w).cuda()
+    ws = [D.DeviceWeight(base.clone(), synth.Q4_K, 4096, 4096) for _ in range(64)]
+    x = torch.from_numpy(synth.activations(synth.rng_for(0xC0 + 1), 4096)).cuda()
+    ys = torch.empty(64, 4096, device="cuda")
+    for _ in range(3):
+        for i in range(64):
+            D.gemv(ws[i], x, ys[i])
+    torch.cuda.synchronize()
+    print("pmc workload done: 3 x 64 MiB copy, 192 Q4_K 4096x4096 GEMV launches", flush=True)
 
 
 # ------------------------------------------------------------------ timing --
@@ -327,6 +359,9 @@ def main():
     if not torch.cuda.is_available() or not _lib.available():
         raise SystemExit("bench.py needs an MI355X (gfx950) and libinferno_hip.so")
     torch.cuda.set_device(0)
+    if args.pmc_workload:
+        pmc_workload(torch, synth, D)
+        return
     stream = torch.cuda.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
 
@@ -381,7 +416,7 @@ def main():
                    "rows": 4096, "cols": 4096, "weight_bytes": 9437184,
                    "algorithmic_bytes_per_step": g["bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes()},
         "cpu_baseline": cpu,
         "extras": extras,
     }

@@ -51,10 +51,13 @@ struct KFmt<kQ5_K> {
 // block b: low nibbles are elements 64j + l (sub-block 2j), high nibbles
 // 64j + 32 + l (sub-block 2j+1), l = 0..31 (src/Dequant.jl:364-371).
 //
-// Both operands are staged in LDS so that every global load is a fully
-// contiguous 1 KB wave access: the rows' bytes with direct-to-LDS loads, x
-// with plain loads into a padded layout (4 floats of padding after every 64)
-// under which a lane's 16-byte x reads hit distinct banks across the wave.
+// The weight bytes go straight to registers (three 128-bit loads per row and
+// lane).  x is read once per workgroup with contiguous loads and kept in LDS
+// in a padded layout (4 floats of padding after every 64) under which a
+// lane's 16-byte reads hit distinct banks across the wave; the workgroup also
+// leaves the sum of every 32-element sub-block of x there.  Loads are issued
+// x first, then every row's weights, so x can be staged while the weights are
+// still in flight, and each row is reduced as soon as its own bytes land.
 struct XWide {
     float a[32], b[32];
     float sa, sb;
@@ -63,7 +66,38 @@ struct XWide {
 constexpr int kXPadFloats = 4096 + 4096 / 64 * 4;
 __device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
 
-__device__ __forceinline__ void x_from_lds(const float *xs, int b, int j, XWide &X)
+// Stage x[col0, col0 + 4096) (zeros past `inner`) and its 128 sub-block sums.
+// `xv` holds this thread's four float4 of x, loaded by the caller.
+__device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&xv)[4])
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = 4 * (tid + 256 * k);
+        *reinterpret_cast<float4 *>(xs + xpad(i)) = xv[k];
+        // 8 consecutive threads hold one 32-element sub-block
+        float t = (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w);
+        t += __shfl_xor(t, 1, 64);
+        t += __shfl_xor(t, 2, 64);
+        t += __shfl_xor(t, 4, 64);
+        if ((tid & 7) == 0)
+            xsum[(tid + 256 * k) >> 3] = t;
+    }
+}
+
+__device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col0, int inner,
+                                            float4 (&xv)[4])
+{
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int col = col0 + 4 * (threadIdx.x + 256 * k);
+        xv[k] = col < inner ? *reinterpret_cast<const float4 *>(x + col)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+__device__ __forceinline__ void x_from_lds(const float *xs, const float *xsum, int b, int j,
+                                           XWide &X)
 {
     const int base = 256 * b + 64 * j;
 #pragma unroll
@@ -73,14 +107,9 @@ __device__ __forceinline__ void x_from_lds(const float *xs, int b, int j, XWide 
         X.a[4 * t + 0] = va.x; X.a[4 * t + 1] = va.y; X.a[4 * t + 2] = va.z; X.a[4 * t + 3] = va.w;
         X.b[4 * t + 0] = vb.x; X.b[4 * t + 1] = vb.y; X.b[4 * t + 2] = vb.z; X.b[4 * t + 3] = vb.w;
     }
-    float sa0 = 0.0f, sa1 = 0.0f, sb0 = 0.0f, sb1 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i += 2) {
-        sa0 += X.a[i]; sa1 += X.a[i + 1];
-        sb0 += X.b[i]; sb1 += X.b[i + 1];
-    }
-    X.sa = sa0 + sa1;
-    X.sb = sb0 + sb1;
+    const float2 s2 = *reinterpret_cast<const float2 *>(xsum + 8 * b + 2 * j);
+    X.sa = s2.x;
+    X.sb = s2.y;
 }
 
 // The block bytes one lane needs for one row: header (d, dmin, scales), its
@@ -90,7 +119,7 @@ struct KBytes {
 };
 
 template <int FMT>
-__device__ __forceinline__ void kbytes_from_lds(const uint8_t *blk, int j, KBytes &B)
+__device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int j, KBytes &B)
 {
     using F = KFmt<FMT>;
     B.h = *reinterpret_cast<const uint4 *>(blk);
@@ -103,6 +132,25 @@ __device__ __forceinline__ void kbytes_from_lds(const uint8_t *blk, int j, KByte
 }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// 6-bit scale and min of sub-blocks 2j and 2j+1 as floats (src/Dequant.jl:345-362),
+// from header dwords s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].
+__device__ __forceinline__ void k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                                 float &scA, float &mA, float &scB, float &mB)
+{
+    const uint32_t sh = 16u * (uint32_t)(j & 1); // bytes 2(j&1), 2(j&1)+1
+    const uint32_t w0 = s0 >> sh, w1 = s1 >> sh, w2 = s2 >> sh;
+    // sub-blocks 0..3: low 6 bits of scales[i] / scales[i+4]
+    const uint32_t sc_lo = w0 & 0x3f3fu, m_lo = w1 & 0x3f3fu;
+    // sub-blocks 4..7: nibbles of scales[i+4], top bits of scales[i-4] / scales[i]
+    const uint32_t sc_hi = (w2 & 0x0f0fu) | ((w0 >> 2) & 0x3030u);
+    const uint32_t m_hi = ((w2 >> 4) & 0x0f0fu) | ((w1 >> 2) & 0x3030u);
+    const uint32_t sc = j >= 2 ? sc_hi : sc_lo, m = j >= 2 ? m_hi : m_lo;
+    scA = ubyte_f(sc, 0);
+    scB = ubyte_f(sc, 1);
+    mA = ubyte_f(m, 0);
+    mB = ubyte_f(m, 1);
+}
 
 // One lane's contribution to one row.
 //
@@ -162,21 +210,17 @@ __device__ __forceinline__ float kwide_dot(const KBytes &B, int j, const XWide &
         sb0 += sb1;
     }
     const float d = h2f(B.h.x & 0xffffu), dmin = h2f(B.h.x >> 16);
-    uint32_t scA, mA, scB, mB;
-    k_scale_min(B.h.y, B.h.z, B.h.w, 2 * j, scA, mA);
-    k_scale_min(B.h.y, B.h.z, B.h.w, 2 * j + 1, scB, mB);
-    float r = (d * (float)scA) * sa0;
-    r = fmaf(d * (float)scB, sb0, r);
-    r = fmaf(-(dmin * (float)mA), X.sa, r);
-    r = fmaf(-(dmin * (float)mB), X.sb, r);
-    return r;
+    float scA, mA, scB, mB;
+    k_scale_min_pair(B.h.y, B.h.z, B.h.w, j, scA, mA, scB, mB);
+    const float pos = fmaf(scA, sa0, scB * sb0);
+    const float neg = fmaf(mA, X.sa, mB * X.sb);
+    return fmaf(d, pos, -(dmin * neg));
 }
 
 // Plain GEMV (GATEUP == false) or fused gate/up + SwiGLU (GATEUP == true:
 // W2 is the up weight, y[r] = silu(g[r]) * u[r]).  Wave w of workgroup g
-// owns rows [(4g + w) R, (4g + w + 1) R).  Per 4096-column pass: each wave
-// copies its rows' bytes into its LDS region, the workgroup stages x, one
-// barrier, then every wave reduces its rows from LDS.
+// owns rows [(4g + w) R, (4g + w + 1) R); rows past `outer` re-read the last
+// row and are not stored.
 template <int FMT, int R, bool GATEUP>
 __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ W,
                                                     const uint8_t *__restrict__ W2,
@@ -185,18 +229,14 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
 {
     using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
-    constexpr int PASS_BYTES = 16 * F::BYTES; // one row's bytes of a 16-block pass
-    constexpr int WAVE_BYTES = NW * R * PASS_BYTES;
     __shared__ __attribute__((aligned(16))) float xs[kXPadFloats];
-    __shared__ __attribute__((aligned(16))) uint8_t wb[4 * WAVE_BYTES];
+    __shared__ __attribute__((aligned(16))) float xsum[128];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
-    const bool live = row0 < outer; // wave-uniform; dead waves still join the barriers
     const int b = lane >> 2, j = lane & 3;
     const int inner = nblk * 256;
     const size_t row_bytes = (size_t)nblk * F::BYTES;
-    uint8_t *mine = wb + wave * WAVE_BYTES;
 
     float acc[NW][R];
 #pragma unroll
@@ -207,56 +247,38 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
     const int npass = (nblk + 15) >> 4;
     for (int pass = 0; pass < npass; ++pass) {
         const int nb = min(16, nblk - pass * 16);
-        if (live) {
-            const int chunks = nb * (F::BYTES / 16);
+        const bool active = b < nb;
+        const int blk = pass * 16 + (active ? b : 0);
+        float4 xv[4];
+        x_load_pass(x, pass * 4096, inner, xv);
+        KBytes B[NW][R];
 #pragma unroll
-            for (int m = 0; m < NW; ++m) {
-                const uint8_t *Wm = m == 0 ? W : W2;
+        for (int m = 0; m < NW; ++m) {
+            const uint8_t *Wm = m == 0 ? W : W2;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int row = min(row0 + r, outer - 1); // rows past the end re-read the last
-                    const uint8_t *src = Wm + (size_t)row * row_bytes + (size_t)pass * PASS_BYTES;
-                    uint8_t *dst = mine + (m * R + r) * PASS_BYTES;
-                    for (int c0 = 0; c0 < chunks; c0 += 64) {
-                        const int c = c0 + lane;
-                        if (c < chunks)
-                            __builtin_amdgcn_global_load_lds(
-                                (const void *)(src + 16 * (size_t)c),
-                                (__attribute__((address_space(3))) void *)(dst + 16 * c0), 16, 0, 0);
-                    }
-                }
+            for (int r = 0; r < R; ++r) {
+                const int row = min(row0 + r, outer - 1);
+                kbytes_load<FMT>(Wm + (size_t)row * row_bytes + (size_t)blk * F::BYTES, j, B[m][r]);
             }
         }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = 4 * (tid + 256 * k); // float index inside the pass
-            const int col = pass * 4096 + i;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (col < inner)
-                v = *reinterpret_cast<const float4 *>(x + col);
-            *reinterpret_cast<float4 *>(xs + xpad(i)) = v;
-        }
-        __builtin_amdgcn_s_waitcnt(0); // this wave's LDS copies have landed
+        // keep every load above in flight before the first use
+        __builtin_amdgcn_sched_barrier(0);
+        if (pass > 0)
+            __syncthreads(); // the previous pass is done with xs / xsum
+        x_stage(xs, xsum, xv);
         __syncthreads();
-        if (live) {
-            XWide X;
-            x_from_lds(xs, b, j, X);
-            const bool active = b < nb;
+        XWide X;
+        x_from_lds(xs, xsum, b, j, X);
 #pragma unroll
-            for (int m = 0; m < NW; ++m)
+        for (int m = 0; m < NW; ++m)
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    KBytes B;
-                    kbytes_from_lds<FMT>(mine + (m * R + r) * PASS_BYTES + b * F::BYTES, j, B);
-                    const float c = kwide_dot<FMT>(B, j, X);
-                    acc[m][r] += active ? c : 0.0f;
-                }
-        }
-        if (pass + 1 < npass)
-            __syncthreads(); // the next pass overwrites xs and wb
+            for (int r = 0; r < R; ++r) {
+                const float c = kwide_dot<FMT>(B[m][r], j, X);
+                acc[m][r] += active ? c : 0.0f;
+            }
     }
-    if (!live)
-        return;
+    if (row0 >= outer)
+        return; // wave-uniform, after the last barrier
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float g = wave_sum(acc[0][r]);
@@ -640,9 +662,10 @@ __global__ __launch_bounds__(256) void k_gemv_staged(const uint8_t *__restrict__
 // ------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------
-static int g_rows_wide = 2;   // rows per wave, Q4_K/Q5_K GEMV
-static int g_rows_gateup = 2; // rows per wave, fused gate/up
-static int g_rows_staged = 2; // rows per wave, Q6_K/Q8_0 GEMV
+// Rows per wave; 0 = the measured default for the format.
+static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 4 / 2)
+static int g_rows_gateup = 0; // fused gate/up (default 2)
+static int g_rows_staged = 0; // Q6_K/Q8_0 GEMV (default 2)
 
 void set_tuning(const char *name, int value)
 {
@@ -657,6 +680,8 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
 {
     const int nblk = inner / 256;
     int R = GATEUP ? g_rows_gateup : g_rows_wide;
+    if (R <= 0)
+        R = (GATEUP || FMT == kQ5_K) ? 2 : 4;
     if (FMT == kQ5_K && GATEUP && R > 2)
         R = 2; // register budget
 #define IHIP_KW(RR)                                                                          \
@@ -685,7 +710,7 @@ static hipError_t launch_staged(const void *w, const float *x, float *y, int inn
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int S = stage_segments(nseg);
-    const int R = g_rows_staged == 1 ? 1 : 2;
+    const int R = g_rows_staged == 1 ? 1 : 2; // default 2
     const int nrg = (outer + 4 * R - 1) / (4 * R);
     const int grid = ARGMAX ? min(nrg, kArgMaxParts) : nrg;
 #define IHIP_KS(RR, SS)                                                                      \
@@ -739,7 +764,7 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
     }
     if (e != hipSuccess)
         return e;
-    const int R = g_rows_staged == 1 ? 1 : 2;
+    const int R = g_rows_staged == 1 ? 1 : 2; // default 2
     const int nparts = min((vocab + 4 * R - 1) / (4 * R), kArgMaxParts);
     hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws, nparts,
                        token, flags);

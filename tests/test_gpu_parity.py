@@ -179,7 +179,7 @@ def test_gemv_every_kernel_variant(knob, value, t, outer, inner):
     try:
         y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
     finally:
-        _lib.set_tuning(knob, 2)
+        _lib.set_tuning(knob, 0)
     ref = oracle.gemv_f64(t, w, x, inner, outer)
     tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
     assert_within(y, ref, tol, f"{knob}={value} type {t} {outer}x{inner}")
@@ -200,7 +200,7 @@ def test_gate_up_every_kernel_variant(value, t):
         h = D.gate_up_swiglu(dweight(wg, t, hidden, inter), dweight(wu, t, hidden, inter),
                              dev(x)).cpu().numpy()
     finally:
-        _lib.set_tuning("rows_gateup", 2)
+        _lib.set_tuning("rows_gateup", 0)
     g = oracle.gemv_f64(t, wg, x, hidden, inter)
     u = oracle.gemv_f64(t, wu, x, hidden, inter)
     hb = _h_bound(g, u, oracle.row_norms(t, wg, hidden, inter), oracle.row_norms(t, wu, hidden, inter), x)
