@@ -79,8 +79,8 @@ int ihip_init(int device);
 int ihip_shutdown(void);
 /* Performance knobs (no effect on results beyond fp32 summation order):
  * "rows_wide" (rows per wave of the Q4_K/Q5_K GEMV: 1, 2, 4), "rows_gateup"
- * (the fused gate/up GEMV: 1, 2, 4), "rows_staged" (Q6_K/Q8_0 GEMV: 1, 2);
- * 0 restores the default. */
+ * (the fused gate/up GEMV: 1, 2, 4), "stream_rows" (rows per workgroup chunk
+ * of the Q6_K/Q8_0 GEMV: 1..64); 0 restores the default. */
 int ihip_set_tuning(const char *name, int value);
 
 /* ---- weight registry (host entry points use it implicitly) ------------ */

@@ -51,13 +51,27 @@ __device__ __forceinline__ void k_scale_min(uint32_t s0, uint32_t s1, uint32_t s
     m = i < 4 ? m_lo : m_hi;
 }
 
-// Sum over the 64 lanes of a wavefront; every lane gets the total.
+// v + (v moved across lanes by a DPP pattern); lanes outside row_mask add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v)
+{
+    const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+    return v + __int_as_float(moved);
+}
+
+// Sum over the 64 lanes of a wavefront; every lane gets the total.  DPP lane
+// moves (no LDS traffic): pairs, quads, half-rows and rows of 16 by
+// quad_perm / row_half_mirror / row_mirror, then row_bcast:15 and
+// row_bcast:31 carry the row sums up to lane 63, whose value is broadcast.
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1)
-        v += __shfl_xor(v, o, 64);
-    return v;
+    v = dpp_add<0xb1, 0xf>(v);  // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e, 0xf>(v);  // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v); // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v); // row_mirror
+    v = dpp_add<0x142, 0xa>(v); // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v); // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Read 8 bytes starting at byte `off` of a 4-byte-aligned LDS array as two

@@ -77,9 +77,9 @@ __device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&x
         *reinterpret_cast<float4 *>(xs + xpad(i)) = xv[k];
         // 8 consecutive threads hold one 32-element sub-block
         float t = (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w);
-        t += __shfl_xor(t, 1, 64);
-        t += __shfl_xor(t, 2, 64);
-        t += __shfl_xor(t, 4, 64);
+        t = dpp_add<0xb1, 0xf>(t);  // pairs
+        t = dpp_add<0x4e, 0xf>(t);  // quads
+        t = dpp_add<0x141, 0xf>(t); // 8 lanes (row_half_mirror)
         if ((tid & 7) == 0)
             xsum[(tid + 256 * k) >> 3] = t;
     }
@@ -232,7 +232,8 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
     __shared__ __attribute__((aligned(16))) float xs[kXPadFloats];
     __shared__ __attribute__((aligned(16))) float xsum[128];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
     const int row0 = (blockIdx.x * 4 + wave) * R;
     const int b = lane >> 2, j = lane & 3;
     const int inner = nblk * 256;
@@ -331,41 +332,46 @@ struct SX<kQ8_0> {
     float x[32];
 };
 
+// All loads first, then the selects and sums, so that the loads are in
+// flight together.
 template <int FMT>
 __device__ __forceinline__ void staged_load_x(const float *__restrict__ xseg, int lane,
                                               int seg_blocks, SX<FMT> &X)
 {
+    float4 v[8];
+    bool active;
     if constexpr (FMT == kQ6_K) {
         const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-        const bool active = bs < seg_blocks;
+        active = bs < seg_blocks;
+        const float *base = xseg + (active ? 256 * bs + 128 * n + l0 : 0);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            if (active) {
-                const float4 *p =
-                    reinterpret_cast<const float4 *>(xseg + 256 * bs + 128 * n + 32 * g + l0);
-                const float4 v0 = p[0], v1 = p[1];
-                X.x[g][0] = v0.x; X.x[g][1] = v0.y; X.x[g][2] = v0.z; X.x[g][3] = v0.w;
-                X.x[g][4] = v1.x; X.x[g][5] = v1.y; X.x[g][6] = v1.z; X.x[g][7] = v1.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) X.x[g][i] = 0.0f;
-            }
-            float sum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sum += X.x[g][i];
-            X.s[g] = sum;
+            const float4 *p = reinterpret_cast<const float4 *>(base + 32 * g);
+            v[2 * g] = p[0];
+            v[2 * g + 1] = p[1];
         }
     } else {
-        if (lane < seg_blocks) {
-            const float4 *p = reinterpret_cast<const float4 *>(xseg + 32 * lane);
+        active = lane < seg_blocks;
+        const float4 *p = reinterpret_cast<const float4 *>(xseg + (active ? 32 * lane : 0));
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const float4 v = p[t];
-                X.x[4 * t] = v.x; X.x[4 * t + 1] = v.y; X.x[4 * t + 2] = v.z; X.x[4 * t + 3] = v.w;
-            }
-        } else {
+        for (int t = 0; t < 8; ++t) v[t] = p[t];
+    }
 #pragma unroll
-            for (int i = 0; i < 32; ++i) X.x[i] = 0.0f;
+    for (int t = 0; t < 8; ++t)
+        if (!active) v[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (FMT == kQ6_K) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 a = v[2 * g], b = v[2 * g + 1];
+            X.x[g][0] = a.x; X.x[g][1] = a.y; X.x[g][2] = a.z; X.x[g][3] = a.w;
+            X.x[g][4] = b.x; X.x[g][5] = b.y; X.x[g][6] = b.z; X.x[g][7] = b.w;
+            X.s[g] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            X.x[4 * t] = v[t].x; X.x[4 * t + 1] = v[t].y;
+            X.x[4 * t + 2] = v[t].z; X.x[4 * t + 3] = v[t].w;
         }
     }
 }
@@ -555,123 +561,166 @@ __global__ __launch_bounds__(256) void k_argmax_partials(const float *__restrict
     argmax_store_partial(key, fl, parts + blockIdx.x);
 }
 
-// ---- the staged GEMV ------------------------------------------------------
-// Workgroup = 4 waves; wave w of row group g owns rows [(4g + w) R, +R).
-// Each wave stages up to S segments of its R rows into its own LDS region
-// (R * S * SEG_BYTES bytes) with direct-to-LDS loads, waits, then computes;
-// the x slice of the next segment is loaded while the current one is
-// reduced.  ARGMAX: the workgroup walks row groups grid-stride and stores
-// one argmax partial; `y` may then be null.
-template <int FMT, int R, int S, bool ARGMAX>
-__global__ __launch_bounds__(256) void k_gemv_staged(const uint8_t *__restrict__ W,
-                                                     const float *__restrict__ x,
-                                                     float *__restrict__ y, int outer, int nblk,
-                                                     ArgPart *__restrict__ parts)
+// ---- the streamed staged GEMV --------------------------------------------
+// Workgroup = NW waves; wave w owns K segments w, w + NW, ... so the x slice
+// of its segment stays in registers while it streams the workgroup's rows
+// through a D-slot LDS ring filled by direct-to-LDS 128-bit loads: the copy
+// of row i + D is issued as soon as row i has been reduced, so D rows per
+// wave are always in flight.  Per-row partial sums meet in LDS and the
+// workgroup's threads finish the rows (and, ARGMAX, fold them into one
+// partial per workgroup).  Workgroups walk chunks of `rpc` rows grid-stride.
+
+// Wait until at most n of this wave's vector-memory operations are
+// outstanding (n <= 31; expcnt and lgkmcnt are not waited on).
+__device__ __forceinline__ void wait_vmcnt(int n)
+{
+#define IHIP_VM(N)                                                                             \
+    case N:                                                                                    \
+        __builtin_amdgcn_s_waitcnt(((N)&15) | (((N) >> 4) << 14) | 0x0F70);                    \
+        break;
+    switch (n) {
+        IHIP_VM(0) IHIP_VM(1) IHIP_VM(2) IHIP_VM(3) IHIP_VM(4) IHIP_VM(5) IHIP_VM(6) IHIP_VM(7)
+        IHIP_VM(8) IHIP_VM(9) IHIP_VM(10) IHIP_VM(11) IHIP_VM(12) IHIP_VM(13) IHIP_VM(14)
+        IHIP_VM(15) IHIP_VM(16) IHIP_VM(17) IHIP_VM(18) IHIP_VM(19) IHIP_VM(20) IHIP_VM(21)
+        IHIP_VM(22) IHIP_VM(23) IHIP_VM(24) IHIP_VM(25) IHIP_VM(26) IHIP_VM(27) IHIP_VM(28)
+        IHIP_VM(29) IHIP_VM(30) IHIP_VM(31)
+    default:
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+#undef IHIP_VM
+}
+
+constexpr int kStreamMaxRows = 64; // rows per chunk (one partial slot per row and wave)
+
+template <int FMT, int NW, int D, bool ARGMAX>
+__global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restrict__ W,
+                                                         const float *__restrict__ x,
+                                                         float *__restrict__ y, int outer,
+                                                         int nblk, int rpc,
+                                                         ArgPart *__restrict__ parts)
 {
     using F = SFmt<FMT>;
-    constexpr int WAVE_BYTES = R * S * F::SEG_BYTES;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[4 * WAVE_BYTES + 16];
+    constexpr int SLOT = F::SEG_BYTES + 16; // Q8_0 reads one dword past a segment
+    __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * SLOT];
+    __shared__ float part[kStreamMaxRows][NW];
+    __shared__ unsigned long long wkey[NW];
+    __shared__ uint32_t wflag[NW];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t row_bytes = (size_t)nblk * block_bytes(FMT);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
+    const int bb = block_bytes(FMT);
+    const size_t row_bytes = (size_t)nblk * bb;
     const int nseg = (nblk + F::SEG_BLOCKS - 1) / F::SEG_BLOCKS;
-    const int nrg = (outer + 4 * R - 1) / (4 * R);
-    uint8_t *wt = tile + wave * WAVE_BYTES; // this wave's LDS region
-    const uint32_t wt_off = (uint32_t)(wave * WAVE_BYTES);
+    const int nchunks = (outer + rpc - 1) / rpc;
+    const uint32_t my_ring = (uint32_t)(w * D * SLOT);
 
     unsigned long long key = 0;
     uint32_t fl = 0;
+    SX<FMT> X;
+    int x_seg = -1; // segment whose x slice X holds
 
-    for (int rg = blockIdx.x; rg < nrg; rg += (ARGMAX ? gridDim.x : nrg)) {
-        const int row0 = (rg * 4 + wave) * R;
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-        if (row0 < outer) { // wave-uniform
-            for (int st = 0; st < nseg; st += S) {
-                const int ns = min(S, nseg - st);
-                // bytes of this stage in one row: whole segments except a
-                // short last one, always a multiple of 16 (checked on the host)
-                const int last_blocks = min(F::SEG_BLOCKS, nblk - (st + ns - 1) * F::SEG_BLOCKS);
-                const int stage_bytes = (ns - 1) * F::SEG_BYTES + last_blocks * block_bytes(FMT);
-                const int chunks = stage_bytes >> 4;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int row = min(row0 + r, outer - 1); // rows past the end re-read the last row
-                    const uint8_t *src = W + (size_t)row * row_bytes + (size_t)st * F::SEG_BYTES;
-                    uint8_t *dst = wt + r * S * F::SEG_BYTES;
-                    for (int c0 = 0; c0 < chunks; c0 += 64) {
-                        const int c = c0 + lane;
-                        if (c < chunks)
-                            __builtin_amdgcn_global_load_lds(
-                                (const void *)(src + 16 * (size_t)c),
-                                (__attribute__((address_space(3))) void *)(dst + 16 * c0), 16, 0, 0);
-                    }
+    for (int chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
+        const int row0 = chunk * rpc;
+        const int nrows = min(rpc, outer - row0);
+        for (int i = tid; i < kStreamMaxRows * NW; i += NW * 64)
+            (&part[0][0])[i] = 0.0f;
+        __syncthreads();
+        for (int sg = w; sg < nseg; sg += NW) { // wave-uniform
+            const int seg_blocks = min(F::SEG_BLOCKS, nblk - sg * F::SEG_BLOCKS);
+            // whole 8-block groups (checked on the host): a multiple of 16 bytes
+            const int chunks16 = seg_blocks * bb / 16;
+            const int ipr = (chunks16 + 63) >> 6; // copy instructions per row
+            const uint8_t *src0 = W + (size_t)row0 * row_bytes + (size_t)sg * F::SEG_BYTES;
+            auto issue = [&](int i) {
+                const uint8_t *src = src0 + (size_t)i * row_bytes;
+                uint8_t *dst = ring + my_ring + (i % D) * SLOT;
+                for (int c0 = 0; c0 < chunks16; c0 += 64) {
+                    const int c = c0 + lane;
+                    if (c < chunks16)
+                        __builtin_amdgcn_global_load_lds(
+                            (const void *)(src + 16 * (size_t)c),
+                            (__attribute__((address_space(3))) void *)(dst + 16 * c0), 16, 0, 0);
                 }
-                SX<FMT> X;
-                staged_load_x<FMT>(x + (size_t)st * 2048, lane,
-                                   min(F::SEG_BLOCKS, nblk - st * F::SEG_BLOCKS), X);
-                __builtin_amdgcn_s_waitcnt(0); // LDS copies (and x) have landed
-                for (int s = 0; s < ns; ++s) {
-                    const int seg = st + s;
-                    const int seg_blocks = min(F::SEG_BLOCKS, nblk - seg * F::SEG_BLOCKS);
-                    SX<FMT> Xn;
-                    if (s + 1 < ns)
-                        staged_load_x<FMT>(x + (size_t)(seg + 1) * 2048, lane,
-                                           min(F::SEG_BLOCKS, nblk - (seg + 1) * F::SEG_BLOCKS), Xn);
-                    if constexpr (FMT == kQ6_K) {
-                        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-                        if (bs < seg_blocks) {
-#pragma unroll
-                            for (int r = 0; r < R; ++r)
-                                acc[r] += q6_dot(tile,
-                                                 wt_off + (uint32_t)((r * S + s) * F::SEG_BYTES + 210 * bs),
-                                                 n, l0, X);
-                        }
-                    } else {
-                        if (lane < seg_blocks) {
-#pragma unroll
-                            for (int r = 0; r < R; ++r)
-                                acc[r] += q80_dot(wt + (r * S + s) * F::SEG_BYTES, 34u * lane, X.x);
-                        }
-                    }
-                    if (s + 1 < ns)
-                        X = Xn;
+            };
+            const int pre = min(D, nrows);
+            for (int i = 0; i < pre; ++i)
+                issue(i);
+            if (x_seg != sg) {
+                staged_load_x<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, X);
+                x_seg = sg;
+            }
+            // x (and the prologue rows) complete here, so that inside the row loop
+            // only ring copies are outstanding and the explicit waits below are
+            // the only ones
+            __builtin_amdgcn_s_waitcnt(0);
+            for (int i = 0; i < nrows; ++i) {
+                wait_vmcnt(ipr * min(D - 1, nrows - 1 - i)); // row i has landed
+                const uint32_t slot = my_ring + (uint32_t)((i % D) * SLOT);
+                float v = 0.0f;
+                if constexpr (FMT == kQ6_K) {
+                    const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+                    if (bs < seg_blocks)
+                        v = q6_dot(ring, slot + (uint32_t)(210 * bs), n, l0, X);
+                } else {
+                    if (lane < seg_blocks)
+                        v = q80_dot(ring + slot, 34u * lane, X.x);
                 }
+                v = wave_sum(v);
+                if (lane == 0)
+                    part[i][w] += v;
+                if (i + D < nrows)
+                    issue(i + D); // slot i % D has been read
             }
         }
+        __syncthreads();
+        for (int i = tid; i < nrows; i += NW * 64) {
+            float v = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float v = wave_sum(acc[r]);
-            const int row = row0 + r;
-            if (row < outer) {
-                if (y && lane == 0)
-                    y[row] = v;
-                if constexpr (ARGMAX)
-                    argmax_fold(v, (uint32_t)row, key, fl);
-            }
+            for (int k = 0; k < NW; ++k)
+                v += part[i][k];
+            if (y)
+                y[row0 + i] = v;
+            if constexpr (ARGMAX)
+                argmax_fold(v, (uint32_t)(row0 + i), key, fl);
         }
-        if constexpr (!ARGMAX)
-            break;
+        __syncthreads(); // part is cleared for the next chunk
     }
-    if constexpr (ARGMAX)
-        argmax_store_partial(key, fl, parts + blockIdx.x);
+    if constexpr (ARGMAX) {
+        argmax_wave_reduce(key, fl);
+        if (lane == 0) {
+            wkey[w] = key;
+            wflag[w] = fl;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long k = wkey[0];
+            uint32_t f = wflag[0];
+#pragma unroll
+            for (int i = 1; i < NW; ++i) {
+                k = wkey[i] > k ? wkey[i] : k;
+                f |= wflag[i];
+            }
+            parts[blockIdx.x].key = k;
+            parts[blockIdx.x].flags = f;
+            parts[blockIdx.x].pad = 0;
+        }
+    }
 }
 
 // ------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------
-// Rows per wave; 0 = the measured default for the format.
+// Rows per wave of the wide kernels and rows per chunk of the streamed
+// kernels; 0 = the measured default.
 static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 4 / 2)
 static int g_rows_gateup = 0; // fused gate/up (default 2)
-static int g_rows_staged = 0; // Q6_K/Q8_0 GEMV (default 2)
+static int g_stream_rows = 0; // Q6_K/Q8_0 rows per chunk (default: see stream_rows())
 
 void set_tuning(const char *name, int value)
 {
     if (!__builtin_strcmp(name, "rows_wide")) g_rows_wide = value;
     if (!__builtin_strcmp(name, "rows_gateup")) g_rows_gateup = value;
-    if (!__builtin_strcmp(name, "rows_staged")) g_rows_staged = value;
+    if (!__builtin_strcmp(name, "stream_rows")) g_stream_rows = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -700,28 +749,40 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
     return hipGetLastError();
 }
 
-// Segments staged per LDS fill: enough to cover the row when it is short.
-static int stage_segments(int nseg) { return nseg <= 1 ? 1 : nseg == 2 ? 2 : nseg <= 3 ? 3 : 6; }
+// Waves per workgroup of the streamed kernel: one per K segment, at most 8.
+static int stream_waves(int nseg) { return nseg >= 8 ? 8 : nseg >= 6 ? 6 : nseg >= 4 ? 4 : nseg; }
+
+// Rows per chunk: enough chunks for about four workgroups per CU (two when
+// a workgroup has four or more waves), within 4..32 (measured on MI355X:
+// longer chunks serialize too many rows per wave).
+static int stream_rows(int outer, int nw)
+{
+    if (g_stream_rows > 0)
+        return min(g_stream_rows, kStreamMaxRows);
+    const int target_wgs = 256 * (nw >= 4 ? 2 : 4);
+    int r = (outer + target_wgs - 1) / target_wgs;
+    r = r < 4 ? 4 : r > 32 ? 32 : r;
+    return r;
+}
+
+static int stream_grid(int outer, int rpc, bool argmax)
+{
+    const int nchunks = (outer + rpc - 1) / rpc;
+    return argmax ? min(nchunks, min(kArgMaxParts, 2048)) : nchunks;
+}
 
 template <int FMT, bool ARGMAX>
-static hipError_t launch_staged(const void *w, const float *x, float *y, int inner, int outer,
+static hipError_t launch_stream(const void *w, const float *x, float *y, int inner, int outer,
                                 void *parts, hipStream_t s)
 {
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
-    const int S = stage_segments(nseg);
-    const int R = g_rows_staged == 1 ? 1 : 2; // default 2
-    const int nrg = (outer + 4 * R - 1) / (4 * R);
-    const int grid = ARGMAX ? min(nrg, kArgMaxParts) : nrg;
-#define IHIP_KS(RR, SS)                                                                      \
-    if (R == RR && S == SS) {                                                                \
-        hipLaunchKernelGGL((k_gemv_staged<FMT, RR, SS, ARGMAX>), dim3(grid), dim3(256), 0, s, \
-                           (const uint8_t *)w, x, y, outer, nblk, (ArgPart *)parts);          \
-        return hipGetLastError();                                                            \
-    }
-    IHIP_KS(1, 1) IHIP_KS(1, 2) IHIP_KS(1, 3) IHIP_KS(1, 6)
-    IHIP_KS(2, 1) IHIP_KS(2, 2) IHIP_KS(2, 3) IHIP_KS(2, 6)
-#undef IHIP_KS
+    const int nw = stream_waves(nseg);
+    const int rpc = stream_rows(outer, nw);
+    const int grid = stream_grid(outer, rpc, ARGMAX);
+#define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts);         return hipGetLastError();                                                                }
+    IHIP_ST(1, 8) IHIP_ST(2, 8) IHIP_ST(3, 6) IHIP_ST(4, 4) IHIP_ST(6, 4) IHIP_ST(8, 4)
+#undef IHIP_ST
     return hipErrorInvalidValue;
 }
 
@@ -731,8 +792,8 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     switch (type) {
     case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s);
     case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s);
-    case kQ6_K: return launch_staged<kQ6_K, false>(w, x, y, inner, outer, nullptr, s);
-    case kQ8_0: return launch_staged<kQ8_0, false>(w, x, y, inner, outer, nullptr, s);
+    case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s);
+    case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -758,14 +819,15 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
 {
     hipError_t e;
     switch (type) {
-    case kQ6_K: e = launch_staged<kQ6_K, true>(w, x, logits, hidden, vocab, ws, s); break;
-    case kQ8_0: e = launch_staged<kQ8_0, true>(w, x, logits, hidden, vocab, ws, s); break;
+    case kQ6_K: e = launch_stream<kQ6_K, true>(w, x, logits, hidden, vocab, ws, s); break;
+    case kQ8_0: e = launch_stream<kQ8_0, true>(w, x, logits, hidden, vocab, ws, s); break;
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess)
         return e;
-    const int R = g_rows_staged == 1 ? 1 : 2; // default 2
-    const int nparts = min((vocab + 4 * R - 1) / (4 * R), kArgMaxParts);
+    const int nblk = hidden / block_elems(type);
+    const int nseg = (nblk + (type == kQ6_K ? 8 : 64) - 1) / (type == kQ6_K ? 8 : 64);
+    const int nparts = stream_grid(vocab, stream_rows(vocab, stream_waves(nseg)), true);
     hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws, nparts,
                        token, flags);
     return hipGetLastError();

@@ -162,9 +162,13 @@ TUNING_CASES = [
     ("rows_wide", r, t, outer, inner)
     for r in (1, 2, 4) for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608))
 ] + [
-    ("rows_staged", r, t, outer, inner)
-    for r in (1, 2) for t, outer, inner in ((synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144),
-                                            (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304))
+    # streamed Q6_K / Q8_0 kernel: rows per chunk x (waves per workgroup = segments, up to 8;
+    # 12 and 5 segments give waves that own two segments)
+    ("stream_rows", r, t, outer, inner)
+    for r in (4, 17, 64) for t, outer, inner in ((synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144),
+                                                 (synth.Q6_K, 300, 24576), (synth.Q6_K, 33, 10240),
+                                                 (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304),
+                                                 (synth.Q8_0, 19, 256))
 ]
 
 
