@@ -94,6 +94,19 @@ __device__ __forceinline__ uint32_t lds_read_u16(const uint8_t *lds, uint32_t of
     return *reinterpret_cast<const uint16_t *>(lds + off);
 }
 
+// Workgroup execution barrier without a memory fence.  __syncthreads()
+// carries a workgroup-scope release fence, which makes the compiler wait for
+// every outstanding direct-to-LDS copy (they count as LDS writes), including
+// copies issued ahead for the next stage.  Kernels that track their copies
+// with explicit s_waitcnt use this instead; the empty asm statements keep the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Hide a value from the optimizer (no instruction is emitted).  Used on
 // nibble-masked dwords so that the byte converts stay v_cvt_f32_ubyte{0..3}
 // instead of being refolded into a bit-field extract plus convert.

@@ -5,14 +5,18 @@
 // runs T independent GEMVs, so the semantics are the Q4_K GEMV applied row
 // by row.  On MI355X the T tokens share every weight byte, which makes this
 // a dense contraction: X is rounded once to fp16 (the matrix-core operand
-// type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not), each
-// K-step dequantizes one Q4_K super-block column of the W tile into LDS as
-// fp16, and v_mfma_f32_32x32x16_f16 accumulates in fp32.
+// type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not) and
+// v_mfma_f32_32x32x16_f16 accumulates in fp32.
 //
-// Tile: BM = 64 tokens x BN = 128 weight rows per workgroup of 4 waves; wave
-// w owns rows [32w, 32w+32) of the BN tile and both 32-token halves of BM.
-// K-step = 256 (one super-block).  Workgroups are mapped so that the 32
-// workgroups of one XCD (blockIdx % 8) share a contiguous band of W rows.
+// Tile: 64 tokens x 128 weight rows per workgroup of 4 waves (256 workgroups
+// at 512 x 4096 x 4096); wave w owns weight rows [32w, 32w+32) of the tile
+// and both 32-token halves.  The activations stream through a double-
+// buffered, bank-swizzled LDS stage one Q4_K block column (256 k) ahead;
+// each lane dequantizes the B operand it feeds the matrix core (one weight
+// row, 8 k per 16-wide step) straight into registers from the block bytes,
+// also loaded one block ahead, so the weights are dequantized exactly once
+// per workgroup and never pass through LDS.  Workgroups are mapped so that
+// those of one XCD (blockIdx % 8) share a contiguous band of W rows.
 #include "kq_common.h"
 #include "kq_launch.h"
 
@@ -21,8 +25,7 @@ namespace ihip {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int PF_BM = 64, PF_BN = 128, PF_BK = 256;
-constexpr int PF_LDA = PF_BK + 8; // halves per LDS row (16-byte pad against bank conflicts)
+constexpr int PF_BM = 64, PF_BN = 128; // workgroup tile: tokens x weight rows
 
 __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ X,
                                                   _Float16 *__restrict__ Xh, int64_t n)
@@ -40,108 +43,234 @@ __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ X,
     }
 }
 
-__global__ __launch_bounds__(256) void k_prefill_q4k(const uint8_t *__restrict__ W,
-                                                     const _Float16 *__restrict__ Xh,
-                                                     float *__restrict__ Y, int T, int K, int N,
-                                                     int mtiles, int ntiles)
-{
-    __shared__ __attribute__((aligned(16))) _Float16 As[PF_BM * PF_LDA];
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[PF_BN * PF_LDA];
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-    // XCD-aware tile order: consecutive workgroups of one XCD walk the
-    // M tiles of one N band.
+// One 64-token x 256-column stage of the fp16 activations in LDS: row m
+// holds 32 chunks of 16 bytes, chunk c at slot c ^ (m & 15), so that the 16
+// lanes of a 128-bit read (same chunk, consecutive rows) hit distinct banks.
+constexpr int PF_ROW_BYTES = 512;
+constexpr int PF_A_STAGE = 64 * PF_ROW_BYTES;   // 32 KB
+constexpr int PF_B_STAGE = PF_BN * 144;          // 18 KB: one Q4_K block of 128 rows
+constexpr int PF_THREADS = 512;                  // 8 waves
+
+// Register double-buffering of one block column: each of the 512 threads
+// loads 4 chunks (16 bytes) of the 64-token activation stage and up to 3 of
+// the 128-row weight stage for block kb + 1 while block kb is reduced, then
+// writes them to the other stage.
+struct PfRegs {
+    uint4 a0, a1, a2, a3, b0, b1, b2; // plain members: the registers must not become an array
+};
+
+__device__ __forceinline__ uint4 pf_load_a(const _Float16 *__restrict__ Xh, int m0, int T, int K,
+                                           int kb, int q)
+{
+    const int rp = q >> 5, slot = q & 31; // stage row q/32, slot q%32
+    const int c = slot ^ (rp & 15);       // the activation chunk that lives in this slot
+    const int row = min(m0 + rp, T - 1);  // rows past T re-read row T-1
+    return *reinterpret_cast<const uint4 *>(Xh + (size_t)row * K + (size_t)kb * 256 + 8 * c);
+}
+
+__device__ __forceinline__ uint4 pf_load_b(const uint8_t *__restrict__ W, int n0, int N,
+                                           size_t row_bytes, int kb, int q)
+{
+    // chunk q of the 128 x 144-byte weight stage (q < 1152; callers clamp)
+    const int row = q / 9, piece = q - 9 * (q / 9);
+    return *reinterpret_cast<const uint4 *>(W + (size_t)min(n0 + row, N - 1) * row_bytes +
+                                            (size_t)kb * 144 + 16 * piece);
+}
+
+__device__ __forceinline__ void pf_load(const _Float16 *__restrict__ Xh,
+                                        const uint8_t *__restrict__ W, int m0, int n0, int T,
+                                        int N, int K, size_t row_bytes, int kb, int tid, PfRegs &R)
+{
+    R.a0 = pf_load_a(Xh, m0, T, K, kb, tid);
+    R.a1 = pf_load_a(Xh, m0, T, K, kb, tid + PF_THREADS);
+    R.a2 = pf_load_a(Xh, m0, T, K, kb, tid + 2 * PF_THREADS);
+    R.a3 = pf_load_a(Xh, m0, T, K, kb, tid + 3 * PF_THREADS);
+    R.b0 = pf_load_b(W, n0, N, row_bytes, kb, tid);
+    R.b1 = pf_load_b(W, n0, N, row_bytes, kb, tid + PF_THREADS);
+    // the third round covers chunks 1024..1151: threads past it re-load chunk 1151
+    R.b2 = pf_load_b(W, n0, N, row_bytes, kb, min(tid + 2 * PF_THREADS, PF_BN * 9 - 1));
+}
+
+__device__ __forceinline__ void pf_store(uint8_t *sa, uint8_t *sb, int tid, const PfRegs &R)
+{
+    *reinterpret_cast<uint4 *>(sa + 16 * tid) = R.a0;
+    *reinterpret_cast<uint4 *>(sa + 16 * (tid + PF_THREADS)) = R.a1;
+    *reinterpret_cast<uint4 *>(sa + 16 * (tid + 2 * PF_THREADS)) = R.a2;
+    *reinterpret_cast<uint4 *>(sa + 16 * (tid + 3 * PF_THREADS)) = R.a3;
+    *reinterpret_cast<uint4 *>(sb + 16 * tid) = R.b0;
+    *reinterpret_cast<uint4 *>(sb + 16 * (tid + PF_THREADS)) = R.b1;
+    if (tid + 2 * PF_THREADS < PF_BN * 9)
+        *reinterpret_cast<uint4 *>(sb + 16 * (tid + 2 * PF_THREADS)) = R.b2;
+}
+
+// 8 nibbles (the low or high nibble of 8 bytes) -> 8 fp16 weights
+// q * dsc - dmm.  A byte 0000qqqq is the OCP e4m3 encoding of q * 2^-9; the
+// scaled convert multiplies by 2^9, giving q exactly in fp16, and one packed
+// fp16 FMA per pair applies the sub-block scale and min.
+__device__ __forceinline__ half8 pf_dequant8(uint2 bytes, bool high, half2v dsc, half2v dmm)
+{
+    uint32_t w0 = bytes.x, w1 = bytes.y;
+    if (high) {
+        w0 >>= 4;
+        w1 >>= 4;
+    }
+    w0 &= 0x0f0f0f0fu;
+    w1 &= 0x0f0f0f0fu;
+    const half2v q01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.0f, false);
+    const half2v q23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 512.0f, true);
+    const half2v q45 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.0f, false);
+    const half2v q67 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 512.0f, true);
+    const half2v r01 = __builtin_elementwise_fma(q01, dsc, dmm);
+    const half2v r23 = __builtin_elementwise_fma(q23, dsc, dmm);
+    const half2v r45 = __builtin_elementwise_fma(q45, dsc, dmm);
+    const half2v r67 = __builtin_elementwise_fma(q67, dsc, dmm);
+    half8 r;
+    r[0] = r01[0]; r[1] = r01[1]; r[2] = r23[0]; r[3] = r23[1];
+    r[4] = r45[0]; r[5] = r45[1]; r[6] = r67[0]; r[7] = r67[1];
+    return r;
+}
+
+// Y[t, n] = sum_k W[n, k] Xh[t, k].  Workgroup tile: 64 tokens x 128 weight
+// rows, 8 waves: wave w owns weight rows n0 + 32 (w & 3) .. +32, both
+// 32-token halves, and half (w >> 2) of every block column (sub-block pairs
+// 2 (w >> 2) and 2 (w >> 2) + 1); the two halves' sums meet in LDS at the
+// end.  Both operands stream through double-buffered LDS stages filled by
+// direct-to-LDS loads one block column ahead; each lane dequantizes the B
+// operand it feeds the matrix core (one weight row, 8 k per 16-wide step)
+// from the stage into registers, so the weights are dequantized exactly once
+// per workgroup.  v_mfma_f32_32x32x16_f16, fp32 accumulation.
+// Reduce block column kb from one stage (sa: activations, blk: this lane's
+// weight row of the B stage) into the accumulators.
+__device__ __forceinline__ void pf_block(const uint8_t *sa, const uint8_t *blk, int kh, int h,
+                                         int li, float16v (&acc)[2])
+{
+    const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+    const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * kh + jj;
+        uint32_t scA, mA, scB, mB;
+        k_scale_min(hd.y, hd.z, hd.w, 2 * j, scA, mA);
+        k_scale_min(hd.y, hd.z, hd.w, 2 * j + 1, scB, mB);
+        const _Float16 dA = (_Float16)(d * (float)scA), mnA = (_Float16)(-(dmin * (float)mA));
+        const _Float16 dB = (_Float16)(d * (float)scB), mnB = (_Float16)(-(dmin * (float)mB));
+        const half2v dsA = {dA, dA}, dmA = {mnA, mnA}, dsB = {dB, dB}, dmB = {mnB, mnB};
+        const uint2 q0 = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
+        const uint2 q1 = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
+        // four 16-wide K steps: k = 64j + 16s + 8h + (0..7)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const half8 b = pf_dequant8((s & 1) ? q1 : q0, s >= 2, s >= 2 ? dsB : dsA,
+                                        s >= 2 ? dmB : dmA);
+            const int c = 8 * j + 2 * s + h; // 16-byte chunk of the stage row
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int m = 32 * t + li;
+                const half8 a =
+                    *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// Y[t, n] = sum_k W[n, k] Xh[t, k].  Workgroup tile: 64 tokens x 128 weight
+// rows, 8 waves: wave w owns weight rows n0 + 32 (w & 3) .. +32, both
+// 32-token halves, and half (w >> 2) of every block column (sub-block pairs
+// 2 (w >> 2) and 2 (w >> 2) + 1); the two halves' sums meet in LDS at the
+// end.  Both operands stream through double-buffered LDS stages filled by
+// register double-buffering (block kb + 1 is loaded into registers while
+// block kb is reduced); each lane dequantizes the B operand it feeds the matrix
+// core (one weight row, 8 k per 16-wide step) from the stage into registers,
+// so the weights are dequantized exactly once per workgroup.
+// v_mfma_f32_32x32x16_f16, fp32 accumulation.
+__global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__restrict__ W,
+                                                            const _Float16 *__restrict__ Xh,
+                                                            float *__restrict__ Y, int T, int K,
+                                                            int N, int mtiles, int ntiles)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t As0[PF_A_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t As1[PF_A_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs0[PF_B_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs1[PF_B_STAGE];
+
+    // XCD-aware tile order: consecutive workgroups of one XCD walk the M
+    // tiles of one N band, so the band's weight bytes are shared in its L2.
     const int bid = blockIdx.x;
     const int nxcd = 8;
     const int per_xcd = (mtiles * ntiles + nxcd - 1) / nxcd;
     const int lin = (bid % nxcd) * per_xcd + bid / nxcd;
     if (lin >= mtiles * ntiles)
-        return;
+        return; // whole workgroup
     const int mt = lin % mtiles, nt = lin / mtiles;
     const int m0 = mt * PF_BM, n0 = nt * PF_BN;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rw = wave & 3, kh = wave >> 2;
+    const int h = lane >> 5, li = lane & 31;
     const int nblk = K / 256;
     const size_t row_bytes = (size_t)nblk * 144;
+    const int brow = 32 * rw + li; // this lane's weight row inside the tile
 
     float16v acc[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[i][j] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 
-    for (int kb = 0; kb < nblk; ++kb) {
-        // ---- A tile: 64 x 256 halves, 16-byte pieces (2048 of them)
-#pragma unroll
-        for (int it = 0; it < 8; ++it) {
-            const int p = tid + 256 * it; // piece index
-            const int r = p >> 5, c = (p & 31) * 8;
-            const int t = m0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (t < T)
-                v = *reinterpret_cast<const uint4 *>(Xh + (size_t)t * K + (size_t)kb * 256 + c);
-            *reinterpret_cast<uint4 *>(As + r * PF_LDA + c) = v;
-        }
-        // ---- B tile: 128 rows x one Q4_K block -> fp16; 4 (row, chunk) per thread
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int u = tid + 256 * it;
-            const int r = u >> 3, k = u & 7, j = k >> 1, l0 = 16 * (k & 1);
-            const int n = n0 + r;
-            uint4 h = make_uint4(0, 0, 0, 0), q = make_uint4(0, 0, 0, 0);
-            if (n < N) {
-                const uint8_t *bp = W + (size_t)n * row_bytes + (size_t)kb * 144;
-                h = *reinterpret_cast<const uint4 *>(bp);
-                q = *reinterpret_cast<const uint4 *>(bp + 16 + 16 * k);
-            }
-            const float d = h2f(h.x & 0xffffu), dmin = h2f(h.x >> 16);
-            uint32_t scA, mA, scB, mB;
-            k_scale_min(h.y, h.z, h.w, 2 * j, scA, mA);
-            k_scale_min(h.y, h.z, h.w, 2 * j + 1, scB, mB);
-            const float dA = d * (float)scA, minA = dmin * (float)mA;
-            const float dB = d * (float)scB, minB = dmin * (float)mB;
-            const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-            half8 va[2], vb[2];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t lo = qw[t] & 0x0f0f0f0fu, hi = (qw[t] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    va[t >> 1][4 * (t & 1) + b] = (_Float16)(dA * ubyte_f(lo, b) - minA);
-                    vb[t >> 1][4 * (t & 1) + b] = (_Float16)(dB * ubyte_f(hi, b) - minB);
-                }
-            }
-            _Float16 *row = Bs + r * PF_LDA;
-            *reinterpret_cast<half8 *>(row + 64 * j + l0) = va[0];
-            *reinterpret_cast<half8 *>(row + 64 * j + l0 + 8) = va[1];
-            *reinterpret_cast<half8 *>(row + 64 * j + 32 + l0) = vb[0];
-            *reinterpret_cast<half8 *>(row + 64 * j + 32 + l0 + 8) = vb[1];
-        }
-        __syncthreads();
-        // ---- 16 MFMA K-steps of 16
-        const int li = lane & 31, kh = 8 * (lane >> 5);
-        const _Float16 *bp = Bs + (32 * wave + li) * PF_LDA + kh;
-        const _Float16 *ap0 = As + li * PF_LDA + kh;
-        const _Float16 *ap1 = As + (32 + li) * PF_LDA + kh;
-#pragma unroll 4
-        for (int ks = 0; ks < PF_BK; ks += 16) {
-            const half8 b = *reinterpret_cast<const half8 *>(bp + ks);
-            const half8 a0 = *reinterpret_cast<const half8 *>(ap0 + ks);
-            const half8 a1 = *reinterpret_cast<const half8 *>(ap1 + ks);
-            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc[1], 0, 0, 0);
-        }
-        __syncthreads();
+    PfRegs R;
+    pf_load(Xh, W, m0, n0, T, N, K, row_bytes, 0, tid, R);
+    pf_store(As0, Bs0, tid, R);
+    __syncthreads();
+
+    // two block columns per trip: stage 0 then stage 1
+    for (int kb = 0; kb < nblk; kb += 2) {
+        const bool more1 = kb + 1 < nblk, more2 = kb + 2 < nblk; // workgroup-uniform
+        if (more1)
+            pf_load(Xh, W, m0, n0, T, N, K, row_bytes, kb + 1, tid, R);
+        pf_block(As0, Bs0 + brow * 144, kh, h, li, acc);
+        if (!more1)
+            break;
+        asm volatile("" ::: "memory"); // the stores below stay after the reduction
+        pf_store(As1, Bs1, tid, R);
+        __syncthreads(); // stage 1 holds block kb + 1; stage 0 is free
+        if (more2)
+            pf_load(Xh, W, m0, n0, T, N, K, row_bytes, kb + 2, tid, R);
+        pf_block(As1, Bs1 + brow * 144, kh, h, li, acc);
+        if (!more2)
+            break;
+        asm volatile("" ::: "memory");
+        pf_store(As0, Bs0, tid, R);
+        __syncthreads(); // stage 0 holds block kb + 2; stage 1 is free
     }
-    // ---- store: D[m][n], lane l, reg j: n = l % 32, m = 8*(j/4) + 4*(l/32) + j%4
-    const int n = n0 + 32 * wave + (lane & 31);
-    if (n < N) {
+    __syncthreads(); // every wave is done with the stages
+    // the second half of K hands its sums to the first through LDS (stage 0
+    // of the activations is free now): wave (rw, 1) -> slot rw
+    float *red = reinterpret_cast<float *>(As0);
+    if (kh == 1) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int m = m0 + 32 * i + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+            for (int r = 0; r < 16; ++r)
+                red[((rw * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (kh == 1)
+        return;
+    // store: D[m][n], lane l, reg r: n = l % 32, m = 8*(r/4) + 4*(l/32) + r%4
+    const int nn = n0 + brow;
+    if (nn < N) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float v = acc[t][r] + red[((rw * 2 + t) * 16 + r) * 64 + lane];
                 if (m < T)
-                    Y[(size_t)m * N + n] = acc[i][j];
+                    Y[(size_t)m * N + nn] = v;
             }
     }
 }
@@ -156,7 +285,7 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
                        (_Float16 *)xh, n);
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
     const int per_xcd = (mtiles * ntiles + 7) / 8;
-    hipLaunchKernelGGL(k_prefill_q4k, dim3(per_xcd * 8), dim3(256), 0, s, (const uint8_t *)w,
+    hipLaunchKernelGGL(k_prefill_q4k, dim3(per_xcd * 8), dim3(PF_THREADS), 0, s, (const uint8_t *)w,
                        (const _Float16 *)xh, Y, T, inner, outer, mtiles, ntiles);
     return hipGetLastError();
 }
