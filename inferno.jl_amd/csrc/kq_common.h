@@ -127,4 +127,23 @@ __device__ __forceinline__ float ubyte_f(uint32_t w, int k)
     return (float)((w >> (8 * k)) & 0xffu);
 }
 
+// 6-bit scale and min of sub-blocks 2j and 2j+1 as floats (src/Dequant.jl:345-362),
+// from header dwords s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].
+__device__ __forceinline__ void k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                                 float &scA, float &mA, float &scB, float &mB)
+{
+    const uint32_t sh = 16u * (uint32_t)(j & 1); // bytes 2(j&1), 2(j&1)+1
+    const uint32_t w0 = s0 >> sh, w1 = s1 >> sh, w2 = s2 >> sh;
+    // sub-blocks 0..3: low 6 bits of scales[i] / scales[i+4]
+    const uint32_t sc_lo = w0 & 0x3f3fu, m_lo = w1 & 0x3f3fu;
+    // sub-blocks 4..7: nibbles of scales[i+4], top bits of scales[i-4] / scales[i]
+    const uint32_t sc_hi = (w2 & 0x0f0fu) | ((w0 >> 2) & 0x3030u);
+    const uint32_t m_hi = ((w2 >> 4) & 0x0f0fu) | ((w1 >> 2) & 0x3030u);
+    const uint32_t sc = j >= 2 ? sc_hi : sc_lo, m = j >= 2 ? m_hi : m_lo;
+    scA = ubyte_f(sc, 0);
+    scB = ubyte_f(sc, 1);
+    mA = ubyte_f(m, 0);
+    mB = ubyte_f(m, 1);
+}
+
 } // namespace ihip

@@ -141,51 +141,62 @@ __device__ __forceinline__ half8 pf_dequant8(uint2 bytes, bool high, half2v dsc,
 // operand it feeds the matrix core (one weight row, 8 k per 16-wide step)
 // from the stage into registers, so the weights are dequantized exactly once
 // per workgroup.  v_mfma_f32_32x32x16_f16, fp32 accumulation.
-// Reduce block column kb from one stage (sa: activations, blk: this lane's
-// weight row of the B stage) into the accumulators.
-__device__ __forceinline__ void pf_block(const uint8_t *sa, const uint8_t *blk, int kh, int h,
-                                         int li, float16v (&acc)[2])
+// Reduce sub-block pair j of block column kb from one stage into the
+// accumulators: this lane's B operands are weight rows `blk0` and `blk1`
+// (rows li and li + 32 of the wave's 64), 8 k of every 16-wide step.
+__device__ __forceinline__ void pf_pair(const uint8_t *sa, const uint8_t *blk0,
+                                        const uint8_t *blk1, int j, int h, int li,
+                                        float16v (&acc)[2][2])
 {
-    const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
-    const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+    half2v dsA[2], dmA[2], dsB[2], dmB[2];
+    uint2 q0[2], q1[2];
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        const int j = 2 * kh + jj;
-        uint32_t scA, mA, scB, mB;
-        k_scale_min(hd.y, hd.z, hd.w, 2 * j, scA, mA);
-        k_scale_min(hd.y, hd.z, hd.w, 2 * j + 1, scB, mB);
-        const _Float16 dA = (_Float16)(d * (float)scA), mnA = (_Float16)(-(dmin * (float)mA));
-        const _Float16 dB = (_Float16)(d * (float)scB), mnB = (_Float16)(-(dmin * (float)mB));
-        const half2v dsA = {dA, dA}, dmA = {mnA, mnA}, dsB = {dB, dB}, dmB = {mnB, mnB};
-        const uint2 q0 = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
-        const uint2 q1 = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
-        // four 16-wide K steps: k = 64j + 16s + 8h + (0..7)
+    for (int u = 0; u < 2; ++u) {
+        const uint8_t *blk = u ? blk1 : blk0;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+        const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+        float scA, mA, scB, mB;
+        k_scale_min_pair(hd.y, hd.z, hd.w, j, scA, mA, scB, mB);
+        const _Float16 a = (_Float16)(d * scA), ma = (_Float16)(-(dmin * mA));
+        const _Float16 bb = (_Float16)(d * scB), mb = (_Float16)(-(dmin * mB));
+        dsA[u] = half2v{a, a};
+        dmA[u] = half2v{ma, ma};
+        dsB[u] = half2v{bb, bb};
+        dmB[u] = half2v{mb, mb};
+        q0[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
+        q1[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
+    }
+    // four 16-wide K steps: k = 64j + 16s + 8h + (0..7)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const half8 b = pf_dequant8((s & 1) ? q1 : q0, s >= 2, s >= 2 ? dsB : dsA,
-                                        s >= 2 ? dmB : dmA);
-            const int c = 8 * j + 2 * s + h; // 16-byte chunk of the stage row
+    for (int s = 0; s < 4; ++s) {
+        const int c = 8 * j + 2 * s + h; // 16-byte chunk of the stage row
+        half8 a[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int m = 32 * t + li;
-                const half8 a =
-                    *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
-                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[t], 0, 0, 0);
-            }
+        for (int t = 0; t < 2; ++t) {
+            const int m = 32 * t + li;
+            a[t] = *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const half8 b = pf_dequant8((s & 1) ? q1[u] : q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
+                                        s >= 2 ? dmB[u] : dmA[u]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[t], b, acc[u][t], 0, 0, 0);
         }
     }
 }
 
 // Y[t, n] = sum_k W[n, k] Xh[t, k].  Workgroup tile: 64 tokens x 128 weight
-// rows, 8 waves: wave w owns weight rows n0 + 32 (w & 3) .. +32, both
-// 32-token halves, and half (w >> 2) of every block column (sub-block pairs
-// 2 (w >> 2) and 2 (w >> 2) + 1); the two halves' sums meet in LDS at the
-// end.  Both operands stream through double-buffered LDS stages filled by
-// register double-buffering (block kb + 1 is loaded into registers while
-// block kb is reduced); each lane dequantizes the B operand it feeds the matrix
-// core (one weight row, 8 k per 16-wide step) from the stage into registers,
-// so the weights are dequantized exactly once per workgroup.
-// v_mfma_f32_32x32x16_f16, fp32 accumulation.
+// rows, 8 waves: wave w owns weight rows n0 + 64 (w & 1) .. +64 (two 32-row
+// MFMA tiles), both 32-token halves, and sub-block pair w >> 1 of every block
+// column; the four pairs' sums meet in LDS at the end.  Both operands stream
+// through double-buffered LDS stages filled by register double-buffering
+// (block kb + 1 is loaded into registers while block kb is reduced); each
+// lane dequantizes the B operands it feeds the matrix core (8 k of one
+// weight row per 16-wide step) from the stage into registers, so the weights
+// are dequantized exactly once per workgroup.  v_mfma_f32_32x32x16_f16, fp32
+// accumulation.
 __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__restrict__ W,
                                                             const _Float16 *__restrict__ Xh,
                                                             float *__restrict__ Y, int T, int K,
@@ -209,17 +220,19 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rw = wave & 3, kh = wave >> 2;
+    const int rh = wave & 1, j = wave >> 1;
     const int h = lane >> 5, li = lane & 31;
     const int nblk = K / 256;
     const size_t row_bytes = (size_t)nblk * 144;
-    const int brow = 32 * rw + li; // this lane's weight row inside the tile
+    const int brow = 64 * rh + li; // this lane's first weight row inside the tile
 
-    float16v acc[2];
+    float16v acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[u][t][r] = 0.0f;
 
     PfRegs R;
     pf_load(Xh, W, m0, n0, T, N, K, row_bytes, 0, tid, R);
@@ -231,7 +244,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
         const bool more1 = kb + 1 < nblk, more2 = kb + 2 < nblk; // workgroup-uniform
         if (more1)
             pf_load(Xh, W, m0, n0, T, N, K, row_bytes, kb + 1, tid, R);
-        pf_block(As0, Bs0 + brow * 144, kh, h, li, acc);
+        pf_pair(As0, Bs0 + brow * 144, Bs0 + (brow + 32) * 144, j, h, li, acc);
         if (!more1)
             break;
         asm volatile("" ::: "memory"); // the stores below stay after the reduction
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
         __syncthreads(); // stage 1 holds block kb + 1; stage 0 is free
         if (more2)
             pf_load(Xh, W, m0, n0, T, N, K, row_bytes, kb + 2, tid, R);
-        pf_block(As1, Bs1 + brow * 144, kh, h, li, acc);
+        pf_pair(As1, Bs1 + brow * 144, Bs1 + (brow + 32) * 144, j, h, li, acc);
         if (!more2)
             break;
         asm volatile("" ::: "memory");
@@ -247,28 +260,44 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
         __syncthreads(); // stage 0 holds block kb + 2; stage 1 is free
     }
     __syncthreads(); // every wave is done with the stages
-    // the second half of K hands its sums to the first through LDS (stage 0
-    // of the activations is free now): wave (rw, 1) -> slot rw
-    float *red = reinterpret_cast<float *>(As0);
-    if (kh == 1) {
+    // pairs 1..3 hand their sums to pair 0 through LDS (the stages are free):
+    // 2 x 2 x 16 floats per lane = 16 KB per (pair, row half); pairs 1 and 2
+    // use the two activation stages (32 KB each), pair 3 the two weight
+    // stages (18 KB each)
+    auto slot_of = [&](int pj, int hh) -> float * {
+        if (pj == 1)
+            return reinterpret_cast<float *>(As0) + hh * 4096;
+        if (pj == 2)
+            return reinterpret_cast<float *>(As1) + hh * 4096;
+        return reinterpret_cast<float *>(hh ? Bs1 : Bs0);
+    };
+    if (j != 0) {
+        float *dst = slot_of(j, rh);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                red[((rw * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    dst[((u * 2 + t) * 16 + r) * 64 + lane] = acc[u][t][r];
     }
     __syncthreads();
-    if (kh == 1)
+    if (j != 0)
         return;
     // store: D[m][n], lane l, reg r: n = l % 32, m = 8*(r/4) + 4*(l/32) + r%4
-    const int nn = n0 + brow;
-    if (nn < N) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int nn = n0 + brow + 32 * u;
+        if (nn >= N)
+            continue;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-                const float v = acc[t][r] + red[((rw * 2 + t) * 16 + r) * 64 + lane];
+                const int idx = ((u * 2 + t) * 16 + r) * 64 + lane;
+                const float v = acc[u][t][r] + slot_of(1, rh)[idx] + slot_of(2, rh)[idx] +
+                                slot_of(3, rh)[idx];
                 if (m < T)
                     Y[(size_t)m * N + nn] = v;
             }
