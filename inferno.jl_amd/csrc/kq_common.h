@@ -146,4 +146,24 @@ __device__ __forceinline__ void k_scale_min_pair(uint32_t s0, uint32_t s1, uint3
     mB = ubyte_f(m, 1);
 }
 
+// Wait until at most n of this wave's vector-memory operations are
+// outstanding (n <= 31; expcnt and lgkmcnt are not waited on).
+__device__ __forceinline__ void wait_vmcnt(int n)
+{
+#define IHIP_VM(N)                                                                             \
+    case N:                                                                                    \
+        __builtin_amdgcn_s_waitcnt(((N)&15) | (((N) >> 4) << 14) | 0x0F70);                    \
+        break;
+    switch (n) {
+        IHIP_VM(0) IHIP_VM(1) IHIP_VM(2) IHIP_VM(3) IHIP_VM(4) IHIP_VM(5) IHIP_VM(6) IHIP_VM(7)
+        IHIP_VM(8) IHIP_VM(9) IHIP_VM(10) IHIP_VM(11) IHIP_VM(12) IHIP_VM(13) IHIP_VM(14)
+        IHIP_VM(15) IHIP_VM(16) IHIP_VM(17) IHIP_VM(18) IHIP_VM(19) IHIP_VM(20) IHIP_VM(21)
+        IHIP_VM(22) IHIP_VM(23) IHIP_VM(24) IHIP_VM(25) IHIP_VM(26) IHIP_VM(27) IHIP_VM(28)
+        IHIP_VM(29) IHIP_VM(30) IHIP_VM(31)
+    default:
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+#undef IHIP_VM
+}
+
 } // namespace ihip

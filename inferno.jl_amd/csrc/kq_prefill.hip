@@ -8,101 +8,115 @@
 // type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not) and
 // v_mfma_f32_32x32x16_f16 accumulates in fp32.
 //
-// Tile: 64 tokens x 128 weight rows per workgroup of 4 waves (256 workgroups
-// at 512 x 4096 x 4096); wave w owns weight rows [32w, 32w+32) of the tile
-// and both 32-token halves.  The activations stream through a double-
-// buffered, bank-swizzled LDS stage one Q4_K block column (256 k) ahead;
-// each lane dequantizes the B operand it feeds the matrix core (one weight
-// row, 8 k per 16-wide step) straight into registers from the block bytes,
-// also loaded one block ahead, so the weights are dequantized exactly once
-// per workgroup and never pass through LDS.  Workgroups are mapped so that
-// those of one XCD (blockIdx % 8) share a contiguous band of W rows.
+// Tile: 64 tokens x 128 weight rows per workgroup of 8 waves (256
+// workgroups at 512 x 4096 x 4096).  Both operands of one Q4_K block column
+// (256 k: 32 KB of fp16 activations, 18 KB of weight blocks) stream through
+// a three-slot LDS ring filled by direct-to-LDS 128-bit copies issued two
+// block columns ahead, so two columns' loads are in flight while one is
+// reduced.  Wave (rh, j) reduces weight rows 64 rh .. 64 rh + 63 of the tile
+// over sub-block pair j of every column, dequantizing its matrix-core
+// operand straight from the block bytes into registers (every weight is
+// dequantized once per workgroup).  The weights are the A operand, so each
+// lane ends with 4 consecutive output rows of one token: the four K-quarter
+// partial sums meet in LDS and leave as 16-byte stores.
 #include "kq_common.h"
 #include "kq_launch.h"
 
 namespace ihip {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_BM = 64, PF_BN = 128; // workgroup tile: tokens x weight rows
 
+// fp32 -> fp16 activations, 8 per thread (two 16-byte loads, one 16-byte store).
 __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ X,
                                                   _Float16 *__restrict__ Xh, int64_t n)
 {
-    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (i + 3 < n) {
-        const float4 v = *reinterpret_cast<const float4 *>(X + i);
-        Xh[i] = (_Float16)v.x;
-        Xh[i + 1] = (_Float16)v.y;
-        Xh[i + 2] = (_Float16)v.z;
-        Xh[i + 3] = (_Float16)v.w;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i + 7 < n) {
+        const float4 v0 = *reinterpret_cast<const float4 *>(X + i);
+        const float4 v1 = *reinterpret_cast<const float4 *>(X + i + 4);
+        half8 h;
+        h[0] = (_Float16)v0.x; h[1] = (_Float16)v0.y; h[2] = (_Float16)v0.z; h[3] = (_Float16)v0.w;
+        h[4] = (_Float16)v1.x; h[5] = (_Float16)v1.y; h[6] = (_Float16)v1.z; h[7] = (_Float16)v1.w;
+        *reinterpret_cast<half8 *>(Xh + i) = h;
     } else {
         for (int64_t j = i; j < n; ++j)
             Xh[j] = (_Float16)X[j];
     }
 }
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-// One 64-token x 256-column stage of the fp16 activations in LDS: row m
-// holds 32 chunks of 16 bytes, chunk c at slot c ^ (m & 15), so that the 16
-// lanes of a 128-bit read (same chunk, consecutive rows) hit distinct banks.
+// One ring slot holds block column kb of both operands:
+//  * activations, 64 token rows x 512 bytes: row m holds 32 chunks of 16
+//    bytes, chunk c at slot c ^ (m & 15), so that the 16 lanes of a 128-bit
+//    read (same chunk, consecutive rows) hit distinct banks;
+//  * weights, 128 rows x 144 bytes: the rows' Q4_K blocks of column kb.
 constexpr int PF_ROW_BYTES = 512;
-constexpr int PF_A_STAGE = 64 * PF_ROW_BYTES;   // 32 KB
-constexpr int PF_B_STAGE = PF_BN * 144;          // 18 KB: one Q4_K block of 128 rows
+constexpr int PF_A_STAGE = PF_BM * PF_ROW_BYTES; // 32 KB
+constexpr int PF_B_STAGE = PF_BN * 144;          // 18 KB
+constexpr int PF_SLOT = PF_A_STAGE + PF_B_STAGE; // 50 KB
+constexpr int PF_NSLOT = 3;
 constexpr int PF_THREADS = 512;                  // 8 waves
+constexpr int PF_B_COPIES = PF_B_STAGE / 1024;   // 18 wave copies of 1 KB
 
-// Register double-buffering of one block column: each of the 512 threads
-// loads 4 chunks (16 bytes) of the 64-token activation stage and up to 3 of
-// the 128-row weight stage for block kb + 1 while block kb is reduced, then
-// writes them to the other stage.
-struct PfRegs {
-    uint4 a0, a1, a2, a3, b0, b1, b2; // plain members: the registers must not become an array
+static_assert(PF_B_STAGE % 1024 == 0, "weight stage is whole wave copies");
+static_assert(PF_NSLOT * PF_SLOT <= 160 * 1024, "ring fits the 160 KB of LDS");
+
+// One direct-to-LDS copy: lane l's 16 bytes at `src` land at LDS byte
+// lds + 16 l.  Written as inline assembly so that the compiler, which would
+// otherwise make every later LDS read wait for all copies in flight
+// (including those issued ahead for later block columns), leaves the waits to
+// the explicit per-wave s_waitcnt of the main loop.
+__device__ __forceinline__ void pf_copy16(const void *src, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+
+// Per-lane sources of the copies of block column 0; column kb adds 512 kb
+// bytes (activations) or 144 kb bytes (weights).  Wave w issues activation
+// copies w, w + 8, w + 16, w + 24 (64 chunks each: chunk q = stage row q / 32,
+// activation chunk (q % 32) ^ (row & 15)) and weight copies w, w + 8 and, for
+// w < 2, w + 16 (chunk q = tile row q / 9, 16-byte piece q % 9): 7 copies for
+// waves 0-1, 6 for the others.  Rows past T (tokens) or N (weights) re-read
+// the last row.
+struct PfSrc {
+    const uint8_t *a0, *a1, *a2, *a3, *b0, *b1, *b2; // plain members: kept in registers
 };
 
-__device__ __forceinline__ uint4 pf_load_a(const _Float16 *__restrict__ Xh, int m0, int T, int K,
-                                           int kb, int q)
+__device__ __forceinline__ const uint8_t *pf_src_a(const _Float16 *Xh, int m0, int T, int K,
+                                                   int w, int lane, int k)
 {
-    const int rp = q >> 5, slot = q & 31; // stage row q/32, slot q%32
-    const int c = slot ^ (rp & 15);       // the activation chunk that lives in this slot
-    const int row = min(m0 + rp, T - 1);  // rows past T re-read row T-1
-    return *reinterpret_cast<const uint4 *>(Xh + (size_t)row * K + (size_t)kb * 256 + 8 * c);
+    const int q = (8 * k + w) * 64 + lane;
+    const int rp = q >> 5, c = (q & 31) ^ (rp & 15);
+    return reinterpret_cast<const uint8_t *>(Xh + (size_t)min(m0 + rp, T - 1) * K + 8 * c);
 }
 
-__device__ __forceinline__ uint4 pf_load_b(const uint8_t *__restrict__ W, int n0, int N,
-                                           size_t row_bytes, int kb, int q)
+__device__ __forceinline__ const uint8_t *pf_src_b(const uint8_t *W, int n0, int N,
+                                                   size_t row_bytes, int lane, int i)
 {
-    // chunk q of the 128 x 144-byte weight stage (q < 1152; callers clamp)
-    const int row = q / 9, piece = q - 9 * (q / 9);
-    return *reinterpret_cast<const uint4 *>(W + (size_t)min(n0 + row, N - 1) * row_bytes +
-                                            (size_t)kb * 144 + 16 * piece);
+    const int q = 64 * min(i, PF_B_COPIES - 1) + lane;
+    const int row = q / 9, piece = q - 9 * row;
+    return W + (size_t)min(n0 + row, N - 1) * row_bytes + 16 * piece;
 }
 
-__device__ __forceinline__ void pf_load(const _Float16 *__restrict__ Xh,
-                                        const uint8_t *__restrict__ W, int m0, int n0, int T,
-                                        int N, int K, size_t row_bytes, int kb, int tid, PfRegs &R)
+// Issue this wave's copies of block column kb into the ring slot at LDS
+// address `slot`.
+__device__ __forceinline__ void pf_issue(const PfSrc &S, int kb, int w, uint32_t slot)
 {
-    R.a0 = pf_load_a(Xh, m0, T, K, kb, tid);
-    R.a1 = pf_load_a(Xh, m0, T, K, kb, tid + PF_THREADS);
-    R.a2 = pf_load_a(Xh, m0, T, K, kb, tid + 2 * PF_THREADS);
-    R.a3 = pf_load_a(Xh, m0, T, K, kb, tid + 3 * PF_THREADS);
-    R.b0 = pf_load_b(W, n0, N, row_bytes, kb, tid);
-    R.b1 = pf_load_b(W, n0, N, row_bytes, kb, tid + PF_THREADS);
-    // the third round covers chunks 1024..1151: threads past it re-load chunk 1151
-    R.b2 = pf_load_b(W, n0, N, row_bytes, kb, min(tid + 2 * PF_THREADS, PF_BN * 9 - 1));
-}
-
-__device__ __forceinline__ void pf_store(uint8_t *sa, uint8_t *sb, int tid, const PfRegs &R)
-{
-    *reinterpret_cast<uint4 *>(sa + 16 * tid) = R.a0;
-    *reinterpret_cast<uint4 *>(sa + 16 * (tid + PF_THREADS)) = R.a1;
-    *reinterpret_cast<uint4 *>(sa + 16 * (tid + 2 * PF_THREADS)) = R.a2;
-    *reinterpret_cast<uint4 *>(sa + 16 * (tid + 3 * PF_THREADS)) = R.a3;
-    *reinterpret_cast<uint4 *>(sb + 16 * tid) = R.b0;
-    *reinterpret_cast<uint4 *>(sb + 16 * (tid + PF_THREADS)) = R.b1;
-    if (tid + 2 * PF_THREADS < PF_BN * 9)
-        *reinterpret_cast<uint4 *>(sb + 16 * (tid + 2 * PF_THREADS)) = R.b2;
+    const size_t ao = (size_t)kb * 512, bo = (size_t)kb * 144;
+    pf_copy16(S.a0 + ao, slot + 1024 * w);
+    pf_copy16(S.a1 + ao, slot + 1024 * (w + 8));
+    pf_copy16(S.a2 + ao, slot + 1024 * (w + 16));
+    pf_copy16(S.a3 + ao, slot + 1024 * (w + 24));
+    pf_copy16(S.b0 + bo, slot + PF_A_STAGE + 1024 * w);
+    pf_copy16(S.b1 + bo, slot + PF_A_STAGE + 1024 * (w + 8));
+    if (w + 16 < PF_B_COPIES) // wave-uniform
+        pf_copy16(S.b2 + bo, slot + PF_A_STAGE + 1024 * (w + 16));
 }
 
 // 8 nibbles (the low or high nibble of 8 bytes) -> 8 fp16 weights
@@ -132,80 +146,84 @@ __device__ __forceinline__ half8 pf_dequant8(uint2 bytes, bool high, half2v dsc,
     return r;
 }
 
-// Y[t, n] = sum_k W[n, k] Xh[t, k].  Workgroup tile: 64 tokens x 128 weight
-// rows, 8 waves: wave w owns weight rows n0 + 32 (w & 3) .. +32, both
-// 32-token halves, and half (w >> 2) of every block column (sub-block pairs
-// 2 (w >> 2) and 2 (w >> 2) + 1); the two halves' sums meet in LDS at the
-// end.  Both operands stream through double-buffered LDS stages filled by
-// direct-to-LDS loads one block column ahead; each lane dequantizes the B
-// operand it feeds the matrix core (one weight row, 8 k per 16-wide step)
-// from the stage into registers, so the weights are dequantized exactly once
-// per workgroup.  v_mfma_f32_32x32x16_f16, fp32 accumulation.
-// Reduce sub-block pair j of block column kb from one stage into the
-// accumulators: this lane's B operands are weight rows `blk0` and `blk1`
-// (rows li and li + 32 of the wave's 64), 8 k of every 16-wide step.
+// Reduce sub-block pair j of one ring slot into the accumulators.  This
+// lane's A operands are weight rows `blk0` and `blk1` (rows li and li + 32 of
+// the wave's 64), 8 k of every 16-wide step; its B operands are tokens li
+// and li + 32.  acc[u][t] is the 32 x 32 tile (weight rows 32u.., tokens
+// 32t..): lane l, register r hold token 32t + l % 32, weight row
+// 32u + 8 (r / 4) + 4 (l / 32) + r % 4.
 __device__ __forceinline__ void pf_pair(const uint8_t *sa, const uint8_t *blk0,
                                         const uint8_t *blk1, int j, int h, int li,
                                         float16v (&acc)[2][2])
 {
-    half2v dsA[2], dmA[2], dsB[2], dmB[2];
+    // every LDS read of the column first (one wait instead of one per step)
+    uint4 hd[2];
     uint2 q0[2], q1[2];
+    half8 x[4][2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const uint8_t *blk = u ? blk1 : blk0;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
-        const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+        hd[u] = *reinterpret_cast<const uint4 *>(blk);
+        q0[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
+        q1[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
+    }
+    // four 16-wide K steps: k = 64j + 16s + 8h + (0..7), 16-byte chunk 8j + 2s + h
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int m = 32 * t + li, c = 8 * j + 2 * s + h;
+            x[s][t] = *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    half2v dsA[2], dmA[2], dsB[2], dmB[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float d = h2f(hd[u].x & 0xffffu), dmin = h2f(hd[u].x >> 16);
         float scA, mA, scB, mB;
-        k_scale_min_pair(hd.y, hd.z, hd.w, j, scA, mA, scB, mB);
+        k_scale_min_pair(hd[u].y, hd[u].z, hd[u].w, j, scA, mA, scB, mB);
         const _Float16 a = (_Float16)(d * scA), ma = (_Float16)(-(dmin * mA));
         const _Float16 bb = (_Float16)(d * scB), mb = (_Float16)(-(dmin * mB));
         dsA[u] = half2v{a, a};
         dmA[u] = half2v{ma, ma};
         dsB[u] = half2v{bb, bb};
         dmB[u] = half2v{mb, mb};
-        q0[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
-        q1[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
     }
-    // four 16-wide K steps: k = 64j + 16s + 8h + (0..7)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int c = 8 * j + 2 * s + h; // 16-byte chunk of the stage row
-        half8 a[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int m = 32 * t + li;
-            a[t] = *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
-        }
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const half8 b = pf_dequant8((s & 1) ? q1[u] : q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
-                                        s >= 2 ? dmB[u] : dmA[u]);
+            const half8 wq = pf_dequant8((s & 1) ? q1[u] : q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
+                                         s >= 2 ? dmB[u] : dmA[u]);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-                acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[t], b, acc[u][t], 0, 0, 0);
+                acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, x[s][t], acc[u][t], 0, 0, 0);
         }
-    }
 }
 
-// Y[t, n] = sum_k W[n, k] Xh[t, k].  Workgroup tile: 64 tokens x 128 weight
-// rows, 8 waves: wave w owns weight rows n0 + 64 (w & 1) .. +64 (two 32-row
-// MFMA tiles), both 32-token halves, and sub-block pair w >> 1 of every block
-// column; the four pairs' sums meet in LDS at the end.  Both operands stream
-// through double-buffered LDS stages filled by register double-buffering
-// (block kb + 1 is loaded into registers while block kb is reduced); each
-// lane dequantizes the B operands it feeds the matrix core (8 k of one
-// weight row per 16-wide step) from the stage into registers, so the weights
-// are dequantized exactly once per workgroup.  v_mfma_f32_32x32x16_f16, fp32
-// accumulation.
+// Wait for this wave's copies: n is 0 or one column's copy count (6 or 7).
+static_assert(PF_B_COPIES == 18, "copy counts 7 (waves 0-1) and 6");
+__device__ __forceinline__ void pf_wait_copies(int n)
+{
+    if (n == 7)
+        __builtin_amdgcn_s_waitcnt(7 | 0x0F70); // vmcnt(7)
+    else if (n == 6)
+        __builtin_amdgcn_s_waitcnt(6 | 0x0F70); // vmcnt(6)
+    else
+        __builtin_amdgcn_s_waitcnt(0 | 0x0F70); // vmcnt(0)
+}
+
+// Y[t, n] = sum_k W[n, k] Xh[t, k] for one 64-token x 128-row tile.  Wave
+// (rh, j) = (wave & 1, wave >> 1) accumulates weight rows 64 rh .. +63 over
+// sub-block pair j of every block column; at the end wave (rh, j) finishes
+// tile combination c = j (weight half u = c >> 1, token half t = c & 1) of
+// its row half from the four waves' partial sums.
 __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__restrict__ W,
                                                             const _Float16 *__restrict__ Xh,
                                                             float *__restrict__ Y, int T, int K,
                                                             int N, int mtiles, int ntiles)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t As0[PF_A_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t As1[PF_A_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs0[PF_B_STAGE];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs1[PF_B_STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t ring[PF_NSLOT * PF_SLOT];
 
     // XCD-aware tile order: consecutive workgroups of one XCD walk the M
     // tiles of one N band, so the band's weight bytes are shared in its L2.
@@ -224,7 +242,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     const int h = lane >> 5, li = lane & 31;
     const int nblk = K / 256;
     const size_t row_bytes = (size_t)nblk * 144;
-    const int brow = 64 * rh + li; // this lane's first weight row inside the tile
+    const int brow = 64 * rh + li;                        // this lane's first weight row
+    const int copies = 4 + (PF_B_COPIES - wave + 7) / 8; // copies this wave issues per column
 
     float16v acc[2][2];
 #pragma unroll
@@ -234,73 +253,95 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[u][t][r] = 0.0f;
 
-    PfRegs R;
-    pf_load(Xh, W, m0, n0, T, N, K, row_bytes, 0, tid, R);
-    pf_store(As0, Bs0, tid, R);
-    __syncthreads();
+    PfSrc S;
+    S.a0 = pf_src_a(Xh, m0, T, K, wave, lane, 0);
+    S.a1 = pf_src_a(Xh, m0, T, K, wave, lane, 1);
+    S.a2 = pf_src_a(Xh, m0, T, K, wave, lane, 2);
+    S.a3 = pf_src_a(Xh, m0, T, K, wave, lane, 3);
+    S.b0 = pf_src_b(W, n0, N, row_bytes, lane, wave);
+    S.b1 = pf_src_b(W, n0, N, row_bytes, lane, wave + 8);
+    S.b2 = pf_src_b(W, n0, N, row_bytes, lane, wave + 16);
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
 
-    // two block columns per trip: stage 0 then stage 1
-    for (int kb = 0; kb < nblk; kb += 2) {
-        const bool more1 = kb + 1 < nblk, more2 = kb + 2 < nblk; // workgroup-uniform
-        if (more1)
-            pf_load(Xh, W, m0, n0, T, N, K, row_bytes, kb + 1, tid, R);
-        pf_pair(As0, Bs0 + brow * 144, Bs0 + (brow + 32) * 144, j, h, li, acc);
-        if (!more1)
-            break;
-        asm volatile("" ::: "memory"); // the stores below stay after the reduction
-        pf_store(As1, Bs1, tid, R);
-        __syncthreads(); // stage 1 holds block kb + 1; stage 0 is free
-        if (more2)
-            pf_load(Xh, W, m0, n0, T, N, K, row_bytes, kb + 2, tid, R);
-        pf_pair(As1, Bs1 + brow * 144, Bs1 + (brow + 32) * 144, j, h, li, acc);
-        if (!more2)
-            break;
-        asm volatile("" ::: "memory");
-        pf_store(As0, Bs0, tid, R);
-        __syncthreads(); // stage 0 holds block kb + 2; stage 1 is free
+    pf_issue(S, 0, wave, ring_lds);
+    if (nblk > 1)
+        pf_issue(S, 1, wave, ring_lds + PF_SLOT);
+    int cur = 0; // slot of column kb
+    for (int kb = 0; kb < nblk; ++kb) {
+        // this wave's copies of column kb have landed (those of kb + 1 may
+        // still be in flight); after the barrier every wave's have, and every
+        // wave is done reading column kb - 1, whose slot takes kb + 2
+        pf_wait_copies(kb + 1 < nblk ? copies : 0);
+        lds_barrier();
+        if (kb + 2 < nblk) {
+            const int nxt = cur == 0 ? 2 : cur - 1; // (kb + 2) % 3
+            pf_issue(S, kb + 2, wave, ring_lds + nxt * PF_SLOT);
+        }
+        const uint8_t *sl = ring + cur * PF_SLOT;
+        pf_pair(sl, sl + PF_A_STAGE + brow * 144, sl + PF_A_STAGE + (brow + 32) * 144, j, h, li,
+                acc);
+        cur = cur == 2 ? 0 : cur + 1;
     }
-    __syncthreads(); // every wave is done with the stages
-    // pairs 1..3 hand their sums to pair 0 through LDS (the stages are free):
-    // 2 x 2 x 16 floats per lane = 16 KB per (pair, row half); pairs 1 and 2
-    // use the two activation stages (32 KB each), pair 3 the two weight
-    // stages (18 KB each)
-    auto slot_of = [&](int pj, int hh) -> float * {
-        if (pj == 1)
-            return reinterpret_cast<float *>(As0) + hh * 4096;
-        if (pj == 2)
-            return reinterpret_cast<float *>(As1) + hh * 4096;
-        return reinterpret_cast<float *>(hh ? Bs1 : Bs0);
-    };
-    if (j != 0) {
-        float *dst = slot_of(j, rh);
+    __syncthreads(); // every wave is done with the ring
+
+    // partial sums in LDS: float4 P[rh][c][src][q][lane] (128 KB), where
+    // q = r / 4 picks 4 consecutive weight rows of one token
+    float4 *P = reinterpret_cast<float4 *>(ring);
+    auto pidx = [&](int c, int src, int q) { return (((rh * 4 + c) * 4 + src) * 4 + q) * 64 + lane; };
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+    for (int c = 0; c < 4; ++c) {
+        if (c == j)
+            continue; // wave-uniform
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    dst[((u * 2 + t) * 16 + r) * 64 + lane] = acc[u][t][r];
+        for (int q = 0; q < 4; ++q) {
+            const float16v &a = acc[c >> 1][c & 1];
+            P[pidx(c, j, q)] = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+        }
     }
     __syncthreads();
-    if (j != 0)
-        return;
-    // store: D[m][n], lane l, reg r: n = l % 32, m = 8*(r/4) + 4*(l/32) + r%4
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int nn = n0 + brow + 32 * u;
-        if (nn >= N)
-            continue;
+    for (int c = 0; c < 4; ++c) {
+        if (c != j)
+            continue; // wave-uniform: this wave finishes combination c
+        const int u = c >> 1, t = c & 1;
+        float4 v[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int q = 0; q < 4; ++q)
+            v[q] = make_float4(acc[u][t][4 * q], acc[u][t][4 * q + 1], acc[u][t][4 * q + 2],
+                               acc[u][t][4 * q + 3]);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-                const int idx = ((u * 2 + t) * 16 + r) * 64 + lane;
-                const float v = acc[u][t][r] + slot_of(1, rh)[idx] + slot_of(2, rh)[idx] +
-                                slot_of(3, rh)[idx];
-                if (m < T)
-                    Y[(size_t)m * N + nn] = v;
+        for (int src = 0; src < 4; ++src) {
+            if (src == j)
+                continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 p = P[pidx(c, src, q)];
+                v[q].x += p.x;
+                v[q].y += p.y;
+                v[q].z += p.z;
+                v[q].w += p.w;
             }
+        }
+        const int m = m0 + 32 * t + li;
+        if (m >= T)
+            break;
+        const int nb = n0 + 64 * rh + 32 * u + 4 * h; // + 8 q: 4 consecutive rows
+        float *yrow = Y + (size_t)m * N;
+        if ((N & 3) == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (nb + 8 * q < N)
+                    *reinterpret_cast<float4 *>(yrow + nb + 8 * q) = v[q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = nb + 8 * q;
+                if (n < N) yrow[n] = v[q].x;
+                if (n + 1 < N) yrow[n + 1] = v[q].y;
+                if (n + 2 < N) yrow[n + 2] = v[q].z;
+                if (n + 3 < N) yrow[n + 3] = v[q].w;
+            }
+        }
     }
 }
 
@@ -310,7 +351,7 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
                               int inner, int outer, hipStream_t s)
 {
     const int64_t n = (int64_t)T * inner;
-    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n / 4 + 255) / 256 + 1)), dim3(256), 0, s, X,
+    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n / 8 + 255) / 256 + 1)), dim3(256), 0, s, X,
                        (_Float16 *)xh, n);
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
     const int per_xcd = (mtiles * ntiles + 7) / 8;
