@@ -142,7 +142,7 @@ int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *
 /* Workspace for the argmax entry points: IHIP_ARGMAX_WS_BYTES of device
  * memory (per-workgroup partial maxima; no initialisation needed).  Calls
  * that share a workspace must not overlap on the GPU. */
-#define IHIP_ARGMAX_WS_BYTES 65536
+#define IHIP_ARGMAX_WS_BYTES 262144
 /* GEMV + fused greedy argmax.  logits may be NULL.  *token and *flags are
  * device int32s (flags: IHIP_FLAG_* bits; the token is meaningless when
  * NAN or POSINF is set). */

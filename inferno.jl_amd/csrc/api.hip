@@ -280,7 +280,7 @@ int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, i
     RET_IF(check_shape(type, hidden, vocab));
     if (!w || !x || !token || !flags || !ws)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    if ((type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden)) {
+    if ((type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden) && lm_head_fusable(vocab)) {
         hipError_t e = launch_lm_head_argmax(type, w, x, logits, token, flags, hidden, vocab, ws, s);
         if (e != hipSuccess)
             return fail(IHIP_ERR_HIP, "lm_head launch failed: %s", hipGetErrorString(e));

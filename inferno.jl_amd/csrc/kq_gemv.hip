@@ -27,6 +27,7 @@
 //     each workgroup writes one (value, index) partial to its own slot and a
 //     one-workgroup kernel reduces the partials, so no two workgroups touch
 //     the same address.
+#include "inferno_hip.h"
 #include "kq_common.h"
 #include "kq_launch.h"
 
@@ -425,7 +426,8 @@ struct ArgPart {
     uint32_t pad;
 };
 static_assert(sizeof(ArgPart) == 16, "ArgPart layout");
-constexpr int kArgMaxParts = 4096;
+constexpr int kArgMaxParts = 16384; // IHIP_ARGMAX_WS_BYTES / sizeof(ArgPart)
+static_assert(kArgMaxParts * sizeof(ArgPart) == IHIP_ARGMAX_WS_BYTES, "argmax workspace size");
 
 __device__ __forceinline__ uint32_t ordered_bits(float v)
 {
@@ -492,18 +494,28 @@ __device__ __forceinline__ void argmax_store_partial(unsigned long long key, uin
 }
 
 // Reduce `nparts` partials; writes the 0-based token and the IHIP_FLAG_* bits.
-__global__ __launch_bounds__(256) void k_argmax_finalize(const ArgPart *__restrict__ parts,
-                                                         int nparts, int32_t *token,
-                                                         uint32_t *flags_out)
+__global__ __launch_bounds__(1024) void k_argmax_finalize(const ArgPart *__restrict__ parts,
+                                                          int nparts, int32_t *token,
+                                                          uint32_t *flags_out)
 {
-    __shared__ unsigned long long wkey[4];
-    __shared__ uint32_t wflag[4];
+    __shared__ unsigned long long wkey[16];
+    __shared__ uint32_t wflag[16];
     unsigned long long key = 0;
     uint32_t fl = 0;
-    for (int i = threadIdx.x; i < nparts; i += 256) {
-        const unsigned long long k = parts[i].key;
-        key = k > key ? k : key;
-        fl |= parts[i].flags;
+    // four 16-byte partials in flight per thread
+    for (int i0 = threadIdx.x; i0 < nparts; i0 += 4 * 1024) {
+        uint4 p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + 1024 * u;
+            p[u] = i < nparts ? reinterpret_cast<const uint4 *>(parts)[i] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const unsigned long long k = ((unsigned long long)p[u].y << 32) | p[u].x;
+            key = k > key ? k : key;
+            fl |= p[u].z;
+        }
     }
     argmax_wave_reduce(key, fl);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -515,7 +527,7 @@ __global__ __launch_bounds__(256) void k_argmax_finalize(const ArgPart *__restri
     if (threadIdx.x == 0) {
         unsigned long long k = wkey[0];
         uint32_t f = wflag[0];
-        for (int w = 1; w < 4; ++w) {
+        for (int w = 1; w < 16; ++w) {
             k = wkey[w] > k ? wkey[w] : k;
             f |= wflag[w];
         }
@@ -674,7 +686,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
 // Rows per wave of the wide kernels and rows per chunk of the streamed
 // kernels; 0 = the measured default.
 static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 4 / 2)
-static int g_rows_gateup = 0; // fused gate/up (default 2)
+static int g_rows_gateup = 0; // fused gate/up (default 1)
 static int g_stream_rows = 0; // Q6_K/Q8_0 rows per chunk (default: see stream_rows())
 
 void set_tuning(const char *name, int value)
@@ -690,8 +702,8 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
 {
     const int nblk = inner / 256;
     int R = GATEUP ? g_rows_gateup : g_rows_wide;
-    if (R <= 0)
-        R = (GATEUP || FMT == kQ5_K) ? 2 : 4;
+    if (R <= 0) // measured on MI355X: 4096 x 4096 GEMV and 2 x 12288 x 4096 gate/up
+        R = GATEUP ? 1 : FMT == kQ5_K ? 2 : 4;
     if (FMT == kQ5_K && GATEUP && R > 2)
         R = 2; // register budget
 #define IHIP_KW(RR)                                                                          \
@@ -713,24 +725,25 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
 // Waves per workgroup of the streamed kernel: one per K segment, at most 8.
 static int stream_waves(int nseg) { return nseg >= 8 ? 8 : nseg >= 6 ? 6 : nseg >= 4 ? 4 : nseg; }
 
-// Rows per chunk: enough chunks for about four workgroups per CU (two when
-// a workgroup has four or more waves), within 4..32 (measured on MI355X:
-// longer chunks serialize too many rows per wave).
-static int stream_rows(int outer, int nw)
+// Rows per chunk: outer / 1024 within 4..16 (at least four workgroups per
+// CU; measured on MI355X at 4096 x 4096 Q8_0, 4096 x 12288 Q6_K and
+// 151936 x 2048 Q6_K).  With the fused argmax every chunk leaves one partial,
+// so the chunk count is kept within kArgMaxParts.
+static int stream_rows(int outer, bool argmax)
 {
-    if (g_stream_rows > 0)
-        return min(g_stream_rows, kStreamMaxRows);
-    const int target_wgs = 256 * (nw >= 4 ? 2 : 4);
-    int r = (outer + target_wgs - 1) / target_wgs;
-    r = r < 4 ? 4 : r > 32 ? 32 : r;
+    int r;
+    if (g_stream_rows > 0) {
+        r = min(g_stream_rows, kStreamMaxRows);
+    } else {
+        r = outer / 1024;
+        r = r < 4 ? 4 : r > 16 ? 16 : r;
+    }
+    if (argmax)
+        r = max(r, (outer + kArgMaxParts - 1) / kArgMaxParts);
     return r;
 }
 
-static int stream_grid(int outer, int rpc, bool argmax)
-{
-    const int nchunks = (outer + rpc - 1) / rpc;
-    return argmax ? min(nchunks, min(kArgMaxParts, 2048)) : nchunks;
-}
+static int stream_grid(int outer, int rpc) { return (outer + rpc - 1) / rpc; }
 
 template <int FMT, bool ARGMAX>
 static hipError_t launch_stream(const void *w, const float *x, float *y, int inner, int outer,
@@ -739,10 +752,10 @@ static hipError_t launch_stream(const void *w, const float *x, float *y, int inn
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int nw = stream_waves(nseg);
-    const int rpc = stream_rows(outer, nw);
-    const int grid = stream_grid(outer, rpc, ARGMAX);
+    const int rpc = stream_rows(outer, ARGMAX);
+    const int grid = stream_grid(outer, rpc);
 #define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts);         return hipGetLastError();                                                                }
-    IHIP_ST(1, 8) IHIP_ST(2, 8) IHIP_ST(3, 6) IHIP_ST(4, 4) IHIP_ST(6, 4) IHIP_ST(8, 4)
+    IHIP_ST(1, 2) IHIP_ST(2, 2) IHIP_ST(3, 2) IHIP_ST(4, 2) IHIP_ST(6, 2) IHIP_ST(8, 2)
 #undef IHIP_ST
     return hipErrorInvalidValue;
 }
@@ -774,10 +787,14 @@ hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const
     }
 }
 
+bool lm_head_fusable(int vocab) { return stream_rows(vocab, true) <= kStreamMaxRows; }
+
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s)
 {
+    if (!lm_head_fusable(vocab))
+        return hipErrorInvalidValue;
     hipError_t e;
     switch (type) {
     case kQ6_K: e = launch_stream<kQ6_K, true>(w, x, logits, hidden, vocab, ws, s); break;
@@ -786,10 +803,8 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
     }
     if (e != hipSuccess)
         return e;
-    const int nblk = hidden / block_elems(type);
-    const int nseg = (nblk + (type == kQ6_K ? 8 : 64) - 1) / (type == kQ6_K ? 8 : 64);
-    const int nparts = stream_grid(vocab, stream_rows(vocab, stream_waves(nseg)), true);
-    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws, nparts,
+    const int nparts = stream_grid(vocab, stream_rows(vocab, true));
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(1024), 0, s, (const ArgPart *)ws, nparts,
                        token, flags);
     return hipGetLastError();
 }
@@ -802,7 +817,7 @@ hipError_t launch_argmax(const float *v, int64_t n, int32_t *token, uint32_t *fl
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(k_argmax_partials, dim3((unsigned)blocks), dim3(256), 0, s, v, n,
                        (ArgPart *)ws);
-    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws,
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(1024), 0, s, (const ArgPart *)ws,
                        (int)blocks, token, flags);
     return hipGetLastError();
 }

@@ -12,6 +12,8 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
 bool gate_up_fusable(int gate_type, int up_type);
 hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,
                                  float *h, int hidden, int inter, hipStream_t s);
+// The fused lm_head argmax handles vocab <= 16384 chunks of at most 64 rows.
+bool lm_head_fusable(int vocab);
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s);

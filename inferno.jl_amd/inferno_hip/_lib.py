@@ -29,7 +29,7 @@ IHIP_ERR_EMPTY = -7
 
 Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 FLAG_NAN, FLAG_POSINF, FLAG_ALL_NEGINF = 1, 2, 4
-ARGMAX_WS_BYTES = 65536
+ARGMAX_WS_BYTES = 262144
 
 
 class LibraryNotBuilt(RuntimeError):
