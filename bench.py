@@ -253,6 +253,30 @@ def q8_0_workloads(torch, stream, synth, D):
                 gemv_us=gemv_us, gemv_gbs=gemv_bytes / (gemv_us * 1e-6) / 1e9)
 
 
+def q8k_gemv(torch, stream, synth, D):
+    """The int8-activation variant (the reference C numerics) at 4096x4096
+    Q4_K: one step = quantize x to Q8_K + the GEMV, weights rotated through HBM."""
+    outer = inner = 4096
+    rng = synth.rng_for(0xC0)
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    x = synth.activations(rng, inner)
+    nbytes = w.size + 4 * inner + 4 * outer
+    ncopy = copies_for(w.size)
+    base = torch.from_numpy(w).cuda()
+    ws = [D.DeviceWeight(base.clone(), synth.Q4_K, inner, outer) for _ in range(ncopy)]
+    xd = torch.from_numpy(x).cuda()
+    q8 = torch.empty(inner // 256 * 292, dtype=torch.uint8, device="cuda")
+    ys = torch.empty(ncopy, outer, device="cuda")
+
+    def step(i):
+        D.quantize_row_q8k(xd, q8)
+        D.gemv_q8k(ws[i % ncopy], q8, ys[i % ncopy])
+    n = 16 * ncopy
+    ms = time_steps(torch, stream, step, ncopy, n, 2 * ncopy)
+    us = ms * 1e3 / n
+    return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9)
+
+
 def lm_head(torch, stream, synth, D):
     vocab, hidden = 151936, 2048
     rng = synth.rng_for(0xC2)
@@ -382,6 +406,10 @@ def main():
         q = q8_0_workloads(torch, stream, synth, D)
         log(f"  dequant {q['dequant_us']:.2f} us ({q['dequant_gbs']:.0f} GB/s), gemv {q['gemv_us']:.2f} us ({q['gemv_gbs']:.0f} GB/s)")
         extras.update({f"q8_0_{k}": v for k, v in q.items()})
+        log("Q4_K GEMV 4096x4096, int8-activation variant (quantize + GEMV)")
+        k8 = q8k_gemv(torch, stream, synth, D)
+        log(f"  {k8['us']:.2f} us, {k8['gbs']:.0f} GB/s")
+        extras.update(q4k_gemv_q8k_us=k8["us"], q4k_gemv_q8k_gbs=k8["gbs"])
         log("Q6_K lm_head 151936x2048 + argmax")
         lm = lm_head(torch, stream, synth, D)
         log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s")

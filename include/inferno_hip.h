@@ -106,6 +106,32 @@ int ihip_q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_b
 int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
                    int outer_dim);
 
+/* ---- int8-activation variant: the reference C numerics, bit for bit ---- */
+/* Q8_K block: float d, int8 qs[256], int16 bsums[16] (292 bytes,
+ * block_q8_K, quant_kernels.c:51-56). */
+#define IHIP_Q8_K_BYTES 292
+/* quantize_row_q8_K(x, y, k) (quant_kernels.c:166-194): k % 256 == 0, y gets
+ * k/256 Q8_K blocks.  Replaces the binding of quantize_q8_k!
+ * (src/QuantizedKernels.jl:151-156), whose ccall passes (y, x, Cint): here
+ * the arguments are in the C order. */
+int ihip_quantize_row_q8_k(const float *x, void *y, int64_t k);
+/* vec_dot_q{4,5,6}_K_q8_K(x, y, nb) (quant_kernels.c:204, 311, 440), bound
+ * by vec_dot_q{4,5,6}_k_q8_k (src/QuantizedKernels.jl:159-178): one weight
+ * row of nb blocks against nb Q8_K blocks; the float result goes to *s. */
+int ihip_vec_dot_q4_k_q8_k(const void *x, const void *y, int nb, float *s);
+int ihip_vec_dot_q5_k_q8_k(const void *x, const void *y, int nb, float *s);
+int ihip_vec_dot_q6_k_q8_k(const void *x, const void *y, int nb, float *s);
+/* q{4,5,6}_k_gemv with the reference C numerics (quant_kernels.c:602-650:
+ * x re-quantized to Q8_K, integer dots): the same arguments as
+ * ihip_q{4,5,6}_k_gemv; when q8_buf is not NULL it receives the Q8_K blocks
+ * of x (inner/256 * IHIP_Q8_K_BYTES), as the reference's scratch does. */
+int ihip_q4_k_gemv_q8k(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+                       int inner_dim, int outer_dim);
+int ihip_q5_k_gemv_q8k(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+                       int inner_dim, int outer_dim);
+int ihip_q6_k_gemv_q8k(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+                       int inner_dim, int outer_dim);
+
 /* ---- Dequant (src/Dequant.jl:304-601): bit-exact blocks -> fp32 -------- */
 /* n = number of elements; src holds n/256 (or n/32) blocks. */
 int ihip_dequantize(int ggml_type, const uint8_t *src, float *dst, int64_t n);
@@ -161,6 +187,13 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
  * of T*inner fp16 values (2 bytes each) for the rounded activations. */
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
+
+/* Device twins of the int8-activation variant.  x: 4-byte aligned fp32,
+ * y / q8: 4-byte aligned Q8_K blocks; w: 16-byte aligned (Q4_K, Q5_K) or
+ * 2-byte aligned (Q6_K). */
+int ihip_quantize_row_q8_k_dev(const float *x, void *y, int64_t k, ihip_stream stream);
+int ihip_gemv_q8k_dev(int ggml_type, const void *w, const void *q8, float *out, int inner,
+                      int outer, ihip_stream stream);
 
 #ifdef __cplusplus
 }

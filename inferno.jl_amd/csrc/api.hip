@@ -323,6 +323,60 @@ int host_gemv(int type, const uint8_t *w, const float *x, float *out, int inner,
     return IHIP_OK;
 }
 
+bool q8k_type(int t) { return t == kQ4_K || t == kQ5_K || t == kQ6_K; }
+
+size_t q8k_bytes(int64_t k) { return (size_t)(k / 256) * IHIP_Q8_K_BYTES; }
+
+// The int8-activation entry points: x re-quantized to Q8_K, integer dots
+// (the reference C numerics, quant_kernels.c:166-194, 204-521, 602-650).
+int host_gemv_q8k(int type, const uint8_t *w, const float *x, float *out, void *q8_buf,
+                  int inner, int outer)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(type, inner, outer));
+    if (!w || !x || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const void *dw = nullptr;
+    RET_IF(resolve_locked(w, type, inner, outer, &dw));
+    RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)inner));
+    RET_IF(ensure(c.t, q8k_bytes(inner)));
+    RET_IF(ensure(c.y, sizeof(float) * (size_t)outer));
+    hipError_t e = launch_quantize_q8k((const float *)c.x.p, c.t.p, inner, c.stream);
+    if (e == hipSuccess)
+        e = launch_gemv_q8k(type, dw, c.t.p, (float *)c.y.p, inner, outer, c.stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
+    HIPCHK(hipMemcpyAsync(out, c.y.p, sizeof(float) * (size_t)outer, hipMemcpyDeviceToHost,
+                          c.stream));
+    if (q8_buf)
+        HIPCHK(hipMemcpyAsync(q8_buf, c.t.p, q8k_bytes(inner), hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+int host_vec_dot_q8k(int type, const void *x, const void *y, int nb, float *s)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    if (!x || !y || !s)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (nb <= 0)
+        return fail(IHIP_ERR_INVALID, "nb=%d must be positive", nb);
+    // a row is not a registered weight: staged, not cached
+    RET_IF(copy_in(c.src, x, (size_t)nb * block_bytes(type)));
+    RET_IF(copy_in(c.t, y, (size_t)nb * IHIP_Q8_K_BYTES));
+    RET_IF(ensure(c.y, sizeof(float)));
+    hipError_t e = launch_gemv_q8k(type, c.src.p, c.t.p, (float *)c.y.p, nb * 256, 1, c.stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "q8k dot launch failed: %s", hipGetErrorString(e));
+    HIPCHK(hipMemcpyAsync(s, c.y.p, sizeof(float), hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
 } // namespace
 
 extern "C" {
@@ -455,6 +509,58 @@ int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_
                    int outer_dim)
 {
     return host_gemv(kQ8_0, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_quantize_row_q8_k(const float *x, void *y, int64_t k)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    if (!x || !y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (k <= 0 || k % 256)
+        return fail(IHIP_ERR_INVALID, "k=%lld is not a positive multiple of 256", (long long)k);
+    RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)k));
+    RET_IF(ensure(c.t, q8k_bytes(k)));
+    hipError_t e = launch_quantize_q8k((const float *)c.x.p, c.t.p, k, c.stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "quantize launch failed: %s", hipGetErrorString(e));
+    HIPCHK(hipMemcpyAsync(y, c.t.p, q8k_bytes(k), hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+int ihip_vec_dot_q4_k_q8_k(const void *x, const void *y, int nb, float *s)
+{
+    return host_vec_dot_q8k(kQ4_K, x, y, nb, s);
+}
+
+int ihip_vec_dot_q5_k_q8_k(const void *x, const void *y, int nb, float *s)
+{
+    return host_vec_dot_q8k(kQ5_K, x, y, nb, s);
+}
+
+int ihip_vec_dot_q6_k_q8_k(const void *x, const void *y, int nb, float *s)
+{
+    return host_vec_dot_q8k(kQ6_K, x, y, nb, s);
+}
+
+int ihip_q4_k_gemv_q8k(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+                       int inner_dim, int outer_dim)
+{
+    return host_gemv_q8k(kQ4_K, weight, x, out, q8_buf, inner_dim, outer_dim);
+}
+
+int ihip_q5_k_gemv_q8k(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+                       int inner_dim, int outer_dim)
+{
+    return host_gemv_q8k(kQ5_K, weight, x, out, q8_buf, inner_dim, outer_dim);
+}
+
+int ihip_q6_k_gemv_q8k(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+                       int inner_dim, int outer_dim)
+{
+    return host_gemv_q8k(kQ6_K, weight, x, out, q8_buf, inner_dim, outer_dim);
 }
 
 int ihip_dequantize(int ggml_type, const uint8_t *src, float *dst, int64_t n)
@@ -704,6 +810,45 @@ int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int
     hipError_t e = launch_prefill_q4k(w, X, xh, Y, T, inner, outer, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_quantize_row_q8_k_dev(const float *x, void *y, int64_t k, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (!x || !y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (k <= 0 || k % 256)
+        return fail(IHIP_ERR_INVALID, "k=%lld is not a positive multiple of 256", (long long)k);
+    if (((uintptr_t)x & 3u) || ((uintptr_t)y & 3u))
+        return fail(IHIP_ERR_INVALID, "x and y must be 4-byte aligned");
+    hipError_t e = launch_quantize_q8k(x, y, k, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "quantize launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_gemv_q8k_dev(int ggml_type, const void *w, const void *q8, float *out, int inner,
+                      int outer, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(ggml_type, inner, outer));
+    if (!q8k_type(ggml_type))
+        return fail(IHIP_ERR_INVALID, "the Q8_K path takes Q4_K, Q5_K or Q6_K, not type %d",
+                    ggml_type);
+    if (!w || !q8 || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const uintptr_t wa = ggml_type == kQ6_K ? 1u : 15u;
+    if (((uintptr_t)w & wa) || ((uintptr_t)q8 & 3u) || ((uintptr_t)out & 3u))
+        return fail(IHIP_ERR_INVALID, "w must be %d-byte aligned, q8 and out 4-byte aligned",
+                    (int)wa + 1);
+    hipError_t e = launch_gemv_q8k(ggml_type, w, q8, out, inner, outer, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;
 }
 

@@ -35,4 +35,9 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
                               int inner, int outer, hipStream_t s);
 void set_prefill_tuning(const char *name, int value);
 
+// kq_q8k.hip
+hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t s);
+hipError_t launch_gemv_q8k(int type, const void *w, const void *q8, float *out, int inner,
+                           int outer, hipStream_t s);
+
 } // namespace ihip

@@ -30,6 +30,7 @@ IHIP_ERR_EMPTY = -7
 Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 FLAG_NAN, FLAG_POSINF, FLAG_ALL_NEGINF = 1, 2, 4
 ARGMAX_WS_BYTES = 262144
+Q8_K_BYTES = 292
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -64,6 +65,13 @@ SIGNATURES = {
     "ihip_q5_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q6_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q8_0_gemv": ([_vp, _vp, _vp, _i, _i], _i),
+    "ihip_quantize_row_q8_k": ([_vp, _vp, _i64], _i),
+    "ihip_vec_dot_q4_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),
+    "ihip_vec_dot_q5_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),
+    "ihip_vec_dot_q6_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),
+    "ihip_q4_k_gemv_q8k": ([_vp, _vp, _vp, _vp, _i, _i], _i),
+    "ihip_q5_k_gemv_q8k": ([_vp, _vp, _vp, _vp, _i, _i], _i),
+    "ihip_q6_k_gemv_q8k": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_dequantize": ([_i, _vp, _vp, _i64], _i),
     "ihip_ffn_swiglu": ([_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_lm_head_argmax": ([_i, _vp, _vp, _vp, C.POINTER(C.c_int32), _i, _i], _i),
@@ -77,6 +85,8 @@ SIGNATURES = {
     "ihip_fused_mlp_gate_mul_dev": ([_vp, _vp, _i64, _vp], _i),
     "ihip_fused_silu_gate_mul_dev": ([_vp, _vp, _vp, _i64, _vp], _i),
     "ihip_prefill_q4_k_dev": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "ihip_quantize_row_q8_k_dev": ([_vp, _vp, _i64, _vp], _i),
+    "ihip_gemv_q8k_dev": ([_i, _vp, _vp, _vp, _i, _i, _vp], _i),
 }
 
 _lib = None

@@ -142,3 +142,24 @@ def prefill_q4_k(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, xh: t
     check(lib().ihip_prefill_q4_k_dev(_ptr(w.data), _ptr(X, torch.float32, "X"), _ptr(xh), _ptr(Y, torch.float32, "Y"),
                                       T, w.inner, w.outer, _stream(stream)))
     return Y
+
+
+def quantize_row_q8k(x: torch.Tensor, y: torch.Tensor = None, stream=None) -> torch.Tensor:
+    """x (fp32, a multiple of 256 elements) -> Q8_K blocks (uint8, 292 bytes
+    per 256 elements), as quantize_row_q8_K (src/kernels/quant_kernels.c:166-194)."""
+    k = x.numel()
+    if y is None:
+        y = torch.empty(k // 256 * _lib.Q8_K_BYTES, dtype=torch.uint8, device=x.device)
+    check(lib().ihip_quantize_row_q8_k_dev(_ptr(x, torch.float32, "x"), _ptr(y, torch.uint8, "y"), k,
+                                           _stream(stream)))
+    return y
+
+
+def gemv_q8k(w: DeviceWeight, q8: torch.Tensor, out: torch.Tensor = None, stream=None) -> torch.Tensor:
+    """out = W x with x given as Q8_K blocks: the reference C path's numerics
+    (vec_dot_q{4,5,6}_K_q8_K per row, src/kernels/quant_kernels.c:204-521)."""
+    if out is None:
+        out = torch.empty(w.outer, dtype=torch.float32, device=q8.device)
+    check(lib().ihip_gemv_q8k_dev(w.ggml_type, _ptr(w.data), _ptr(q8, torch.uint8, "q8"),
+                                  _ptr(out, torch.float32, "out"), w.inner, w.outer, _stream(stream)))
+    return out
