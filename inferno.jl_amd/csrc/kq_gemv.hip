@@ -685,7 +685,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
 // ------------------------------------------------------------------------
 // Rows per wave of the wide kernels and rows per chunk of the streamed
 // kernels; 0 = the measured default.
-static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 4 / 2)
+static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 2)
 static int g_rows_gateup = 0; // fused gate/up (default 1)
 static int g_stream_rows = 0; // Q6_K/Q8_0 rows per chunk (default: see stream_rows())
 
@@ -703,7 +703,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
     const int nblk = inner / 256;
     int R = GATEUP ? g_rows_gateup : g_rows_wide;
     if (R <= 0) // measured on MI355X: 4096 x 4096 GEMV and 2 x 12288 x 4096 gate/up
-        R = GATEUP ? 1 : FMT == kQ5_K ? 2 : 4;
+        R = GATEUP ? 1 : 2;
     if (FMT == kQ5_K && GATEUP && R > 2)
         R = 2; // register budget
 #define IHIP_KW(RR)                                                                          \
