@@ -106,6 +106,27 @@ int ihip_q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_b
 int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
                    int outer_dim);
 
+/* ---- GGUF files feeding the weight registry ------------------------------
+ * read_gguf (src/GGUF.jl:119-165) and the keep-quantized load
+ * (src/LoaderCPU.jl:125-163): the file is memory-mapped and parsed (no GPU
+ * needed); tensors are listed by index; a Q4_K/Q5_K/Q6_K/Q8_0 tensor uploads
+ * into the registry (inner = ne0, outer = ne1) for ihip_weight_device_ptr and
+ * the *_dev entry points. */
+int ihip_gguf_open(const char *path, uint64_t *file_handle);
+int ihip_gguf_close(uint64_t file_handle);
+int ihip_gguf_info(uint64_t file_handle, uint32_t *version, uint64_t *alignment,
+                   uint64_t *data_offset, int64_t *tensor_count);
+/* name is NUL-terminated into name[name_cap]; dims[0] = ne0 (unused dims 1);
+ * offset is relative to the data section; nbytes = blocks x block size of the
+ * type (0 for a type without a known block size). */
+int ihip_gguf_tensor_info(uint64_t file_handle, int64_t index, char *name, size_t name_cap,
+                          int *ggml_type, int *ndim, int64_t dims[4], uint64_t *offset,
+                          uint64_t *nbytes);
+/* get_tensor_raw_bytes (src/GGUF.jl:186-205) sized by the tensor's type
+ * rather than 4 bytes per element: copies nbytes into dst. */
+int ihip_gguf_tensor_bytes(uint64_t file_handle, const char *name, void *dst, size_t dst_bytes);
+int ihip_gguf_upload(uint64_t file_handle, const char *name, uint64_t *weight_handle);
+
 /* ---- int8-activation variant: the reference C numerics, bit for bit ---- */
 /* Q8_K block: float d, int8 qs[256], int16 bsums[16] (292 bytes,
  * block_q8_K, quant_kernels.c:51-56). */

@@ -379,6 +379,23 @@ int host_vec_dot_q8k(int type, const void *x, const void *y, int nb, float *s)
 
 } // namespace
 
+// Hooks for gguf.hip (same library): report an error through
+// ihip_last_error, and upload GGML blocks into the registry.
+int ihip_fail_msg(int code, const char *msg) { return fail(code, "%s", msg); }
+
+int ihip_register_device_copy(const void *host, size_t bytes, int type, int inner, int outer,
+                              uint64_t *handle)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(type, inner, outer));
+    if (bytes < weight_bytes(type, inner, outer))
+        return fail(IHIP_ERR_INVALID, "%zu bytes < %zu needed for %dx%d type %d", bytes,
+                    weight_bytes(type, inner, outer), outer, inner, type);
+    return upload_locked(host, weight_bytes(type, inner, outer), type, inner, outer, false, handle);
+}
+
 extern "C" {
 
 const char *ihip_last_error(void) { return t_err.c_str(); }

@@ -65,6 +65,14 @@ SIGNATURES = {
     "ihip_q5_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q6_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q8_0_gemv": ([_vp, _vp, _vp, _i, _i], _i),
+    "ihip_gguf_open": ([C.c_char_p, C.POINTER(_u64)], _i),
+    "ihip_gguf_close": ([_u64], _i),
+    "ihip_gguf_info": ([_u64, C.POINTER(C.c_uint32), C.POINTER(_u64), C.POINTER(_u64),
+                        C.POINTER(_i64)], _i),
+    "ihip_gguf_tensor_info": ([_u64, _i64, C.c_char_p, _sz, C.POINTER(_i), C.POINTER(_i),
+                               C.POINTER(_i64), C.POINTER(_u64), C.POINTER(_u64)], _i),
+    "ihip_gguf_tensor_bytes": ([_u64, C.c_char_p, _vp, _sz], _i),
+    "ihip_gguf_upload": ([_u64, C.c_char_p, C.POINTER(_u64)], _i),
     "ihip_quantize_row_q8_k": ([_vp, _vp, _i64], _i),
     "ihip_vec_dot_q4_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),
     "ihip_vec_dot_q5_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),
