@@ -168,6 +168,13 @@ int ihip_ffn_swiglu(int gate_type, const uint8_t *wg, int up_type, const uint8_t
  * logits may be NULL.  Returns IHIP_ERR_NONFINITE on NaN/+Inf logits. */
 int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *logits,
                         int32_t *token, int hidden, int vocab);
+/* The MLP half of a decoder layer (src/ModelCPU.jl:913-920): x <- x + Wd h,
+ * h = silu(Wg n) .* (Wu n), n = rmsnorm_cpu!(x, norm_w, eps)
+ * (src/ModelCPU.jl:111-123: x * (1/sqrt(mean(x^2) + eps)) .* norm_w).  x is
+ * updated in place. */
+int ihip_ffn_block(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
+                   int down_type, const uint8_t *wd, const float *norm_w, float eps, float *x,
+                   int hidden, int inter);
 /* Batched prefill: Y[t,:] = W X[t,:] for t < T (W: outer x inner Q4_K);
  * the activations are rounded to fp16 for the matrix cores. */
 int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inner,
@@ -208,6 +215,24 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
  * of T*inner fp16 values (2 bytes each) for the rounded activations. */
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
+
+/* rmsnorm_cpu! (src/ModelCPU.jl:111-123): out = x * (1/sqrt(mean(x^2) + eps))
+ * .* w over n values (out may alias x). */
+int ihip_rmsnorm_dev(const float *x, const float *w, float eps, float *out, int n,
+                     ihip_stream stream);
+/* ihip_ffn_block on device pointers: the norm is folded into the fused gate/up
+ * pass (its scale multiplies the row sums) and the residual add into the down
+ * projection's epilogue.  h: inter floats of caller scratch. */
+int ihip_ffn_block_dev(int gate_type, const void *wg, int up_type, const void *wu, int down_type,
+                       const void *wd, const float *norm_w, float eps, float *x, float *h,
+                       int hidden, int inter, ihip_stream stream);
+/* Final norm + lm_head + greedy token (src/ModelCPU.jl:1014-1015): xn
+ * (hidden floats of caller scratch) receives rmsnorm(x) .* norm_w; the rest
+ * is ihip_lm_head_argmax_dev on xn. */
+int ihip_lm_head_argmax_norm_dev(int ggml_type, const void *w, const float *norm_w, float eps,
+                                 const float *x, float *xn, float *logits, int32_t *token,
+                                 uint32_t *flags, int hidden, int vocab, void *workspace,
+                                 ihip_stream stream);
 
 /* Device twins of the int8-activation variant.  x: 4-byte aligned fp32,
  * y / q8: 4-byte aligned Q8_K blocks; w: 16-byte aligned (Q4_K, Q5_K) or

@@ -69,7 +69,7 @@ struct Ctx {
     std::unordered_map<uint64_t, Weight> by_handle;
     std::unordered_map<const void *, uint64_t> by_host;
     uint64_t next_handle = 1;
-    DevBuf x, y, h, t, src; // staging and scratch, grown on demand
+    DevBuf x, y, h, t, src, nrm; // staging and scratch, grown on demand
     void *argmax_ws = nullptr; // IHIP_ARGMAX_WS_BYTES, left zeroed by the kernels
     int32_t *d_token = nullptr;
     uint32_t *d_flags = nullptr;
@@ -237,34 +237,47 @@ bool fast_ok(int type, const void *w, const float *x, int inner)
     return true;
 }
 
+// resid != nullptr: out = resid + W x (resid may be out)
 int gemv_dev_locked(int type, const void *w, const float *x, float *out, int inner, int outer,
-                    hipStream_t s)
+                    hipStream_t s, const float *resid = nullptr)
 {
     RET_IF(check_shape(type, inner, outer));
     if (!w || !x || !out)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    hipError_t e = fast_ok(type, w, x, inner) ? launch_gemv(type, w, x, out, inner, outer, s)
-                                              : launch_gemv_generic(type, w, x, out, inner, outer, s);
+    hipError_t e = fast_ok(type, w, x, inner)
+                       ? launch_gemv(type, w, x, out, inner, outer, s, resid)
+                       : launch_gemv_generic(type, w, x, out, inner, outer, s, resid);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "gemv launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;
 }
 
+// norm_w != nullptr: the input is rmsnorm(x) .* norm_w (folded into the fused
+// kernel; a one-workgroup norm kernel ahead of the unfused path)
 int gate_up_dev_locked(int gt, const void *wg, int ut, const void *wu, const float *x, float *h,
-                       int hidden, int inter, hipStream_t s)
+                       int hidden, int inter, hipStream_t s, const float *norm_w = nullptr,
+                       float eps = 0.0f)
 {
     RET_IF(check_shape(gt, hidden, inter));
     RET_IF(check_shape(ut, hidden, inter));
     if (!wg || !wu || !x || !h)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    if (gate_up_fusable(gt, ut) && fast_ok(gt, wg, x, hidden) && al16(wu)) {
-        hipError_t e = launch_gate_up_swiglu(gt, wg, wu, x, h, hidden, inter, s);
+    if (gate_up_fusable(gt, ut) && fast_ok(gt, wg, x, hidden) && al16(wu) &&
+        (!norm_w || al16(norm_w))) {
+        hipError_t e = launch_gate_up_swiglu(gt, wg, wu, x, h, hidden, inter, s, norm_w, eps);
         if (e != hipSuccess)
             return fail(IHIP_ERR_HIP, "gate/up launch failed: %s", hipGetErrorString(e));
         return IHIP_OK;
     }
-    // unfused: g -> h, u -> scratch, then h = silu(h) * u
     Ctx &c = ctx();
+    if (norm_w) {
+        RET_IF(ensure(c.nrm, sizeof(float) * (size_t)hidden));
+        hipError_t e = launch_rmsnorm(x, norm_w, eps, (float *)c.nrm.p, hidden, s);
+        if (e != hipSuccess)
+            return fail(IHIP_ERR_HIP, "rmsnorm launch failed: %s", hipGetErrorString(e));
+        x = (const float *)c.nrm.p;
+    }
+    // unfused: g -> h, u -> scratch, then h = silu(h) * u
     RET_IF(ensure(c.t, sizeof(float) * (size_t)inter));
     RET_IF(gemv_dev_locked(gt, wg, x, h, hidden, inter, s));
     RET_IF(gemv_dev_locked(ut, wu, x, (float *)c.t.p, hidden, inter, s));
@@ -433,7 +446,7 @@ int ihip_shutdown(void)
         (void)hipFree(kv.second.dev);
     c.by_handle.clear();
     c.by_host.clear();
-    for (DevBuf *b : {&c.x, &c.y, &c.h, &c.t, &c.src}) {
+    for (DevBuf *b : {&c.x, &c.y, &c.h, &c.t, &c.src, &c.nrm}) {
         if (b->p)
             (void)hipFree(b->p);
         b->p = nullptr;
@@ -631,6 +644,34 @@ int ihip_ffn_swiglu(int gate_type, const uint8_t *wg, int up_type, const uint8_t
     if (h)
         HIPCHK(hipMemcpyAsync(h, c.h.p, sizeof(float) * (size_t)inter, hipMemcpyDeviceToHost, c.stream));
     HIPCHK(hipMemcpyAsync(y, c.y.p, sizeof(float) * (size_t)hidden, hipMemcpyDeviceToHost, c.stream));
+    HIPCHK(hipStreamSynchronize(c.stream));
+    return IHIP_OK;
+}
+
+int ihip_ffn_block(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
+                   int down_type, const uint8_t *wd, const float *norm_w, float eps, float *x,
+                   int hidden, int inter)
+{
+    Ctx &c = ctx();
+    std::lock_guard<std::recursive_mutex> lk(c.mu);
+    RET_IF(ready_locked());
+    RET_IF(check_shape(gate_type, hidden, inter));
+    RET_IF(check_shape(up_type, hidden, inter));
+    RET_IF(check_shape(down_type, inter, hidden));
+    if (!wg || !wu || !wd || !norm_w || !x)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const void *dg, *du, *dd;
+    RET_IF(resolve_locked(wg, gate_type, hidden, inter, &dg));
+    RET_IF(resolve_locked(wu, up_type, hidden, inter, &du));
+    RET_IF(resolve_locked(wd, down_type, inter, hidden, &dd));
+    RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)hidden));
+    RET_IF(copy_in(c.src, norm_w, sizeof(float) * (size_t)hidden));
+    RET_IF(ensure(c.h, sizeof(float) * (size_t)inter));
+    RET_IF(gate_up_dev_locked(gate_type, dg, up_type, du, (const float *)c.x.p, (float *)c.h.p,
+                              hidden, inter, c.stream, (const float *)c.src.p, eps));
+    RET_IF(gemv_dev_locked(down_type, dd, (const float *)c.h.p, (float *)c.x.p, inter, hidden,
+                           c.stream, (const float *)c.x.p));
+    HIPCHK(hipMemcpyAsync(x, c.x.p, sizeof(float) * (size_t)hidden, hipMemcpyDeviceToHost, c.stream));
     HIPCHK(hipStreamSynchronize(c.stream));
     return IHIP_OK;
 }
@@ -867,6 +908,55 @@ int ihip_gemv_q8k_dev(int ggml_type, const void *w, const void *q8, float *out, 
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;
+}
+
+int ihip_rmsnorm_dev(const float *x, const float *w, float eps, float *out, int n,
+                     ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (!x || !w || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (n <= 0)
+        return fail(IHIP_ERR_INVALID, "n=%d must be positive", n);
+    hipError_t e = launch_rmsnorm(x, w, eps, out, n, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "rmsnorm launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_ffn_block_dev(int gate_type, const void *wg, int up_type, const void *wu, int down_type,
+                       const void *wd, const float *norm_w, float eps, float *x, float *h,
+                       int hidden, int inter, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(down_type, inter, hidden));
+    if (!wd || !norm_w || !x || !h)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    RET_IF(gate_up_dev_locked(gate_type, wg, up_type, wu, x, h, hidden, inter, (hipStream_t)stream,
+                              norm_w, eps));
+    return gemv_dev_locked(down_type, wd, h, x, inter, hidden, (hipStream_t)stream, x);
+}
+
+int ihip_lm_head_argmax_norm_dev(int ggml_type, const void *w, const float *norm_w, float eps,
+                                 const float *x, float *xn, float *logits, int32_t *token,
+                                 uint32_t *flags, int hidden, int vocab, void *workspace,
+                                 ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (!norm_w || !x || !xn)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    RET_IF(check_shape(ggml_type, hidden, vocab));
+    hipError_t e = launch_rmsnorm(x, norm_w, eps, xn, hidden, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "rmsnorm launch failed: %s", hipGetErrorString(e));
+    return lm_head_dev_locked(ggml_type, w, xn, logits, token, flags, hidden, vocab, workspace,
+                              (hipStream_t)stream);
 }
 
 } // extern "C"

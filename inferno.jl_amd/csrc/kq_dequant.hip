@@ -62,7 +62,8 @@ __device__ __forceinline__ float elem(const uint8_t *b, int e)
 template <int FMT>
 __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t *__restrict__ W,
                                                       const float *__restrict__ x,
-                                                      float *__restrict__ y, int outer, int inner)
+                                                      float *y, int outer, int inner,
+                                                      const float *resid)
 {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -75,7 +76,7 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t *__restrict_
         acc = fmaf(elem<FMT>(rp + (size_t)(c / BE) * BB, c % BE), x[c], acc);
     acc = wave_sum(acc);
     if (lane == 0)
-        y[row] = acc;
+        y[row] = resid ? resid[row] + acc : acc; // resid may be y
 }
 
 template <int FMT>
@@ -222,15 +223,15 @@ static unsigned grid_for(int64_t n, int64_t per_block, int64_t cap = 65535)
 }
 
 hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y, int inner,
-                               int outer, hipStream_t s)
+                               int outer, hipStream_t s, const float *resid)
 {
     const dim3 grid((outer + 3) / 4), block(256);
     const uint8_t *W = (const uint8_t *)w;
     switch (type) {
-    case kQ4_K: hipLaunchKernelGGL(k_gemv_generic<kQ4_K>, grid, block, 0, s, W, x, y, outer, inner); break;
-    case kQ5_K: hipLaunchKernelGGL(k_gemv_generic<kQ5_K>, grid, block, 0, s, W, x, y, outer, inner); break;
-    case kQ6_K: hipLaunchKernelGGL(k_gemv_generic<kQ6_K>, grid, block, 0, s, W, x, y, outer, inner); break;
-    case kQ8_0: hipLaunchKernelGGL(k_gemv_generic<kQ8_0>, grid, block, 0, s, W, x, y, outer, inner); break;
+    case kQ4_K: hipLaunchKernelGGL(k_gemv_generic<kQ4_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
+    case kQ5_K: hipLaunchKernelGGL(k_gemv_generic<kQ5_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
+    case kQ6_K: hipLaunchKernelGGL(k_gemv_generic<kQ6_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
+    case kQ8_0: hipLaunchKernelGGL(k_gemv_generic<kQ8_0>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -266,6 +267,36 @@ hipError_t launch_dequant(int type, const void *src, float *dst, int64_t n, bool
     case kQ8_0: hipLaunchKernelGGL(k_dequant_generic<kQ8_0>, dim3(grid), dim3(256), 0, s, S, dst, n); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+// ---- rmsnorm_cpu! (src/ModelCPU.jl:111-123) --------------------------------
+// One workgroup: sum of squares, scale = 1 / sqrt(ss / n + eps), then
+// out[i] = x[i] * scale * w[i] in the reference's order.  out may alias x.
+__global__ __launch_bounds__(1024) void k_rmsnorm(const float *x, const float *__restrict__ w,
+                                                  float eps, float *out, int n)
+{
+    __shared__ float part[16];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 1024)
+        ss = fmaf(x[i], x[i], ss);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0)
+        part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        t += part[k];
+    const float scale = 1.0f / sqrtf(t / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 1024)
+        out[i] = x[i] * scale * w[i];
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, float *out, int n,
+                          hipStream_t s)
+{
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, s, x, w, eps, out, n);
     return hipGetLastError();
 }
 

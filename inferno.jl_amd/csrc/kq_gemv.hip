@@ -203,11 +203,19 @@ __device__ __forceinline__ float kwide_dot(const KBytes &B, int j, const XWide &
 // W2 is the up weight, y[r] = silu(g[r]) * u[r]).  Wave w of workgroup g
 // owns rows [(4g + w) R, (4g + w + 1) R); rows past `outer` re-read the last
 // row and are not stored.
+//
+// nw != nullptr: the input is rmsnorm(x) .* nw (rmsnorm_cpu!,
+// src/ModelCPU.jl:111-123).  x .* nw is staged instead of x and the row sums
+// are multiplied by 1/sqrt(mean(x^2) + eps) at the end, so the norm costs no
+// extra pass.  resid != nullptr (plain GEMV): y[r] = resid[r] + (W x)[r], the
+// residual add of src/ModelCPU.jl:913-920 (resid may be y itself).
 template <int FMT, int R, bool GATEUP>
 __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ W,
                                                     const uint8_t *__restrict__ W2,
                                                     const float *__restrict__ x,
-                                                    float *__restrict__ y, int outer, int nblk)
+                                                    float *y, int outer, int nblk,
+                                                    const float *__restrict__ nw, float eps,
+                                                    const float *resid)
 {
     using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
@@ -227,6 +235,11 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
+    float ssq = 0.0f; // this thread's share of sum(x^2) (nw != nullptr)
+    float rv[R];      // residuals of this wave's rows, loaded ahead of the weights
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        rv[r] = resid ? resid[min(row0 + r, outer - 1)] : 0.0f;
     const int npass = (nblk + 15) >> 4;
     for (int pass = 0; pass < npass; ++pass) {
         const int nb = min(16, nblk - pass * 16);
@@ -234,6 +247,19 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
         const int blk = pass * 16 + (active ? b : 0);
         float4 xv[4];
         x_load_pass(x, pass * 4096, inner, xv);
+        if (nw) { // wave-uniform
+            float4 wv[4];
+            x_load_pass(nw, pass * 4096, inner, wv);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                ssq = fmaf(xv[k].x, xv[k].x, ssq);
+                ssq = fmaf(xv[k].y, xv[k].y, ssq);
+                ssq = fmaf(xv[k].z, xv[k].z, ssq);
+                ssq = fmaf(xv[k].w, xv[k].w, ssq);
+                xv[k] = make_float4(xv[k].x * wv[k].x, xv[k].y * wv[k].y, xv[k].z * wv[k].z,
+                                    xv[k].w * wv[k].w);
+            }
+        }
         KBytes B[NW][R];
 #pragma unroll
         for (int m = 0; m < NW; ++m) {
@@ -260,20 +286,29 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
                 acc[m][r] += active ? c : 0.0f;
             }
     }
+    float scale = 1.0f;
+    if (nw) { // wave-uniform: every wave takes part in the barrier
+        __shared__ float ssw[4];
+        const float t = wave_sum(ssq);
+        if (lane == 0)
+            ssw[wave] = t;
+        __syncthreads();
+        scale = 1.0f / sqrtf(((ssw[0] + ssw[1]) + (ssw[2] + ssw[3])) / (float)inner + eps);
+    }
     if (row0 >= outer)
         return; // wave-uniform, after the last barrier
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const float g = wave_sum(acc[0][r]);
+        const float g = wave_sum(acc[0][r]) * scale;
         float v = g;
         if constexpr (GATEUP) {
-            const float u = wave_sum(acc[NW - 1][r]);
+            const float u = wave_sum(acc[NW - 1][r]) * scale;
             // src/ModelCPU.jl:492-503: g / (1 + exp(-g)), then * u
             v = (g / (1.0f + expf(-g))) * u;
         }
         const int row = row0 + r;
         if (lane == 0 && row < outer)
-            y[row] = v;
+            y[row] = resid ? rv[r] + v : v;
     }
 }
 
@@ -564,13 +599,15 @@ __global__ __launch_bounds__(256) void k_argmax_partials(const float *__restrict
 // partial per workgroup).  Workgroups walk chunks of `rpc` rows grid-stride.
 
 constexpr int kStreamMaxRows = 64; // rows per chunk (one partial slot per row and wave)
+static_assert(kStreamMaxRows <= 64, "the epilogue gives every row its own thread");
 
 template <int FMT, int NW, int D, bool ARGMAX>
 __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restrict__ W,
                                                          const float *__restrict__ x,
-                                                         float *__restrict__ y, int outer,
+                                                         float *y, int outer,
                                                          int nblk, int rpc,
-                                                         ArgPart *__restrict__ parts)
+                                                         ArgPart *__restrict__ parts,
+                                                         const float *resid)
 {
     using F = SFmt<FMT>;
     constexpr int SLOT = F::SEG_BYTES + 16; // Q8_0 reads one dword past a segment
@@ -595,6 +632,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
     for (int chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
         const int row0 = chunk * rpc;
         const int nrows = min(rpc, outer - row0);
+        // the residual of this thread's row (the epilogue below has one row
+        // per thread) is loaded now, under the weight stream; the segment
+        // loop's first s_waitcnt(0) completes it before the copy waits start
+        const float rv = (resid && tid < nrows) ? resid[row0 + tid] : 0.0f;
         for (int i = tid; i < kStreamMaxRows * NW; i += NW * 64)
             (&part[0][0])[i] = 0.0f;
         __syncthreads();
@@ -652,7 +693,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
             for (int k = 0; k < NW; ++k)
                 v += part[i][k];
             if (y)
-                y[row0 + i] = v;
+                y[row0 + i] = resid ? rv + v : v; // i == tid; resid may be y
             if constexpr (ARGMAX)
                 argmax_fold(v, (uint32_t)(row0 + i), key, fl);
         }
@@ -698,7 +739,8 @@ void set_tuning(const char *name, int value)
 
 template <int FMT, bool GATEUP>
 static hipError_t launch_kwide(const void *w, const void *w2, const float *x, float *y,
-                               int inner, int outer, hipStream_t s)
+                               int inner, int outer, hipStream_t s, const float *nw = nullptr,
+                               float eps = 0.0f, const float *resid = nullptr)
 {
     const int nblk = inner / 256;
     int R = GATEUP ? g_rows_gateup : g_rows_wide;
@@ -710,7 +752,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
     case RR:                                                                                 \
         hipLaunchKernelGGL((k_gemv_kwide<FMT, RR, GATEUP>),                                  \
                            dim3((outer + 4 * RR - 1) / (4 * RR)), dim3(256), 0, s,            \
-                           (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk);      \
+                           (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid); \
         break;
     switch (R) {
         IHIP_KW(1)
@@ -747,27 +789,27 @@ static int stream_grid(int outer, int rpc) { return (outer + rpc - 1) / rpc; }
 
 template <int FMT, bool ARGMAX>
 static hipError_t launch_stream(const void *w, const float *x, float *y, int inner, int outer,
-                                void *parts, hipStream_t s)
+                                void *parts, hipStream_t s, const float *resid = nullptr)
 {
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int nw = stream_waves(nseg);
     const int rpc = stream_rows(outer, ARGMAX);
     const int grid = stream_grid(outer, rpc);
-#define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts);         return hipGetLastError();                                                                }
+#define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);         return hipGetLastError();                                                                }
     IHIP_ST(1, 2) IHIP_ST(2, 2) IHIP_ST(3, 2) IHIP_ST(4, 2) IHIP_ST(6, 2) IHIP_ST(8, 2)
 #undef IHIP_ST
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
-                       hipStream_t s)
+                       hipStream_t s, const float *resid)
 {
     switch (type) {
-    case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s);
-    case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s);
-    case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s);
-    case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s);
+    case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid);
+    case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid);
+    case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid);
+    case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid);
     default: return hipErrorInvalidValue;
     }
 }
@@ -778,11 +820,12 @@ bool gate_up_fusable(int gate_type, int up_type)
 }
 
 hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,
-                                 float *h, int hidden, int inter, hipStream_t s)
+                                 float *h, int hidden, int inter, hipStream_t s,
+                                 const float *norm_w, float eps)
 {
     switch (type) {
-    case kQ4_K: return launch_kwide<kQ4_K, true>(wg, wu, x, h, hidden, inter, s);
-    case kQ5_K: return launch_kwide<kQ5_K, true>(wg, wu, x, h, hidden, inter, s);
+    case kQ4_K: return launch_kwide<kQ4_K, true>(wg, wu, x, h, hidden, inter, s, norm_w, eps);
+    case kQ5_K: return launch_kwide<kQ5_K, true>(wg, wu, x, h, hidden, inter, s, norm_w, eps);
     default: return hipErrorInvalidValue;
     }
 }

@@ -7,11 +7,14 @@
 namespace ihip {
 
 // kq_gemv.hip
+// resid != nullptr: y = resid + W x (resid may be y).
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
-                       hipStream_t s);
+                       hipStream_t s, const float *resid = nullptr);
 bool gate_up_fusable(int gate_type, int up_type);
+// norm_w != nullptr: the input is rmsnorm(x) .* norm_w (eps inside the root).
 hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,
-                                 float *h, int hidden, int inter, hipStream_t s);
+                                 float *h, int hidden, int inter, hipStream_t s,
+                                 const float *norm_w = nullptr, float eps = 0.0f);
 // The fused lm_head argmax handles vocab <= 16384 chunks of at most 64 rows.
 bool lm_head_fusable(int vocab);
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
@@ -23,7 +26,10 @@ void set_tuning(const char *name, int value);
 
 // kq_dequant.hip
 hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y, int inner,
-                               int outer, hipStream_t s);
+                               int outer, hipStream_t s, const float *resid = nullptr);
+// rmsnorm_cpu! (src/ModelCPU.jl:111-123): out = x * (1/sqrt(mean(x^2) + eps)) .* w
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, float *out, int n,
+                          hipStream_t s);
 hipError_t launch_dequant(int type, const void *src, float *dst, int64_t n, bool aligned,
                           hipStream_t s);
 hipError_t launch_mlp_gate_mul(float *gate, const float *up, int64_t n, hipStream_t s);

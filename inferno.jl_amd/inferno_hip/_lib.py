@@ -84,6 +84,11 @@ SIGNATURES = {
     "ihip_ffn_swiglu": ([_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_lm_head_argmax": ([_i, _vp, _vp, _vp, C.POINTER(C.c_int32), _i, _i], _i),
     "ihip_prefill_q4_k": ([_vp, _vp, _vp, _i, _i, _i], _i),
+    "ihip_ffn_block": ([_i, _vp, _i, _vp, _i, _vp, _vp, C.c_float, _vp, _i, _i], _i),
+    "ihip_rmsnorm_dev": ([_vp, _vp, C.c_float, _vp, _i, _vp], _i),
+    "ihip_ffn_block_dev": ([_i, _vp, _i, _vp, _i, _vp, _vp, C.c_float, _vp, _vp, _i, _i, _vp], _i),
+    "ihip_lm_head_argmax_norm_dev": ([_i, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _vp, _i, _i,
+                                      _vp, _vp], _i),
     "ihip_gemv_dev": ([_i, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_dequantize_dev": ([_i, _vp, _vp, _i64, _vp], _i),
     "ihip_gate_up_swiglu_dev": ([_i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp], _i),

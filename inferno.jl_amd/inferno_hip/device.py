@@ -163,3 +163,41 @@ def gemv_q8k(w: DeviceWeight, q8: torch.Tensor, out: torch.Tensor = None, stream
     check(lib().ihip_gemv_q8k_dev(w.ggml_type, _ptr(w.data), _ptr(q8, torch.uint8, "q8"),
                                   _ptr(out, torch.float32, "out"), w.inner, w.outer, _stream(stream)))
     return out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor = None,
+            stream=None) -> torch.Tensor:
+    """rmsnorm_cpu! (src/ModelCPU.jl:111-123): x * (1/sqrt(mean(x^2) + eps)) .* w."""
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().ihip_rmsnorm_dev(_ptr(x, torch.float32, "x"), _ptr(w, torch.float32, "w"), eps,
+                                 _ptr(out, torch.float32, "out"), x.numel(), _stream(stream)))
+    return out
+
+
+def ffn_block(wg: DeviceWeight, wu: DeviceWeight, wd: DeviceWeight, norm_w: torch.Tensor,
+              eps: float, x: torch.Tensor, h: torch.Tensor = None, stream=None) -> torch.Tensor:
+    """The MLP half of a decoder layer (src/ModelCPU.jl:913-920), in place on x:
+    x += Wd (silu(Wg n) * (Wu n)), n = rmsnorm(x) .* norm_w."""
+    if h is None:
+        h = torch.empty(wg.outer, dtype=torch.float32, device=x.device)
+    check(lib().ihip_ffn_block_dev(wg.ggml_type, _ptr(wg.data), wu.ggml_type, _ptr(wu.data),
+                                   wd.ggml_type, _ptr(wd.data), _ptr(norm_w, torch.float32, "norm_w"),
+                                   eps, _ptr(x, torch.float32, "x"), _ptr(h, torch.float32, "h"),
+                                   wg.inner, wg.outer, _stream(stream)))
+    return x
+
+
+def lm_head_argmax_norm(w: DeviceWeight, norm_w: torch.Tensor, eps: float, x: torch.Tensor,
+                        ws: "ArgmaxWorkspace", xn: torch.Tensor = None, logits: torch.Tensor = None,
+                        stream=None):
+    """Final norm + lm_head + greedy token (src/ModelCPU.jl:1014-1015); the
+    token and flags land in ws.token / ws.flags (device)."""
+    if xn is None:
+        xn = torch.empty_like(x)
+    check(lib().ihip_lm_head_argmax_norm_dev(
+        w.ggml_type, _ptr(w.data), _ptr(norm_w, torch.float32, "norm_w"), eps,
+        _ptr(x, torch.float32, "x"), _ptr(xn, torch.float32, "xn"),
+        None if logits is None else _ptr(logits, torch.float32, "logits"),
+        ws.token.data_ptr(), ws.flags.data_ptr(), w.inner, w.outer, ws.ws.data_ptr(), _stream(stream)))
+    return xn

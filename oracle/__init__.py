@@ -58,11 +58,16 @@ def lib():
         L.orc_ffn_swiglu_f64.argtypes = [C.c_int, _u8p, C.c_int, _u8p, C.c_int, _u8p, _f32p,
                                          C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
                                          _f64p]
+        L.orc_rmsnorm_f64.argtypes = [_f32p, _f32p, C.c_float, C.c_int, _f64p]
+        L.orc_ffn_block_f64.argtypes = [C.c_int, _u8p, C.c_int, _u8p, C.c_int, _u8p, _f32p, _f32p,
+                                        C.c_float, C.c_int, C.c_int, _f64p, _f64p, _f64p, _f64p,
+                                        _f64p]
         L.orc_quantize_row_q8k.argtypes = [_f32p, _u8p, C.c_int64]
         L.orc_gemv_q8k.argtypes = [C.c_int, _u8p, _f32p, _f32p, _u8p, C.c_int, C.c_int]
         L.orc_gemv_q8_0_lanes.argtypes = [_u8p, _f32p, _f32p, C.c_int, C.c_int]
         for name in ("orc_dequant", "orc_gemv_f64", "orc_row_norms", "orc_gemv_f32_serial",
-                     "orc_argmax", "orc_ffn_swiglu_f64", "orc_quantize_row_q8k",
+                     "orc_argmax", "orc_ffn_swiglu_f64", "orc_rmsnorm_f64", "orc_ffn_block_f64",
+                     "orc_quantize_row_q8k",
                      "orc_gemv_q8k", "orc_gemv_q8_0_lanes"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -150,6 +155,23 @@ def ffn_swiglu_f64(gtype, wg, utype, wu, dtype_, wd, x, hidden, inter):
                                   np.ascontiguousarray(x, np.float32), hidden, inter,
                                   g.ctypes.data, u.ctypes.data, h.ctypes.data, y), "ffn")
     return g, u, h, y
+
+
+def rmsnorm_f64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    out = np.empty(len(x), np.float64)
+    _chk(lib().orc_rmsnorm_f64(np.ascontiguousarray(x, np.float32), np.ascontiguousarray(w, np.float32),
+                               eps, len(x), out), "rmsnorm")
+    return out
+
+
+def ffn_block_f64(gtype, wg, utype, wu, dtype_, wd, x, nw, eps, hidden, inter):
+    n = np.empty(hidden, np.float64)
+    g, u, h = (np.empty(inter, np.float64) for _ in range(3))
+    y = np.empty(hidden, np.float64)
+    _chk(lib().orc_ffn_block_f64(gtype, wg, utype, wu, dtype_, wd, np.ascontiguousarray(x, np.float32),
+                                 np.ascontiguousarray(nw, np.float32), eps, hidden, inter,
+                                 n, g, u, h, y), "ffn_block")
+    return n, g, u, h, y
 
 
 def quantize_row_q8k(x: np.ndarray) -> np.ndarray:

@@ -394,6 +394,63 @@ int orc_ffn_swiglu_f64(int gate_type, const uint8_t *wg, int up_type,
     return 0;
 }
 
+/* rmsnorm_cpu!, src/ModelCPU.jl:111-123, in fp64 over the fp32 inputs:
+ * out[i] = x[i] * (1 / sqrt(sum(x^2) / n + eps)) * w[i]. */
+int orc_rmsnorm_f64(const float *x, const float *w, float eps, int n, double *out)
+{
+    if (n <= 0)
+        return -1;
+    double ss = 0.0;
+    for (int i = 0; i < n; ++i)
+        ss += (double)x[i] * (double)x[i];
+    const double scale = 1.0 / sqrt(ss / (double)n + (double)eps);
+    for (int i = 0; i < n; ++i)
+        out[i] = (double)x[i] * scale * (double)w[i];
+    return 0;
+}
+
+/* y = W v for an fp64 input vector (dequantized rows, fp64 sums). */
+static void gemv_f64_dvec(int type, const uint8_t *w, const double *v, double *y, int inner,
+                          int outer)
+{
+    const deq_fn f = deq_for(type);
+    const int be = orc_block_elems(type), bb = orc_block_bytes(type);
+    const int nb = inner / be;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < outer; ++r) {
+        float blk[256];
+        double acc = 0.0;
+        for (int b = 0; b < nb; ++b) {
+            f(w + ((size_t)r * nb + b) * bb, blk);
+            for (int i = 0; i < be; ++i)
+                acc += (double)blk[i] * v[(size_t)b * be + i];
+        }
+        y[r] = acc;
+    }
+}
+
+/* The MLP half of a decoder layer, src/ModelCPU.jl:913-920, in fp64:
+ * n = rmsnorm(x) .* nw, h = silu(Wg n) * (Wu n), y = x + Wd h. */
+int orc_ffn_block_f64(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
+                      int down_type, const uint8_t *wd, const float *x, const float *nw,
+                      float eps, int hidden, int inter, double *n, double *g, double *u,
+                      double *h, double *y)
+{
+    if (check_dims(gate_type, hidden, inter) || check_dims(up_type, hidden, inter) ||
+        check_dims(down_type, inter, hidden))
+        return -1;
+    if (orc_rmsnorm_f64(x, nw, eps, hidden, n))
+        return -1;
+    gemv_f64_dvec(gate_type, wg, n, g, hidden, inter);
+    gemv_f64_dvec(up_type, wu, n, u, hidden, inter);
+    for (int i = 0; i < inter; ++i)
+        h[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
+    gemv_f64_dvec(down_type, wd, h, y, inter, hidden);
+    for (int r = 0; r < hidden; ++r)
+        y[r] += (double)x[r];
+    return 0;
+}
+
 /* ------------------------------------------------------------------ */
 /* The reference C int8-activation path                                  */
 /* ------------------------------------------------------------------ */

@@ -70,6 +70,15 @@ int orc_ffn_swiglu_f64(int gate_type, const uint8_t *wg, int up_type,
                        const float *x, int hidden, int inter,
                        double *g, double *u, double *h, double *y);
 
+/* rmsnorm_cpu!, src/ModelCPU.jl:111-123, in fp64. */
+int orc_rmsnorm_f64(const float *x, const float *w, float eps, int n, double *out);
+/* Decoder MLP half, src/ModelCPU.jl:913-920, in fp64: n = rmsnorm(x) .* nw,
+ * h = silu(Wg n) * (Wu n), y = x + Wd h (n, g, u, h: hidden/inter/inter/inter). */
+int orc_ffn_block_f64(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
+                      int down_type, const uint8_t *wd, const float *x, const float *nw,
+                      float eps, int hidden, int inter, double *n, double *g, double *u,
+                      double *h, double *y);
+
 /* Reference C int8-activation path, src/kernels/quant_kernels.c:166-194. */
 int orc_quantize_row_q8k(const float *x, uint8_t *q8, int64_t k);
 /* q{4,5,6}_k_gemv with the AVX2 lane order, quant_kernels.c:204-277,

@@ -1,0 +1,157 @@
+"""GPU parity of the path's fused neighbours: rmsnorm_cpu! (src/ModelCPU.jl:
+111-123) folded into the gate/up pass, the residual add of the decoder's MLP
+half (src/ModelCPU.jl:913-920) folded into the down projection, and the final
+norm ahead of the lm_head (src/ModelCPU.jl:1014-1015), against the fp64
+oracle (oracle.rmsnorm_f64, oracle.ffn_block_f64).
+
+Bars: rmsnorm within 4 fp32 ulps of the fp64 value; the FFN under the same
+per-row GEMV bound as the plain FFN tests, with x' = rmsnorm(x) .* w as the
+GEMV input; the residual adds one fp32 rounding; token ids exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from inferno_hip import _lib
+    assert _lib.available(), "libinferno_hip.so reports no usable gfx950 device"
+    yield
+    torch.cuda.synchronize()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def dweight(w, t, inner, outer):
+    from inferno_hip.device import DeviceWeight
+    return DeviceWeight(dev(w), t, inner, outer)
+
+
+def check_within(y, ref, tol, what):
+    err = np.abs(np.asarray(y, np.float64) - ref)
+    say(f"{what}: max err/tol = {float(np.max(err / tol)):.3e}")
+    assert np.all(err <= tol), f"{what}: {int(np.sum(err > tol))} over tolerance"
+
+
+def h_bound(g, u, ng, nu, xin):
+    tg = oracle.tolerance(ng, xin)
+    tu = oracle.tolerance(nu, xin)
+    s = 1 / (1 + np.exp(-g))
+    silu = g * s
+    dsilu = s * (1 + g * (1 - s))
+    return np.abs(dsilu * u) * tg + np.abs(silu) * tu + 1e-6 * np.abs(silu * u) + 1e-30
+
+
+@pytest.mark.parametrize("n,eps", [(4096, 1e-6), (2048, 1e-5), (1000, 0.5)])
+def test_rmsnorm(n, eps):
+    from inferno_hip import device as D
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    say(f"rmsnorm n={n} eps={eps}")
+    ref = oracle.rmsnorm_f64(x, w, eps)
+    tol = 4 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) + 1e-30
+    check_within(D.rmsnorm(dev(x), dev(w), eps).cpu().numpy(), ref, tol, "rmsnorm")
+    xd = dev(x)
+    D.rmsnorm(xd, dev(w), eps, out=xd)  # in place
+    check_within(xd.cpu().numpy(), ref, tol, "rmsnorm in place")
+
+
+FFN_CASES = [
+    (4096, 12288, synth.Q4_K, synth.Q6_K),   # decode FFN block, full size: fused norm + residual
+    (2048, 5632, synth.Q5_K, synth.Q6_K),
+    (1024, 2816, synth.Q4_K, synth.Q4_K),    # residual in the wide kernel's epilogue
+    (512, 768, synth.Q8_0, synth.Q8_0),      # unfused gate/up: norm kernel first
+]
+
+
+def _block_case(hidden, inter, gt, dt, seed):
+    rng = synth.rng_for(seed)
+    wg = synth.weight(rng, gt, inter, hidden)
+    wu = synth.weight(rng, gt, inter, hidden)
+    wd = synth.weight(rng, dt, hidden, inter)
+    x = synth.activations(rng, hidden) * np.float32(2.5)
+    nw = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+    return wg, wu, wd, x, nw
+
+
+def _check_block(x_out, h, x, case, gt, dt, hidden, inter, eps):
+    wg, wu, wd, _, nw = case
+    n, g, u, h_ref, y_ref = oracle.ffn_block_f64(gt, wg, gt, wu, dt, wd, x, nw, eps, hidden, inter)
+    ng = oracle.row_norms(gt, wg, hidden, inter)
+    nu = oracle.row_norms(gt, wu, hidden, inter)
+    if h is not None:
+        check_within(h, h_ref, h_bound(g, u, ng, nu, n), "h = silu(g)*u of the normed x")
+    nd = oracle.row_norms(dt, wd, inter, hidden)
+    dh = 0.0 if h is None else np.linalg.norm(np.asarray(h, np.float64) - h_ref)
+    if h is None:  # host entry point: bound h by its own tolerance
+        dh = np.linalg.norm(h_bound(g, u, ng, nu, n))
+    tol = 1e-4 * nd * np.linalg.norm(h_ref) + nd * dh + 2 * np.spacing(np.abs(y_ref).astype(np.float32))
+    check_within(x_out, y_ref, tol, "x + Wd h")
+
+
+@pytest.mark.parametrize("hidden,inter,gt,dt", FFN_CASES)
+def test_ffn_block_with_norm_and_residual(hidden, inter, gt, dt):
+    from inferno_hip import device as D
+    eps = 1e-6
+    case = _block_case(hidden, inter, gt, dt, 0xB10C + hidden)
+    wg, wu, wd, x, nw = case
+    say(f"ffn block hidden={hidden} inter={inter} gate/up={gt} down={dt}")
+    xd = dev(x)
+    h = torch.empty(inter, device="cuda")
+    D.ffn_block(dweight(wg, gt, hidden, inter), dweight(wu, gt, hidden, inter),
+                dweight(wd, dt, inter, hidden), dev(nw), eps, xd, h=h)
+    _check_block(xd.cpu().numpy(), h.cpu().numpy(), x, case, gt, dt, hidden, inter, eps)
+
+
+def test_ffn_block_host_entry_point():
+    from inferno_hip import _lib
+    hidden, inter, gt, dt = 1024, 2816, synth.Q4_K, synth.Q6_K if 2816 % 2048 == 0 else synth.Q8_0
+    eps = 1e-5
+    case = _block_case(hidden, inter, gt, dt, 0xB10D)
+    wg, wu, wd, x, nw = case
+    say("ihip_ffn_block host")
+    xo = x.copy()
+    _lib.check(_lib.lib().ihip_ffn_block(gt, wg.ctypes.data, gt, wu.ctypes.data, dt, wd.ctypes.data,
+                                         nw.ctypes.data, eps, xo.ctypes.data, hidden, inter))
+    _check_block(xo, None, x, case, gt, dt, hidden, inter, eps)
+
+
+@pytest.mark.parametrize("t,vocab,hidden,seed", [(synth.Q6_K, 32000, 2048, 0x7E), (synth.Q4_K, 5003, 1024, 0x7F)])
+def test_lm_head_with_final_norm(t, vocab, hidden, seed):
+    from inferno_hip import device as D
+    rng = synth.rng_for(seed)
+    w = synth.weight(rng, t, vocab, hidden)
+    x = synth.activations(rng, hidden) * np.float32(4.0)
+    nw = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+    eps = 1e-6
+    say(f"final norm + lm_head type={t} vocab={vocab}")
+    ws = D.ArgmaxWorkspace()
+    logits = torch.empty(vocab, device="cuda")
+    xn = D.lm_head_argmax_norm(dweight(w, t, hidden, vocab), dev(nw), eps, dev(x), ws, logits=logits)
+    tok = ws.result()
+    n = oracle.rmsnorm_f64(x, nw, eps)
+    ref = np.empty(vocab)
+    ref[:] = oracle.gemv_f64(t, w, n.astype(np.float32), hidden, vocab)
+    tol = oracle.tolerance(oracle.row_norms(t, w, hidden, vocab), n) + 1e-6 * np.abs(ref)
+    check_within(logits.cpu().numpy(), ref, tol, "logits of the normed x")
+    check_within(xn.cpu().numpy(), n, 4 * np.spacing(np.abs(n).astype(np.float32)) + 1e-30, "xn")
+    best = int(np.argmax(ref))
+    gap = ref[best] - np.max(np.delete(ref, best))
+    assert gap > 2 * tol.max(), "seed gives an ambiguous maximum"
+    assert tok == best

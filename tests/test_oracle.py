@@ -273,3 +273,43 @@ def test_argmax_matches_numpy_first_occurrence():
     for n in (1, 2, 31, 32, 33, 1000, 151936):
         v = rng.integers(-50, 50, size=n).astype(np.float32)
         assert oracle.argmax(v)[0] == int(np.argmax(v))
+
+
+# ---- rmsnorm and the decoder MLP half (src/ModelCPU.jl:111-123, 913-920) ----
+
+def test_rmsnorm_oracle_properties():
+    rng = np.random.default_rng(0x4E)
+    x = rng.standard_normal(4096).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float32)
+    one = np.ones(4096, np.float32)
+    # eps = 0: invariant under exact power-of-two scaling of x (a missing root
+    # or a sum instead of a mean breaks it)
+    a = oracle.rmsnorm_f64(x, w, 0.0)
+    assert np.array_equal(a, oracle.rmsnorm_f64(x * np.float32(4.0), w, 0.0))
+    # unit weights, eps = 0: mean of squares is 1
+    assert abs(np.mean(oracle.rmsnorm_f64(x, one, 0.0) ** 2) - 1.0) < 1e-12
+    # constant input c: c / sqrt(c^2 + eps) * w, elementwise
+    c, eps = np.float32(0.37), np.float32(1e-2)
+    got = oracle.rmsnorm_f64(np.full(64, c, np.float32), w[:64], float(eps))
+    want = float(c) / np.sqrt(float(c) ** 2 + float(eps)) * w[:64].astype(np.float64)
+    assert np.allclose(got, want, rtol=1e-14, atol=0)
+
+
+def test_ffn_block_oracle_is_norm_then_ffn_then_residual():
+    rng = synth.rng_for(0x4F)
+    hidden, inter = 512, 768
+    wg = synth.weight(rng, synth.Q4_K, inter, hidden)
+    wu = synth.weight(rng, synth.Q4_K, inter, hidden)
+    wd = synth.weight(rng, synth.Q6_K, hidden, inter) if inter % 2048 == 0 else \
+        synth.weight(rng, synth.Q8_0, hidden, inter)
+    dt = synth.Q6_K if inter % 2048 == 0 else synth.Q8_0
+    x = synth.activations(rng, hidden) * np.float32(3.0)
+    nw = rng.uniform(0.5, 1.5, hidden).astype(np.float32)
+    n, g, u, h, y = oracle.ffn_block_f64(synth.Q4_K, wg, synth.Q4_K, wu, dt, wd, x, nw, 1e-6,
+                                         hidden, inter)
+    assert np.array_equal(n, oracle.rmsnorm_f64(x, nw, 1e-6))
+    # the same FFN on the fp32-rounded normed input, plus the residual
+    g2, u2, h2, y2 = oracle.ffn_swiglu_f64(synth.Q4_K, wg, synth.Q4_K, wu, dt, wd,
+                                           n.astype(np.float32), hidden, inter)
+    nrm = oracle.row_norms(dt, wd, inter, hidden)
+    assert np.all(np.abs((y - x) - y2) <= 1e-5 * nrm * np.linalg.norm(h2))
