@@ -105,6 +105,12 @@ int ihip_q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_b
 /* Same arguments as q8_0_gemv (quant_kernels.c:657). */
 int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
                    int outer_dim);
+/* mul_quant_mat_vec(::IQ4NL_Matrix) (src/ModelCPU.jl:381-408): 18-byte
+ * blocks of 32 (f16 d, 16 bytes of 4-bit indices into the grid of
+ * src/QuantsData.jl:384); GGML type 20.  The same arguments as
+ * ihip_q8_0_gemv. */
+int ihip_iq4_nl_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
+                     int outer_dim);
 
 /* ---- GGUF files feeding the weight registry ------------------------------
  * read_gguf (src/GGUF.jl:119-165) and the keep-quantized load

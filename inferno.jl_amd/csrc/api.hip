@@ -224,12 +224,13 @@ int resolve_locked(const void *host, int type, int inner, int outer, const void 
 }
 
 // Fast kernels need 16-byte aligned weights and x, and (staged formats)
-// 16-byte aligned rows: Q6_K rows of a multiple of 8 blocks, Q8_0 rows of a
-// multiple of 8 blocks.
+// 16-byte aligned rows: Q6_K, Q8_0 and IQ4_NL rows of a multiple of 8 blocks.
 bool fast_ok(int type, const void *w, const float *x, int inner)
 {
     if (!al16(w) || !al16(x))
         return false;
+    if (type == kIQ4_NL) // 8-block groups of 144 bytes
+        return inner % 256 == 0;
     if (type == kQ6_K)
         return inner % 2048 == 0;
     if (type == kQ8_0)
@@ -539,6 +540,12 @@ int ihip_q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_
                    int outer_dim)
 {
     return host_gemv(kQ8_0, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_iq4_nl_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim,
+                     int outer_dim)
+{
+    return host_gemv(kIQ4_NL, weight, x, out, inner_dim, outer_dim);
 }
 
 int ihip_quantize_row_q8_k(const float *x, void *y, int64_t k)

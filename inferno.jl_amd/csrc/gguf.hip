@@ -396,9 +396,9 @@ int ihip_gguf_upload(uint64_t file_handle, const char *name, uint64_t *weight_ha
     if (ti == f.by_name.end())
         return ihip_fail_msg(IHIP_ERR_INVALID, (std::string("tensor not found: ") + name).c_str());
     const Tensor &t = f.tensors[ti->second];
-    if (t.type != 8 && t.type != 12 && t.type != 13 && t.type != 14)
-        return ihip_fail_msg(IHIP_ERR_INVALID,
-                             "only Q4_K, Q5_K, Q6_K and Q8_0 tensors are kept quantized on the device");
+    if (t.type != 8 && t.type != 12 && t.type != 13 && t.type != 14 && t.type != 20)
+        return ihip_fail_msg(IHIP_ERR_INVALID, "only Q4_K, Q5_K, Q6_K, Q8_0 and IQ4_NL tensors are "
+                                               "kept quantized on the device");
     if (t.ndim > 2 || t.dims[0] > INT32_MAX || t.dims[1] > INT32_MAX)
         return ihip_fail_msg(IHIP_ERR_INVALID, "a weight tensor has rank 1 or 2 and int-sized dims");
     // src/LoaderCPU.jl:130-132: inner = ne0, outer = ne1

@@ -13,17 +13,18 @@
 
 namespace ihip {
 
-constexpr int kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14;
+constexpr int kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ4_NL = 20;
 
 constexpr int kBytesQ4K = 144, kBytesQ5K = 176, kBytesQ6K = 210, kBytesQ80 = 34;
 
 __host__ __device__ constexpr int block_bytes(int t)
 {
-    return t == kQ4_K ? 144 : t == kQ5_K ? 176 : t == kQ6_K ? 210 : t == kQ8_0 ? 34 : 0;
+    return t == kQ4_K ? 144 : t == kQ5_K ? 176 : t == kQ6_K ? 210 : t == kQ8_0 ? 34
+         : t == kIQ4_NL ? 18 : 0;
 }
 __host__ __device__ constexpr int block_elems(int t)
 {
-    return (t == kQ4_K || t == kQ5_K || t == kQ6_K) ? 256 : t == kQ8_0 ? 32 : 0;
+    return (t == kQ4_K || t == kQ5_K || t == kQ6_K) ? 256 : (t == kQ8_0 || t == kIQ4_NL) ? 32 : 0;
 }
 
 // fp16 bits -> fp32.  v_cvt_f32_f16 widens exactly, fp16 subnormals

@@ -29,11 +29,20 @@ __device__ __forceinline__ void k_scale_min_bytes(const uint8_t *s, int i, uint3
 }
 
 // Element e of one block, src/Dequant.jl element order.
+// IQ4_NL's non-linear 4-bit grid (src/QuantsData.jl:384).
+__constant__ int8_t kIQ4NLValues[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                        1,    13,   25,  38,  53,  69,  89,  113};
+
 template <int FMT>
 __device__ __forceinline__ float elem(const uint8_t *b, int e)
 {
     if constexpr (FMT == kQ8_0) {
         return h2f(rd16(b)) * (float)(int8_t)b[2 + e];
+    } else if constexpr (FMT == kIQ4_NL) {
+        // src/Dequant.jl:683-693: element j low nibble of qs[j], element
+        // j + 16 high nibble; d * value (exact in fp32)
+        const uint32_t qb = b[2 + (e & 15)];
+        return h2f(rd16(b)) * (float)kIQ4NLValues[e < 16 ? (qb & 15u) : (qb >> 4)];
     } else if constexpr (FMT == kQ6_K) {
         const int n = e >> 7, r = e & 127, g = r >> 5, l = r & 31;
         const uint32_t lb = b[64 * n + l + 32 * (g & 1)];
@@ -232,6 +241,7 @@ hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y
     case kQ5_K: hipLaunchKernelGGL(k_gemv_generic<kQ5_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
     case kQ6_K: hipLaunchKernelGGL(k_gemv_generic<kQ6_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
     case kQ8_0: hipLaunchKernelGGL(k_gemv_generic<kQ8_0>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
+    case kIQ4_NL: hipLaunchKernelGGL(k_gemv_generic<kIQ4_NL>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -265,6 +275,7 @@ hipError_t launch_dequant(int type, const void *src, float *dst, int64_t n, bool
     case kQ5_K: hipLaunchKernelGGL(k_dequant_generic<kQ5_K>, dim3(grid), dim3(256), 0, s, S, dst, n); break;
     case kQ6_K: hipLaunchKernelGGL(k_dequant_generic<kQ6_K>, dim3(grid), dim3(256), 0, s, S, dst, n); break;
     case kQ8_0: hipLaunchKernelGGL(k_dequant_generic<kQ8_0>, dim3(grid), dim3(256), 0, s, S, dst, n); break;
+    case kIQ4_NL: hipLaunchKernelGGL(k_dequant_generic<kIQ4_NL>, dim3(grid), dim3(256), 0, s, S, dst, n); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

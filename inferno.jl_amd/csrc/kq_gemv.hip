@@ -328,15 +328,21 @@ template <>
 struct SFmt<kQ8_0> {
     static constexpr int SEG_BLOCKS = 64, SEG_BYTES = 64 * 34;
 };
+template <>
+struct SFmt<kIQ4_NL> {
+    static constexpr int SEG_BLOCKS = 64, SEG_BYTES = 64 * 18;
+};
 static_assert(SFmt<kQ6_K>::SEG_BYTES % 16 == 0, "Q6_K segment must be 16-byte aligned");
 static_assert(SFmt<kQ8_0>::SEG_BYTES % 16 == 0, "Q8_0 segment must be 16-byte aligned");
+static_assert(SFmt<kIQ4_NL>::SEG_BYTES % 16 == 0, "IQ4_NL segment must be 16-byte aligned");
 
 // Q6_K lane geometry: block bs = lane>>3; unit u = lane&7: half n = u>>2,
 // positions l0 = 8*(u&3) .. +7.  Group g (0..3) of the unit holds the
 // elements 128n + 32g + l0 + i (src/Dequant.jl:584-597): g=0 low nibble of
 // ql[64n+l0+i], g=1 low nibble of ql[64n+32+l0+i], g=2/3 the high nibbles,
 // with qh[32n+l0+i] bits 2g..2g+1 on top and scale sc[8n + 2g + (l0>>4)].
-// Q8_0 lane geometry: lane = block of the 64-block segment, 32 weights.
+// Q8_0 and IQ4_NL lane geometry: lane = block of the 64-block segment, 32
+// weights (IQ4_NL also keeps the sum of its 32 x values).
 template <int FMT>
 struct SX;
 template <>
@@ -347,6 +353,11 @@ struct SX<kQ6_K> {
 template <>
 struct SX<kQ8_0> {
     float x[32];
+};
+template <>
+struct SX<kIQ4_NL> {
+    float x[32];
+    float s;
 };
 
 // All loads first, then the selects and sums, so that the loads are in
@@ -389,6 +400,13 @@ __device__ __forceinline__ void staged_load_x(const float *__restrict__ xseg, in
         for (int t = 0; t < 8; ++t) {
             X.x[4 * t] = v[t].x; X.x[4 * t + 1] = v[t].y;
             X.x[4 * t + 2] = v[t].z; X.x[4 * t + 3] = v[t].w;
+        }
+        if constexpr (FMT == kIQ4_NL) {
+            float a = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                a += (v[t].x + v[t].y) + (v[t].z + v[t].w);
+            X.s = a;
         }
     }
 }
@@ -449,6 +467,54 @@ __device__ __forceinline__ float q80_dot(const uint8_t *row_lds, uint32_t off, c
         a1 = fmaf(sbyte_f(q, 3), xr[4 * t + 3], a1);
     }
     return d * (a0 + a1);
+}
+
+// IQ4_NL block at byte `off` of the 16-byte-aligned LDS row `row_lds`
+// (src/Dequant.jl:683-693: element j = low nibble of qs[j], element j + 16 =
+// high nibble; weight = d * grid[nibble], grid src/QuantsData.jl:384).  The
+// grid, biased by +128 to unsigned bytes, is looked up four nibbles at a time
+// with byte permutes (grid[0..7] and grid[8..15], then a choice by the
+// nibble's bit 3); the bias comes back off through the lane's x sum.
+constexpr uint32_t kIQ4G0 = 0x3F2D1801u; // grid + 128: 1, 24, 45, 63
+constexpr uint32_t kIQ4G1 = 0x766A5D4Fu; // 79, 93, 106, 118
+constexpr uint32_t kIQ4G2 = 0xA6998D81u; // 129, 141, 153, 166
+constexpr uint32_t kIQ4G3 = 0xF1D9C5B5u; // 181, 197, 217, 241
+
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t nib) // four nibbles in bytes
+{
+    const uint32_t n7 = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIQ4G1, kIQ4G0, n7); // bytes 0-3 of G0, 4-7 of G1
+    const uint32_t hi = __builtin_amdgcn_perm(kIQ4G3, kIQ4G2, n7);
+    const uint32_t pick = 0x03020100u + ((nib & 0x08080808u) >> 1); // byte i of lo or of hi
+    return __builtin_amdgcn_perm(hi, lo, pick);
+}
+
+__device__ __forceinline__ float iq4nl_dot(const uint8_t *row_lds, uint32_t off,
+                                           const SX<kIQ4_NL> &X)
+{
+    const float d = h2f(lds_read_u16(row_lds, off));
+    const uint32_t o = off + 2;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
+    const uint32_t sh = o & 3u;
+    uint32_t w[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) w[i] = p[i];
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh); // qs[4t..4t+3]
+        const uint32_t vl = opaque(iq4nl_lookup(q & 0x0f0f0f0fu));         // elements 4t + b
+        const uint32_t vh = opaque(iq4nl_lookup((q >> 4) & 0x0f0f0f0fu));  // elements 16 + 4t + b
+        a0 = fmaf(ubyte_f(vl, 0), X.x[4 * t + 0], a0);
+        a1 = fmaf(ubyte_f(vl, 1), X.x[4 * t + 1], a1);
+        a0 = fmaf(ubyte_f(vl, 2), X.x[4 * t + 2], a0);
+        a1 = fmaf(ubyte_f(vl, 3), X.x[4 * t + 3], a1);
+        a0 = fmaf(ubyte_f(vh, 0), X.x[16 + 4 * t + 0], a0);
+        a1 = fmaf(ubyte_f(vh, 1), X.x[16 + 4 * t + 1], a1);
+        a0 = fmaf(ubyte_f(vh, 2), X.x[16 + 4 * t + 2], a0);
+        a1 = fmaf(ubyte_f(vh, 3), X.x[16 + 4 * t + 3], a1);
+    }
+    return d * fmaf(-128.0f, X.s, a0 + a1);
 }
 
 // ---- greedy argmax partials ----------------------------------------------
@@ -675,6 +741,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
                     const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
                     if (bs < seg_blocks)
                         v = q6_dot(ring, slot + (uint32_t)(210 * bs), n, l0, X);
+                } else if constexpr (FMT == kIQ4_NL) {
+                    if (lane < seg_blocks)
+                        v = iq4nl_dot(ring + slot, 18u * lane, X);
                 } else {
                     if (lane < seg_blocks)
                         v = q80_dot(ring + slot, 34u * lane, X.x);
@@ -810,6 +879,7 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid);
     case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid);
     case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid);
+    case kIQ4_NL: return launch_stream<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid);
     default: return hipErrorInvalidValue;
     }
 }

@@ -6,10 +6,11 @@ from __future__ import annotations
 import numpy as np
 
 from . import _lib
-from ._lib import Q4_K, Q5_K, Q6_K, Q8_0, IHIPArgumentError, check, lib
+from ._lib import IQ4_NL, Q4_K, Q5_K, Q6_K, Q8_0, IHIPArgumentError, check, lib
 from .synth import BLOCK_BYTES, BLOCK_ELEMS
 
-__all__ = ["dequantize_q4_k", "dequantize_q5_k", "dequantize_q6_k", "dequantize_q8_0", "dequantize"]
+__all__ = ["dequantize_q4_k", "dequantize_q5_k", "dequantize_q6_k", "dequantize_q8_0",
+           "dequantize_iq4_nl", "dequantize"]
 
 
 def dequantize(ggml_type: int, data: np.ndarray, num_elements: int) -> np.ndarray:
@@ -39,3 +40,8 @@ def dequantize_q6_k(data, num_elements):
 
 def dequantize_q8_0(data, num_elements):
     return dequantize(Q8_0, data, num_elements)
+
+
+def dequantize_iq4_nl(data, num_elements):
+    """src/Dequant.jl:655-693: d * KVALUES_IQ4NL[nibble], 32 per 18-byte block."""
+    return dequantize(IQ4_NL, data, num_elements)

@@ -23,7 +23,7 @@ import ctypes
 import numpy as np
 
 from . import _lib
-from ._lib import Q4_K, Q5_K, Q6_K, Q8_0, IHIPArgumentError, check, lib
+from ._lib import IQ4_NL, Q4_K, Q5_K, Q6_K, Q8_0, IHIPArgumentError, check, lib
 from .synth import BLOCK_BYTES, BLOCK_ELEMS
 
 __all__ = ["quant_kernels_available", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
@@ -73,6 +73,13 @@ def q6_k_gemv_(out, weight_data, x, inner_dim, outer_dim):
 def q8_0_gemv_(out, weight_data, x, inner_dim, outer_dim):
     w, xp, op = _args(Q8_0, out, weight_data, x, inner_dim, outer_dim)
     check(lib().ihip_q8_0_gemv(w, xp, op, inner_dim, outer_dim))
+    return out
+
+
+def iq4_nl_gemv_(out, weight_data, x, inner_dim, outer_dim):
+    """mul_quant_mat_vec(::IQ4NL_Matrix, x, out) (src/ModelCPU.jl:381-408)."""
+    w, xp, op = _args(IQ4_NL, out, weight_data, x, inner_dim, outer_dim)
+    check(lib().ihip_iq4_nl_gemv(w, xp, op, inner_dim, outer_dim))
     return out
 
 

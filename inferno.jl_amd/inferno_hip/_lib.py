@@ -27,7 +27,7 @@ IHIP_ERR_DISABLED = -5
 IHIP_ERR_NOMEM = -6
 IHIP_ERR_EMPTY = -7
 
-Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL = 8, 12, 13, 14, 20
 FLAG_NAN, FLAG_POSINF, FLAG_ALL_NEGINF = 1, 2, 4
 ARGMAX_WS_BYTES = 262144
 Q8_K_BYTES = 292
@@ -65,6 +65,7 @@ SIGNATURES = {
     "ihip_q5_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q6_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q8_0_gemv": ([_vp, _vp, _vp, _i, _i], _i),
+    "ihip_iq4_nl_gemv": ([_vp, _vp, _vp, _i, _i], _i),
     "ihip_gguf_open": ([C.c_char_p, C.POINTER(_u64)], _i),
     "ihip_gguf_close": ([_u64], _i),
     "ihip_gguf_info": ([_u64, C.POINTER(C.c_uint32), C.POINTER(_u64), C.POINTER(_u64),

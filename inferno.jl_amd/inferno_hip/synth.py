@@ -20,10 +20,10 @@ from __future__ import annotations
 
 import numpy as np
 
-Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
-BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL = 8, 12, 13, 14, 20
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 18}
+BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_NL: 32}
+TYPE_NAMES = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_NL: "IQ4_NL"}
 
 
 def rng_for(seed: int) -> np.random.Generator:
@@ -67,7 +67,15 @@ def q8_0_blocks(rng: np.random.Generator, nblocks: int) -> np.ndarray:
     return b.reshape(-1)
 
 
-_GEN = {Q4_K: q4_k_blocks, Q5_K: q5_k_blocks, Q6_K: q6_k_blocks, Q8_0: q8_0_blocks}
+def iq4_nl_blocks(rng: np.random.Generator, nblocks: int) -> np.ndarray:
+    b = np.empty((nblocks, 18), dtype=np.uint8)
+    b[:, 0:2] = _half_bytes(np.abs(rng.standard_normal(nblocks)) * 0.0005)
+    b[:, 2:18] = rng.integers(0, 256, size=(nblocks, 16), dtype=np.uint8)
+    return b.reshape(-1)
+
+
+_GEN = {Q4_K: q4_k_blocks, Q5_K: q5_k_blocks, Q6_K: q6_k_blocks, Q8_0: q8_0_blocks,
+        IQ4_NL: iq4_nl_blocks}
 
 
 def weight(rng: np.random.Generator, ggml_type: int, outer: int, inner: int) -> np.ndarray:

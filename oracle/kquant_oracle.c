@@ -99,6 +99,7 @@ int orc_block_bytes(int type)
     case ORC_Q4_K: return 144;
     case ORC_Q5_K: return 176;
     case ORC_Q6_K: return 210;
+    case ORC_IQ4_NL: return 18;
     default: return 0;
     }
 }
@@ -106,7 +107,7 @@ int orc_block_bytes(int type)
 int orc_block_elems(int type)
 {
     switch (type) {
-    case ORC_Q8_0: return 32;
+    case ORC_Q8_0: case ORC_IQ4_NL: return 32;
     case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
     default: return 0;
     }
@@ -212,6 +213,20 @@ static void deq_q8_0_block(const uint8_t *b, float *y)
         y[j] = d * (float)(int8_t)b[2 + j];
 }
 
+/* src/Dequant.jl:683-693 (dequantize_iq4_nl_into!): y[j] = d *
+ * KVALUES_IQ4NL[qs[j] & 15], y[j + 16] = d * KVALUES_IQ4NL[qs[j] >> 4]
+ * (the grid is src/QuantsData.jl:384). */
+static void deq_iq4_nl_block(const uint8_t *b, float *y)
+{
+    static const int8_t kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+    const float d = orc_half_to_float(rd16(b));
+    for (int j = 0; j < 16; ++j) {
+        y[j] = d * (float)kv[b[2 + j] & 15];
+        y[j + 16] = d * (float)kv[b[2 + j] >> 4];
+    }
+}
+
 typedef void (*deq_fn)(const uint8_t *, float *);
 
 static deq_fn deq_for(int type)
@@ -221,6 +236,7 @@ static deq_fn deq_for(int type)
     case ORC_Q4_K: return deq_q4_k_block;
     case ORC_Q5_K: return deq_q5_k_block;
     case ORC_Q6_K: return deq_q6_k_block;
+    case ORC_IQ4_NL: return deq_iq4_nl_block;
     default: return NULL;
     }
 }

@@ -37,6 +37,7 @@ enum {
     ORC_Q4_K = 12,
     ORC_Q5_K = 13,
     ORC_Q6_K = 14,
+    ORC_IQ4_NL = 20,
 };
 
 float    orc_half_to_float(uint16_t h);

@@ -72,6 +72,8 @@ def test_dequant_all_half_patterns_bit_exact():
     (synth.Q6_K, 3, 768),       # 9 blocks: not a multiple of 8 -> generic path
     (synth.Q8_0, 5, 96),        # 15 blocks -> generic path
     (synth.Q4_K, 1, 256),
+    (synth.IQ4_NL, 1024, 4096),
+    (synth.IQ4_NL, 3, 96),
 ])
 def test_dequant_bit_exact(t, outer, inner):
     say(f"dequant type={t} {outer}x{inner}")
@@ -83,7 +85,7 @@ def test_dequant_bit_exact(t, outer, inner):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0])
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0, synth.IQ4_NL])
 def test_dequant_host_entry_point_and_misaligned_source(t):
     say(f"Dequant host mirror type={t}")
     from inferno_hip import Dequant, device as D
@@ -101,6 +103,36 @@ def test_dequant_host_entry_point_and_misaligned_source(t):
     assert np.array_equal(got2.view(np.uint32), want.view(np.uint32))
 
 
+def test_dequant_iq4_nl_reference_known_answers():
+    """The IQ4_NL cases of the reference's tests/unit/core_components.jl:177-205."""
+    from inferno_hip import Dequant
+    blocks = np.zeros((4, 18), np.uint8)
+    for i, (d_bits, qs0) in enumerate(((0x3C00, 0), (0x3C00, 0x18), (0x4000, 0x18),
+                                       (0x3C00, 0b1110_1011))):
+        blocks[i, 0:2] = np.array([d_bits], np.uint16).view(np.uint8)
+        blocks[i, 2] = qs0
+    say("IQ4_NL known answers")
+    y = Dequant.dequantize_iq4_nl(blocks.reshape(-1), 128).reshape(4, 32)
+    assert np.all(y[0] == -127.0)
+    assert (y[1, 0], y[1, 16], y[1, 15], y[1, 31]) == (1.0, -104.0, -127.0, -127.0)
+    assert (y[2, 0], y[2, 16]) == (2.0, -208.0)
+    assert (y[3, 0], y[3, 16]) == (38.0, 89.0)
+
+
+def test_iq4_nl_gemv_host_mirror():
+    from inferno_hip import QuantizedKernels as QK
+    rng = synth.rng_for(0x1A4)
+    outer, inner = 257, 1024
+    w = synth.weight(rng, synth.IQ4_NL, outer, inner)
+    x = synth.activations(rng, inner)
+    say("iq4_nl_gemv_ host mirror")
+    out = np.zeros(outer, np.float32)
+    QK.iq4_nl_gemv_(out, w, x, inner, outer)
+    ref = oracle.gemv_f64(synth.IQ4_NL, w, x, inner, outer)
+    assert_within(out, ref, oracle.tolerance(oracle.row_norms(synth.IQ4_NL, w, inner, outer), x),
+                  "IQ4_NL host mirror")
+
+
 # ---------------------------------------------------------------- GEMV ----
 
 GEMV_CASES = [
@@ -116,6 +148,10 @@ GEMV_CASES = [
     (synth.Q8_0, 4096, 4096),
     (synth.Q8_0, 11, 2304),       # partial 64-block segment
     (synth.Q8_0, 6, 96),          # generic kernel
+    (synth.IQ4_NL, 2048, 1024),   # an SSM-projection-sized IQ4_NL matrix
+    (synth.IQ4_NL, 1000, 4096),   # two 64-block segments per row
+    (synth.IQ4_NL, 13, 2304),     # partial segment (72 blocks)
+    (synth.IQ4_NL, 5, 96),        # generic kernel
 ]
 
 

@@ -313,3 +313,26 @@ def test_ffn_block_oracle_is_norm_then_ffn_then_residual():
                                            n.astype(np.float32), hidden, inter)
     nrm = oracle.row_norms(dt, wd, inter, hidden)
     assert np.all(np.abs((y - x) - y2) <= 1e-5 * nrm * np.linalg.norm(h2))
+
+
+# ---- IQ4_NL (src/Dequant.jl:655-693; grid src/QuantsData.jl:384) ----
+
+def test_iq4_nl_oracle_reference_known_answers():
+    """tests/unit/core_components.jl:177-205 of the reference, case by case."""
+    def block(d_bits, qs0):
+        b = np.zeros(18, np.uint8)
+        b[0:2] = np.array([d_bits], np.uint16).view(np.uint8)
+        b[2] = qs0
+        return b
+    y = oracle.dequant(synth.IQ4_NL, block(0x3C00, 0), 32)
+    assert np.all(y == np.float32(-127.0))
+    y = oracle.dequant(synth.IQ4_NL, block(0x3C00, 0x18), 32)
+    assert (y[0], y[16], y[15], y[31]) == (1.0, -104.0, -127.0, -127.0)
+    y = oracle.dequant(synth.IQ4_NL, block(0x4000, 0x18), 32)
+    assert (y[0], y[16]) == (2.0, -208.0)
+    y = oracle.dequant(synth.IQ4_NL, block(0x3C00, 0b1110_1011), 32)
+    assert (y[0], y[16]) == (38.0, 89.0)
+    # the whole grid, in nibble order, sorted and distinct (the reference's
+    # table checks, core_components.jl:254-256)
+    grid = [oracle.dequant(synth.IQ4_NL, block(0x3C00, v), 32)[0] for v in range(16)]
+    assert grid[0] == -127 and grid[-1] == 113 and grid == sorted(grid) and len(set(grid)) == 16
