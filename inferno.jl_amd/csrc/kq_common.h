@@ -75,6 +75,25 @@ __device__ __forceinline__ float wave_sum(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Unsigned maximum over the 64 lanes of a wavefront (the wave_sum pattern
+// with max; lanes a DPP move does not write contribute 0).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v)
+{
+    const uint32_t moved = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+    return v > moved ? v : moved;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = dpp_max_u32<0xb1, 0xf>(v);
+    v = dpp_max_u32<0x4e, 0xf>(v);
+    v = dpp_max_u32<0x141, 0xf>(v);
+    v = dpp_max_u32<0x140, 0xf>(v);
+    v = dpp_max_u32<0x142, 0xa>(v);
+    v = dpp_max_u32<0x143, 0xc>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Read 8 bytes starting at byte `off` of a 4-byte-aligned LDS array as two
 // dwords.  The dword reads stay 4-byte aligned; the byte phase (off & 3) is
 // taken out with v_alignbyte.  `off` must be relative to the aligned array

@@ -68,13 +68,15 @@ constexpr int kXPadFloats = 4096 + 4096 / 64 * 4;
 __device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
 
 // Stage x[col0, col0 + 4096) (zeros past `inner`) and its 128 sub-block sums.
-// `xv` holds this thread's four float4 of x, loaded by the caller.
-__device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&xv)[4])
+// `xv` holds this thread's float4s of x (NT threads: 1024 / NT each), loaded
+// by the caller.
+template <int NT>
+__device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&xv)[1024 / NT])
 {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = 4 * (tid + 256 * k);
+    for (int k = 0; k < 1024 / NT; ++k) {
+        const int i = 4 * (tid + NT * k);
         *reinterpret_cast<float4 *>(xs + xpad(i)) = xv[k];
         // 8 consecutive threads hold one 32-element sub-block
         float t = (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w);
@@ -82,16 +84,17 @@ __device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&x
         t = dpp_add<0x4e, 0xf>(t);  // quads
         t = dpp_add<0x141, 0xf>(t); // 8 lanes (row_half_mirror)
         if ((tid & 7) == 0)
-            xsum[(tid + 256 * k) >> 3] = t;
+            xsum[(tid + NT * k) >> 3] = t;
     }
 }
 
+template <int NT>
 __device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col0, int inner,
-                                            float4 (&xv)[4])
+                                            float4 (&xv)[1024 / NT])
 {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int col = col0 + 4 * (threadIdx.x + 256 * k);
+    for (int k = 0; k < 1024 / NT; ++k) {
+        const int col = col0 + 4 * (threadIdx.x + NT * k);
         xv[k] = col < inner ? *reinterpret_cast<const float4 *>(x + col)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -199,18 +202,185 @@ __device__ __forceinline__ float kwide_dot(const KBytes &B, int j, const XWide &
     return fmaf(d, pos, -(dmin * neg));
 }
 
+// ---- integer-digit activations -------------------------------------------
+// The dot of a lane's nibbles with x can run on the integer dot units
+// (v_dot4_{u32_u8,i32_i8}: four byte products and the accumulate in one
+// instruction) when x is written as an integer.  Each 32-element sub-block of
+// x is scaled by 2^(22-e), e the binary exponent of the sub-block's largest
+// |x| (|x| < 2^e), and truncated to an integer X with |X| < 2^22: the error of
+// x ~ X * 2^(e-22) is below 2^(e-22) <= |x|max * 2^-21, so a dot product of n
+// such values is off by less than sqrt(n) * 2^-21 * ||w||_2 ||x||_2 (3.1e-5
+// relative at n = 4096, against the 1e-4 row bound, whatever the data; about
+// 1e-7 for random data).  X is split into three byte digits,
+// X = 65536 * b2 + 256 * b1 + b0 (b0, b1 unsigned, b2 signed); the products
+// q * b are exact integers, so the per-sub-block sums are exact and
+// independent of summation order.  A sub-block holding a non-finite value has
+// its fp32 sum (which every row's dmin term multiplies) set to NaN, so the
+// outputs it reaches are NaN.
+struct XDig {
+    uint32_t p[3][16]; // digit planes; dwords 0..7 the lane's low-nibble elements, 8..15 high
+    float sa, sb;      // fp32 sums of the two sub-blocks of x (the dmin term)
+    int ea, eb;        // their exponents
+};
+
+// Plane layout in LDS: dword g holds digit p of elements 4g..4g+3, with 4
+// dwords of padding after every 16 so a lane's 16-dword reads (lanes 16
+// dwords apart) fall on distinct banks.
+constexpr int kDigPlaneDw = 1024 + 1024 / 16 * 4;
+__device__ __forceinline__ int dpad(int g) { return g + ((g >> 4) << 2); }
+
+// Byte digits of X0..X3 -> one dword per plane (digit p of element i in byte i).
+__device__ __forceinline__ void dig_pack(int X0, int X1, int X2, int X3, uint32_t &d0,
+                                         uint32_t &d1, uint32_t &d2)
+{
+    const uint32_t p01 = __builtin_amdgcn_perm(X1, X0, 0x05010400u); // X0.b0 X1.b0 X0.b1 X1.b1
+    const uint32_t p23 = __builtin_amdgcn_perm(X3, X2, 0x05010400u);
+    const uint32_t q01 = __builtin_amdgcn_perm(X1, X0, 0x0c0c0602u); // X0.b2 X1.b2 0 0
+    const uint32_t q23 = __builtin_amdgcn_perm(X3, X2, 0x0c0c0602u);
+    d0 = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+    d1 = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
+    d2 = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
+}
+
+// Digits of four elements that share exponent e (finite == false: zeros).
+__device__ __forceinline__ void dig_four(float4 v, int e, bool finite, uint32_t &d0, uint32_t &d1,
+                                         uint32_t &d2)
+{
+    const int sh = 22 - e;
+    const int X0 = finite ? (int)__builtin_ldexpf(v.x, sh) : 0;
+    const int X1 = finite ? (int)__builtin_ldexpf(v.y, sh) : 0;
+    const int X2 = finite ? (int)__builtin_ldexpf(v.z, sh) : 0;
+    const int X3 = finite ? (int)__builtin_ldexpf(v.w, sh) : 0;
+    dig_pack(X0, X1, X2, X3, d0, d1, d2);
+}
+
+// |x| bits of four elements, maxed: NaN > +Inf > every finite value.
+__device__ __forceinline__ uint32_t abs_bits_max(float4 v)
+{
+    const uint32_t m01 = max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu);
+    const uint32_t m23 = max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu);
+    return max(m01, m23);
+}
+
+// Stage the digits of x[col0, col0 + 4096), its 128 sub-block sums and their
+// exponents.  Thread t (of NT) holds float4 k of elements 4(t + NT k): 8
+// consecutive threads hold one 32-element sub-block, reduced with three DPP
+// steps.
+template <int NT>
+__device__ __forceinline__ void x_stage_dig(uint32_t *pl, float *xsum, int *xexp,
+                                            const float4 (&xv)[1024 / NT])
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 1024 / NT; ++k) {
+        const float4 v = xv[k];
+        float t = (v.x + v.y) + (v.z + v.w);
+        uint32_t m = abs_bits_max(v);
+        t = dpp_add<0xb1, 0xf>(t);
+        m = dpp_max_u32<0xb1, 0xf>(m);
+        t = dpp_add<0x4e, 0xf>(t);
+        m = dpp_max_u32<0x4e, 0xf>(m);
+        t = dpp_add<0x141, 0xf>(t);
+        m = dpp_max_u32<0x141, 0xf>(m);
+        const bool finite = m < 0x7f800000u;
+        const int e = finite ? __builtin_amdgcn_frexp_expf(__uint_as_float(m)) : 0;
+        uint32_t d0, d1, d2;
+        dig_four(v, e, finite, d0, d1, d2);
+        const int g = dpad(tid + NT * k);
+        pl[g] = d0;
+        pl[kDigPlaneDw + g] = d1;
+        pl[2 * kDigPlaneDw + g] = d2;
+        if ((tid & 7) == 0) {
+            const int sb = (tid + NT * k) >> 3;
+            xsum[sb] = finite ? t : __builtin_nanf("");
+            xexp[sb] = e;
+        }
+    }
+}
+
+__device__ __forceinline__ void x_from_lds_dig(const uint32_t *pl, const float *xsum,
+                                               const int *xexp, int b, int j, XDig &X)
+{
+    const int g0 = dpad(64 * b + 16 * j); // 16 contiguous dwords
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(pl + p * kDigPlaneDw + g0 + 4 * t);
+            X.p[p][4 * t + 0] = v.x; X.p[p][4 * t + 1] = v.y;
+            X.p[p][4 * t + 2] = v.z; X.p[p][4 * t + 3] = v.w;
+        }
+    const float2 s2 = *reinterpret_cast<const float2 *>(xsum + 8 * b + 2 * j);
+    const int2 e2 = *reinterpret_cast<const int2 *>(xexp + 8 * b + 2 * j);
+    X.sa = s2.x;
+    X.sb = s2.y;
+    X.ea = e2.x;
+    X.eb = e2.y;
+}
+
+// Exact digit sums S0, S1 (unsigned planes) and S2 (signed) of one sub-block
+// -> 65536 * S2 + 256 * S1 + S0 in fp32.  |S2| <= 32 * 63 * 64 and
+// S0, S1 <= 32 * 63 * 255 for 6-bit weights, so 256 * S2 + S1 is an exact
+// fp32 integer (< 2^24) and the combine rounds once.
+__device__ __forceinline__ float dig_combine(uint32_t s0, uint32_t s1, int s2)
+{
+    return fmaf((float)(int)(((uint32_t)s2 << 8) + s1), 256.0f, (float)s0);
+}
+
+// One lane's contribution to one row with digit activations: the same sum as
+// kwide_dot.
+template <int FMT>
+__device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
+{
+    const uint32_t qw[8] = {B.q0.x, B.q0.y, B.q0.z, B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w};
+    uint32_t a0 = 0, a1 = 0, c0 = 0, c1 = 0;
+    int a2 = 0, c2 = 0;
+    uint32_t ew[8];
+    if constexpr (FMT == kQ5_K) {
+        const uint32_t sh = 2 * j;
+        const uint32_t e[8] = {B.e0.x, B.e0.y, B.e0.z, B.e0.w, B.e1.x, B.e1.y, B.e1.z, B.e1.w};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) ew[t] = e[t] >> sh;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        uint32_t lo = qw[t] & 0x0f0f0f0fu;
+        uint32_t hi = (qw[t] >> 4) & 0x0f0f0f0fu;
+        if constexpr (FMT == kQ5_K) {
+            lo |= (ew[t] & 0x01010101u) << 4;
+            hi |= (ew[t] & 0x02020202u) << 3;
+        }
+        a0 = __builtin_amdgcn_udot4(lo, X.p[0][t], a0, false);
+        a1 = __builtin_amdgcn_udot4(lo, X.p[1][t], a1, false);
+        a2 = __builtin_amdgcn_sdot4((int)lo, (int)X.p[2][t], a2, false);
+        c0 = __builtin_amdgcn_udot4(hi, X.p[0][8 + t], c0, false);
+        c1 = __builtin_amdgcn_udot4(hi, X.p[1][8 + t], c1, false);
+        c2 = __builtin_amdgcn_sdot4((int)hi, (int)X.p[2][8 + t], c2, false);
+    }
+    const float vA = dig_combine(a0, a1, a2), vB = dig_combine(c0, c1, c2);
+    const float d = h2f(B.h.x & 0xffffu), dmin = h2f(B.h.x >> 16);
+    float scA, mA, scB, mB;
+    k_scale_min_pair(B.h.y, B.h.z, B.h.w, j, scA, mA, scB, mB);
+    // ldexp after the product: exact scaling, gradual underflow for tiny x
+    const float pos = __builtin_ldexpf(scA * vA, X.ea - 22) + __builtin_ldexpf(scB * vB, X.eb - 22);
+    const float neg = fmaf(mA, X.sa, mB * X.sb);
+    return fmaf(d, pos, -(dmin * neg));
+}
+
 // Plain GEMV (GATEUP == false) or fused gate/up + SwiGLU (GATEUP == true:
 // W2 is the up weight, y[r] = silu(g[r]) * u[r]).  Wave w of workgroup g
-// owns rows [(4g + w) R, (4g + w + 1) R); rows past `outer` re-read the last
-// row and are not stored.
+// (NWV waves) owns rows [(NWV g + w) R, (NWV g + w + 1) R); rows past `outer`
+// re-read the last row and are not stored.
 //
-// nw != nullptr: the input is rmsnorm(x) .* nw (rmsnorm_cpu!,
-// src/ModelCPU.jl:111-123).  x .* nw is staged instead of x and the row sums
-// are multiplied by 1/sqrt(mean(x^2) + eps) at the end, so the norm costs no
-// extra pass.  resid != nullptr (plain GEMV): y[r] = resid[r] + (W x)[r], the
-// residual add of src/ModelCPU.jl:913-920 (resid may be y itself).
-template <int FMT, int R, bool GATEUP>
-__global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ W,
+// EXT selects an optional neighbour at compile time (a runtime test would
+// cost a branch at the head of every wave):
+//   GATEUP: the input is rmsnorm(x) .* nw (rmsnorm_cpu!, src/ModelCPU.jl:111-123).
+//     x .* nw is staged instead of x and the row sums are multiplied by
+//     1/sqrt(mean(x^2) + eps) at the end, so the norm costs no extra pass.
+//   plain: y[r] = resid[r] + (W x)[r], the residual add of
+//     src/ModelCPU.jl:913-920 (resid may be y itself).
+template <int FMT, int R, bool GATEUP, bool DIG, bool EXT, int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restrict__ W,
                                                     const uint8_t *__restrict__ W2,
                                                     const float *__restrict__ x,
                                                     float *y, int outer, int nblk,
@@ -219,12 +389,17 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
 {
     using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
-    __shared__ __attribute__((aligned(16))) float xs[kXPadFloats];
+    constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
+    constexpr int NT = NWV * 64, NXV = 1024 / NT;
+    // fp32 x (kXPadFloats) or its three digit planes (3 * kDigPlaneDw dwords)
+    __shared__ __attribute__((aligned(16))) uint32_t xbuf[DIG ? 3 * kDigPlaneDw : kXPadFloats];
     __shared__ __attribute__((aligned(16))) float xsum[128];
+    __shared__ __attribute__((aligned(8))) int xexp[DIG ? 128 : 1];
+    float *xs = reinterpret_cast<float *>(xbuf);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
-    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int row0 = (blockIdx.x * NWV + wave) * R;
     const int b = lane >> 2, j = lane & 3;
     const int inner = nblk * 256;
     const size_t row_bytes = (size_t)nblk * F::BYTES;
@@ -235,23 +410,23 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
 
-    float ssq = 0.0f; // this thread's share of sum(x^2) (nw != nullptr)
+    float ssq = 0.0f; // this thread's share of sum(x^2) (NORM)
     float rv[R];      // residuals of this wave's rows, loaded ahead of the weights
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        rv[r] = resid ? resid[min(row0 + r, outer - 1)] : 0.0f;
+        rv[r] = RESID ? resid[min(row0 + r, outer - 1)] : 0.0f;
     const int npass = (nblk + 15) >> 4;
     for (int pass = 0; pass < npass; ++pass) {
         const int nb = min(16, nblk - pass * 16);
         const bool active = b < nb;
         const int blk = pass * 16 + (active ? b : 0);
-        float4 xv[4];
-        x_load_pass(x, pass * 4096, inner, xv);
-        if (nw) { // wave-uniform
-            float4 wv[4];
-            x_load_pass(nw, pass * 4096, inner, wv);
+        float4 xv[NXV];
+        x_load_pass<NT>(x, pass * 4096, inner, xv);
+        if constexpr (NORM) {
+            float4 wv[NXV];
+            x_load_pass<NT>(nw, pass * 4096, inner, wv);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < NXV; ++k) {
                 ssq = fmaf(xv[k].x, xv[k].x, ssq);
                 ssq = fmaf(xv[k].y, xv[k].y, ssq);
                 ssq = fmaf(xv[k].z, xv[k].z, ssq);
@@ -262,11 +437,11 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
         }
         KBytes B[NW][R];
 #pragma unroll
-        for (int m = 0; m < NW; ++m) {
-            const uint8_t *Wm = m == 0 ? W : W2;
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, outer - 1);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = min(row0 + r, outer - 1);
+            for (int m = 0; m < NW; ++m) {
+                const uint8_t *Wm = m == 0 ? W : W2;
                 kbytes_load<FMT>(Wm + (size_t)row * row_bytes + (size_t)blk * F::BYTES, j, B[m][r]);
             }
         }
@@ -274,26 +449,47 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
         __builtin_amdgcn_sched_barrier(0);
         if (pass > 0)
             __syncthreads(); // the previous pass is done with xs / xsum
-        x_stage(xs, xsum, xv);
-        __syncthreads();
-        XWide X;
-        x_from_lds(xs, xsum, b, j, X);
+        if constexpr (DIG) {
+            x_stage_dig<NT>(xbuf, xsum, xexp, xv);
+            __syncthreads();
+            XDig X;
+            x_from_lds_dig(xbuf, xsum, xexp, b, j, X);
+            // rows one after the other, in load order: row r is reduced as soon as
+            // its own bytes have landed instead of after every row's
 #pragma unroll
-        for (int m = 0; m < NW; ++m)
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float c = kwide_dot<FMT>(B[m][r], j, X);
-                acc[m][r] += active ? c : 0.0f;
-            }
+                for (int m = 0; m < NW; ++m) {
+                    const float c = kdig_dot<FMT>(B[m][r], j, X);
+                    acc[m][r] += active ? c : 0.0f;
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        } else {
+            x_stage<NT>(xs, xsum, xv);
+            __syncthreads();
+            XWide X;
+            x_from_lds(xs, xsum, b, j, X);
+#pragma unroll
+            for (int m = 0; m < NW; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float c = kwide_dot<FMT>(B[m][r], j, X);
+                    acc[m][r] += active ? c : 0.0f;
+                }
+        }
     }
     float scale = 1.0f;
-    if (nw) { // wave-uniform: every wave takes part in the barrier
-        __shared__ float ssw[4];
+    if constexpr (NORM) { // every wave takes part in the barrier
+        __shared__ float ssw[NWV];
         const float t = wave_sum(ssq);
         if (lane == 0)
             ssw[wave] = t;
         __syncthreads();
-        scale = 1.0f / sqrtf(((ssw[0] + ssw[1]) + (ssw[2] + ssw[3])) / (float)inner + eps);
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; ++i)
+            tot += ssw[i];
+        scale = 1.0f / sqrtf(tot / (float)inner + eps);
     }
     if (row0 >= outer)
         return; // wave-uniform, after the last barrier
@@ -308,7 +504,7 @@ __global__ __launch_bounds__(256) void k_gemv_kwide(const uint8_t *__restrict__ 
         }
         const int row = row0 + r;
         if (lane == 0 && row < outer)
-            y[row] = resid ? rv[r] + v : v;
+            y[row] = RESID ? rv[r] + v : v;
     }
 }
 
@@ -798,12 +994,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
 static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 2)
 static int g_rows_gateup = 0; // fused gate/up (default 1)
 static int g_stream_rows = 0; // Q6_K/Q8_0 rows per chunk (default: see stream_rows())
+static int g_wide_fp32 = 0;   // Q4_K/Q5_K: 1 = fp32 activations instead of integer digits
+static int g_wide_waves = 0;  // Q4_K/Q5_K waves per workgroup (4 or 8; default 8)
 
 void set_tuning(const char *name, int value)
 {
     if (!__builtin_strcmp(name, "rows_wide")) g_rows_wide = value;
     if (!__builtin_strcmp(name, "rows_gateup")) g_rows_gateup = value;
     if (!__builtin_strcmp(name, "stream_rows")) g_stream_rows = value;
+    if (!__builtin_strcmp(name, "wide_fp32")) g_wide_fp32 = value;
+    if (!__builtin_strcmp(name, "wide_waves")) g_wide_waves = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -817,18 +1017,27 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
         R = GATEUP ? 1 : 2;
     if (FMT == kQ5_K && GATEUP && R > 2)
         R = 2; // register budget
-#define IHIP_KW(RR)                                                                          \
-    case RR:                                                                                 \
-        hipLaunchKernelGGL((k_gemv_kwide<FMT, RR, GATEUP>),                                  \
-                           dim3((outer + 4 * RR - 1) / (4 * RR)), dim3(256), 0, s,            \
-                           (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid); \
-        break;
-    switch (R) {
-        IHIP_KW(1)
-        IHIP_KW(4)
-    default:
-        IHIP_KW(2)
+    const bool dig = g_wide_fp32 <= 0;
+    const bool ext = GATEUP ? nw != nullptr : resid != nullptr;
+    const int nwv = g_wide_waves == 4 ? 4 : 8;
+#define IHIP_KW(RR, DG, EX, NV)                                                              \
+    hipLaunchKernelGGL((k_gemv_kwide<FMT, RR, GATEUP, DG, EX, NV>),                          \
+                       dim3((outer + NV * RR - 1) / (NV * RR)), dim3(NV * 64), 0, s,          \
+                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid)
+#define IHIP_KW_R(DG, EX)                                                                    \
+    do {                                                                                     \
+        if (nwv == 8) {                                                                      \
+            if (R == 1) IHIP_KW(1, DG, EX, 8); else if (R == 4) IHIP_KW(4, DG, EX, 8); else IHIP_KW(2, DG, EX, 8); \
+        } else {                                                                             \
+            if (R == 1) IHIP_KW(1, DG, EX, 4); else if (R == 4) IHIP_KW(4, DG, EX, 4); else IHIP_KW(2, DG, EX, 4); \
+        }                                                                                    \
+    } while (0)
+    if (dig) {
+        if (ext) IHIP_KW_R(true, true); else IHIP_KW_R(true, false);
+    } else {
+        if (ext) IHIP_KW_R(false, true); else IHIP_KW_R(false, false);
     }
+#undef IHIP_KW_R
 #undef IHIP_KW
     return hipGetLastError();
 }

@@ -198,6 +198,11 @@ TUNING_CASES = [
     ("rows_wide", r, t, outer, inner)
     for r in (1, 2, 4) for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608))
 ] + [
+    # Q4_K/Q5_K: fp32 activations instead of integer digits; four waves per workgroup
+    (knob, 1 if knob == "wide_fp32" else 4, t, outer, inner)
+    for knob in ("wide_fp32", "wide_waves")
+    for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608), (synth.Q4_K, 9, 8448))
+] + [
     # streamed Q6_K / Q8_0 kernel: rows per chunk x (waves per workgroup = segments, up to 8;
     # 12 and 5 segments give waves that own two segments)
     ("stream_rows", r, t, outer, inner)
@@ -245,6 +250,64 @@ def test_gate_up_every_kernel_variant(value, t):
     u = oracle.gemv_f64(t, wu, x, hidden, inter)
     hb = _h_bound(g, u, oracle.row_norms(t, wg, hidden, inter), oracle.row_norms(t, wu, hidden, inter), x)
     assert_within(h, g / (1 + np.exp(-g)) * u, hb, "h")
+
+
+@pytest.mark.parametrize("fp32", [0, 1])
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0])
+def test_gemv_activation_dynamic_range(t, fp32):
+    """Sub-blocks of x spread over 10^-30 .. 10^30 (fp32 subnormals included):
+    the integer-digit activations scale every 32-element sub-block on its own,
+    so small sub-blocks next to huge ones keep their precision."""
+    from inferno_hip import _lib, device as D
+    rng = synth.rng_for(777 + t + 5 * fp32)
+    outer, inner = 96, 4096
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner).astype(np.float64)
+    x *= np.repeat(10.0 ** rng.uniform(-30, 30, inner // 32), 32)
+    x[:32] *= 1e-10  # a subnormal sub-block
+    x = x.astype(np.float32)
+    say(f"dynamic range type={t} fp32={fp32}")
+    _lib.set_tuning("wide_fp32", fp32)
+    try:
+        y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
+    finally:
+        _lib.set_tuning("wide_fp32", 0)
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
+    assert_within(y, ref, tol, f"type {t} dynamic range")
+    # the small sub-blocks alone (the large ones zeroed) are not lost either
+    xs = np.where(np.abs(x) < 1e-20, x, 0).astype(np.float32)
+    _lib.set_tuning("wide_fp32", fp32)
+    try:
+        ys = D.gemv(dweight(w, t, inner, outer), dev(xs)).cpu().numpy()
+    finally:
+        _lib.set_tuning("wide_fp32", 0)
+    refs = oracle.gemv_f64(t, w, xs, inner, outer)
+    tols = oracle.tolerance(oracle.row_norms(t, w, inner, outer), xs)
+    assert_within(ys, refs, tols, f"type {t} small sub-blocks only")
+
+
+@pytest.mark.parametrize("fp32", [0, 1])
+def test_gemv_nonfinite_activations(fp32):
+    """A NaN or an infinity in x makes every output non-finite (the fp32 sum
+    of the reference gives +-Inf or NaN per row; the integer-digit path gives
+    NaN for all of them)."""
+    from inferno_hip import _lib, device as D
+    rng = synth.rng_for(4343)
+    outer, inner = 64, 4096
+    for t in (synth.Q4_K, synth.Q5_K):
+        w = synth.weight(rng, t, outer, inner)
+        dw = dweight(w, t, inner, outer)
+        for bad in (np.nan, np.inf, -np.inf):
+            x = synth.activations(rng, inner)
+            x[1234] = bad
+            say(f"nonfinite type={t} fp32={fp32} x[1234]={bad}")
+            _lib.set_tuning("wide_fp32", fp32)
+            try:
+                y = D.gemv(dw, dev(x)).cpu().numpy()
+            finally:
+                _lib.set_tuning("wide_fp32", 0)
+            assert not np.any(np.isfinite(y)), (t, bad)
 
 
 def test_gemv_special_inputs():
