@@ -508,6 +508,141 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
     }
 }
 
+// Persistent form of the digit kernel for matrices of many rows and at most
+// 4096 columns (one pass): a workgroup per CU stages x's digits once, each
+// lane keeps its 48 digit dwords in registers, and every wave walks row
+// groups grid-stride with NB register buffers, so the loads of the next
+// NB - 1 groups are in flight while a group is reduced (HBM latency under
+// load is a microsecond or more, several group reductions).  A group is R
+// rows (GATEUP: R gate rows and the same R up rows).  Same outputs as
+// k_gemv_kwide<FMT, R, GATEUP, true, EXT, NWV>.
+template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restrict__ W,
+                                                         const uint8_t *__restrict__ W2,
+                                                         const float *__restrict__ x,
+                                                         float *y, int outer, int nblk,
+                                                         const float *__restrict__ nw, float eps,
+                                                         const float *resid)
+{
+    using F = KFmt<FMT>;
+    constexpr int NM = GATEUP ? 2 : 1;
+    constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
+    constexpr int NT = NWV * 64, NXV = 1024 / NT;
+    __shared__ __attribute__((aligned(16))) uint32_t xbuf[3 * kDigPlaneDw];
+    __shared__ __attribute__((aligned(16))) float xsum[128];
+    __shared__ __attribute__((aligned(8))) int xexp[128];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = lane >> 2, j = lane & 3;
+    const bool active = b < nblk;
+    const int blk = active ? b : 0;
+    const int inner = nblk * 256;
+    const size_t row_bytes = (size_t)nblk * F::BYTES;
+    const int ngroups = (outer + R - 1) / R;
+    const int stride = gridDim.x * NWV;
+    const int g0 = blockIdx.x * NWV + wave;
+
+    // weights (and the residuals) of group gi into one register buffer
+    auto load = [&](KBytes (&B)[NM][R], float (&RV)[R], int gi) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(gi * R + r, outer - 1);
+            if constexpr (RESID)
+                RV[r] = resid[row]; // wave-uniform: a scalar load
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+                kbytes_load<FMT>((m == 0 ? W : W2) + (size_t)row * row_bytes + (size_t)blk * F::BYTES,
+                                 j, B[m][r]);
+        }
+    };
+
+    float4 xv[NXV];
+    x_load_pass<NT>(x, 0, inner, xv);
+    float ssq = 0.0f;
+    if constexpr (NORM) {
+        float4 wv[NXV];
+        x_load_pass<NT>(nw, 0, inner, wv);
+#pragma unroll
+        for (int k = 0; k < NXV; ++k) {
+            ssq = fmaf(xv[k].x, xv[k].x, ssq);
+            ssq = fmaf(xv[k].y, xv[k].y, ssq);
+            ssq = fmaf(xv[k].z, xv[k].z, ssq);
+            ssq = fmaf(xv[k].w, xv[k].w, ssq);
+            xv[k] = make_float4(xv[k].x * wv[k].x, xv[k].y * wv[k].y, xv[k].z * wv[k].z,
+                                xv[k].w * wv[k].w);
+        }
+    }
+    KBytes B[NB][NM][R];
+    float RV[NB][R];
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+        load(B[q], RV[q], min(g0 + q * stride, ngroups - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    x_stage_dig<NT>(xbuf, xsum, xexp, xv);
+    float scale = 1.0f;
+    if constexpr (NORM) {
+        __shared__ float ssw[NWV];
+        const float t = wave_sum(ssq);
+        if (lane == 0)
+            ssw[wave] = t;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; ++i)
+            tot += ssw[i];
+        scale = 1.0f / sqrtf(tot / (float)inner + eps);
+    } else {
+        __syncthreads();
+    }
+    XDig X;
+    x_from_lds_dig(xbuf, xsum, xexp, b, j, X);
+
+    auto reduce = [&](const KBytes (&Bq)[NM][R], const float (&RVq)[R], int gi) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = gi * R + r;
+            float v[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const float c = kdig_dot<FMT>(Bq[m][r], j, X);
+                v[m] = wave_sum(active ? c : 0.0f) * scale;
+            }
+            float o = v[0];
+            if constexpr (GATEUP)
+                o = (v[0] / (1.0f + expf(-v[0]))) * v[1]; // src/ModelCPU.jl:492-503
+            // every lane holds the row's value: an unpredicated store (a row
+            // past `outer` re-reads and rewrites row outer - 1 with its own value)
+            y[min(row, outer - 1)] = RESID ? RVq[r] + o : o;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Steady state without predicated loads, so the compiler's vmcnt waits
+    // stay exact (a load under a branch makes it wait for every load in
+    // flight): every buffer is refilled with a group that exists.
+    int gi = g0;
+    for (; gi + (2 * NB - 1) * stride < ngroups; gi += NB * stride) { // wave-uniform
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            reduce(B[q], RV[q], gi + q * stride);
+            load(B[q], RV[q], gi + (q + NB) * stride);
+        }
+    }
+    // the tail: buffer q holds group gi + q stride; refill only with groups that exist
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+        if (gi + q * stride < ngroups)
+            reduce(B[q], RV[q], gi + q * stride);
+        if (gi + (q + NB) * stride < ngroups)
+            load(B[q], RV[q], gi + (q + NB) * stride);
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+        if (gi + (q + NB) * stride < ngroups)
+            reduce(B[q], RV[q], gi + (q + NB) * stride);
+}
+
 // ------------------------------------------------------------------------
 // Staged kernels (Q6_K, Q8_0)
 // ------------------------------------------------------------------------
@@ -528,6 +663,11 @@ template <>
 struct SFmt<kIQ4_NL> {
     static constexpr int SEG_BLOCKS = 64, SEG_BYTES = 64 * 18;
 };
+__host__ __device__ constexpr int SFmtSegBlocks(int fmt)
+{
+    return fmt == kQ6_K ? SFmt<kQ6_K>::SEG_BLOCKS : fmt == kQ8_0 ? SFmt<kQ8_0>::SEG_BLOCKS
+         : SFmt<kIQ4_NL>::SEG_BLOCKS;
+}
 static_assert(SFmt<kQ6_K>::SEG_BYTES % 16 == 0, "Q6_K segment must be 16-byte aligned");
 static_assert(SFmt<kQ8_0>::SEG_BYTES % 16 == 0, "Q8_0 segment must be 16-byte aligned");
 static_assert(SFmt<kIQ4_NL>::SEG_BYTES % 16 == 0, "IQ4_NL segment must be 16-byte aligned");
@@ -986,6 +1126,366 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
     }
 }
 
+// ---- persistent streamed kernel with integer-digit activations -----------
+// One workgroup per CU (NW waves) walks chunks of rpc rows grid-stride.  The
+// K segments of a row (2048 columns each, nseg <= NW) are spread over the
+// waves: wave w owns segment w % nseg and, when there are more waves than
+// segments, every (NW / nseg)-th row of a chunk.  A wave computes the digits
+// of its x slice once, then streams its rows of all its chunks through a
+// private D-slot LDS ring of direct-to-LDS copies that runs across chunk
+// boundaries (the copy of the row D ahead is issued as soon as a row is
+// reduced).  Per chunk the segment sums meet in LDS and the workgroup
+// finishes the rows (residual add, argmax fold).
+//
+// Digits: as for the wide kernels, but each lane scales its own 32 elements
+// (one exponent per lane, no cross-lane reduction).  Q6_K's weights q - 32
+// and the signed Q8_0 / IQ4_NL weights enter the unsigned digit planes as
+// unsigned bytes (q, q + 128, grid + 128); the offsets are taken off exactly
+// by starting each integer sum at -offset * (sum of the digits).
+struct SXD {
+    uint32_t p[3][8]; // digit planes of the lane's 32 elements, 4 per dword
+    int init[3][4];   // dot accumulator starts (Q6_K: per 8-element group; else [p][0])
+    int e;            // the lane's exponent
+    float poison;     // 0, or NaN when the lane's x slice holds a non-finite value
+};
+
+// Load the lane's 32 elements of x; returns false for a lane past the
+// segment's blocks (its loads read block 0 and staged_dig_x zeroes them).
+template <int FMT>
+__device__ __forceinline__ bool staged_dig_load(const float *xseg, int lane,
+                                                int seg_blocks, float4 (&v)[8])
+{
+    bool active;
+    if constexpr (FMT == kQ6_K) {
+        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+        active = bs < seg_blocks;
+        const float *base = xseg + (active ? 256 * bs + 128 * n + l0 : 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 *q = reinterpret_cast<const float4 *>(base + 32 * g);
+            v[2 * g] = q[0];
+            v[2 * g + 1] = q[1];
+        }
+    } else {
+        active = lane < seg_blocks;
+        const float4 *q = reinterpret_cast<const float4 *>(xseg + (active ? 32 * lane : 0));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = q[t];
+    }
+    return active;
+}
+
+// The lane's digits, exponent and accumulator starts from its loaded x.
+template <int FMT>
+__device__ __forceinline__ void staged_dig_x(float4 (&v)[8], bool active, SXD &X)
+{
+    const uint32_t keep = active ? 0xffffffffu : 0u; // a mask, not a branch around loaded registers
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+        v[t] = make_float4(__uint_as_float(__float_as_uint(v[t].x) & keep),
+                           __uint_as_float(__float_as_uint(v[t].y) & keep),
+                           __uint_as_float(__float_as_uint(v[t].z) & keep),
+                           __uint_as_float(__float_as_uint(v[t].w) & keep));
+    uint32_t m = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+        m = max(m, abs_bits_max(v[t]));
+    const bool finite = m < 0x7f800000u;
+    const int e = finite ? __builtin_amdgcn_frexp_expf(__uint_as_float(m)) : 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+        dig_four(v[t], e, finite, X.p[0][t], X.p[1][t], X.p[2][t]);
+    X.e = e;
+    X.poison = finite ? 0.0f : __builtin_nanf("");
+    constexpr uint32_t ones = 0x01010101u;
+    if constexpr (FMT == kQ6_K) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int t = 2 * g;
+            X.init[0][g] = -32 * (int)__builtin_amdgcn_udot4(X.p[0][t + 1], ones, __builtin_amdgcn_udot4(X.p[0][t], ones, 0, false), false);
+            X.init[1][g] = -32 * (int)__builtin_amdgcn_udot4(X.p[1][t + 1], ones, __builtin_amdgcn_udot4(X.p[1][t], ones, 0, false), false);
+            X.init[2][g] = -32 * __builtin_amdgcn_sdot4((int)X.p[2][t + 1], (int)ones, __builtin_amdgcn_sdot4((int)X.p[2][t], (int)ones, 0, false), false);
+        }
+    } else {
+        uint32_t s0 = 0, s1 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            s0 = __builtin_amdgcn_udot4(X.p[0][t], ones, s0, false);
+            s1 = __builtin_amdgcn_udot4(X.p[1][t], ones, s1, false);
+        }
+        X.init[0][0] = -128 * (int)s0;
+        X.init[1][0] = -128 * (int)s1;
+        X.init[2][0] = 0; // the signed plane takes the signed weights
+    }
+}
+
+// a * b + c for a, b in the signed 24-bit range (v_mad_i32_i24, full rate;
+// the compiler cannot prove the range and would use the quarter-rate 32-bit
+// multiply).
+__device__ __forceinline__ int mad_i24(int a, int b, int c)
+{
+    int d;
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
+// Q6_K block at byte `bo` of the LDS tile (lane geometry of q6_dot).
+__device__ __forceinline__ float q6_dot_dig(const uint8_t *tile, uint32_t bo, int n, int l0,
+                                            const SXD &X)
+{
+    uint32_t A[2], B[2], H[2], S[2];
+    lds_read8_even(tile, bo + 64 * n + l0, A[0], A[1]);
+    lds_read8_even(tile, bo + 64 * n + 32 + l0, B[0], B[1]);
+    lds_read8_even(tile, bo + 128 + 32 * n + l0, H[0], H[1]);
+    lds_read8_even(tile, bo + 192 + 8 * n, S[0], S[1]);
+    const float d = h2f(lds_read_u16(tile, bo + 208));
+    int acc[3][4];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) acc[p][g] = X.init[p][g];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t v[4] = {
+            (A[t] & 0x0f0f0f0fu) | ((H[t] & 0x03030303u) << 4),
+            (B[t] & 0x0f0f0f0fu) | ((H[t] & 0x0c0c0c0cu) << 2),
+            ((A[t] >> 4) & 0x0f0f0f0fu) | (H[t] & 0x30303030u),
+            ((B[t] >> 4) & 0x0f0f0f0fu) | ((H[t] >> 2) & 0x30303030u),
+        };
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            acc[0][g] = (int)__builtin_amdgcn_udot4(v[g], X.p[0][2 * g + t], (uint32_t)acc[0][g], false);
+            acc[1][g] = (int)__builtin_amdgcn_udot4(v[g], X.p[1][2 * g + t], (uint32_t)acc[1][g], false);
+            acc[2][g] = __builtin_amdgcn_sdot4((int)v[g], (int)X.p[2][2 * g + t], acc[2][g], false);
+        }
+    }
+    // scale-weighted sums per plane: |acc| <= 8 * 63 * 255, |sc| <= 128 (24-bit products)
+    const int c = l0 >> 4;
+    int T[3] = {0, 0, 0};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int si = 2 * g + c; // byte of the 8 scales sc[8n..8n+7]
+        const int sc = __builtin_amdgcn_sbfe(S[si >> 2], 8 * (si & 3), 8);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) T[p] = mad_i24(sc, acc[p][g], T[p]);
+    }
+    const float v = fmaf(fmaf((float)T[2], 256.0f, (float)T[1]), 256.0f, (float)T[0]);
+    return d * __builtin_ldexpf(v + X.poison, X.e - 22);
+}
+
+// Q8_0 block at byte `off` of an LDS row.
+__device__ __forceinline__ float q80_dot_dig(const uint8_t *row_lds, uint32_t off, const SXD &X)
+{
+    const float d = h2f(lds_read_u16(row_lds, off));
+    const uint32_t o = off + 2;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
+    const uint32_t sh = o & 3u;
+    uint32_t w[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w[i] = p[i];
+    uint32_t a0 = (uint32_t)X.init[0][0], a1 = (uint32_t)X.init[1][0];
+    int a2 = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh);
+        const uint32_t u = q ^ 0x80808080u; // q + 128 as unsigned bytes
+        a0 = __builtin_amdgcn_udot4(u, X.p[0][t], a0, false);
+        a1 = __builtin_amdgcn_udot4(u, X.p[1][t], a1, false);
+        a2 = __builtin_amdgcn_sdot4((int)q, (int)X.p[2][t], a2, false);
+    }
+    const float v = fmaf(fmaf((float)a2, 256.0f, (float)(int)a1), 256.0f, (float)(int)a0);
+    return d * __builtin_ldexpf(v + X.poison, X.e - 22);
+}
+
+// IQ4_NL block at byte `off` of an LDS row (element j = low nibble of qs[j],
+// element j + 16 = high nibble).
+__device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t off, const SXD &X)
+{
+    const float d = h2f(lds_read_u16(row_lds, off));
+    const uint32_t o = off + 2;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
+    const uint32_t sh = o & 3u;
+    uint32_t w[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) w[i] = p[i];
+    uint32_t a0 = (uint32_t)X.init[0][0], a1 = (uint32_t)X.init[1][0];
+    int a2 = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh); // qs[4t..4t+3]
+        const uint32_t ul = iq4nl_lookup(q & 0x0f0f0f0fu);          // grid + 128, elements 4t + b
+        const uint32_t uh = iq4nl_lookup((q >> 4) & 0x0f0f0f0fu);   // elements 16 + 4t + b
+        a0 = __builtin_amdgcn_udot4(ul, X.p[0][t], a0, false);
+        a1 = __builtin_amdgcn_udot4(ul, X.p[1][t], a1, false);
+        a2 = __builtin_amdgcn_sdot4((int)(ul ^ 0x80808080u), (int)X.p[2][t], a2, false);
+        a0 = __builtin_amdgcn_udot4(uh, X.p[0][4 + t], a0, false);
+        a1 = __builtin_amdgcn_udot4(uh, X.p[1][4 + t], a1, false);
+        a2 = __builtin_amdgcn_sdot4((int)(uh ^ 0x80808080u), (int)X.p[2][4 + t], a2, false);
+    }
+    const float v = fmaf(fmaf((float)a2, 256.0f, (float)(int)a1), 256.0f, (float)(int)a0);
+    return d * __builtin_ldexpf(v + X.poison, X.e - 22);
+}
+
+constexpr int kSdigMaxRows = 64; // rows per chunk of the persistent streamed kernel
+
+template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
+__global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
+                                                       const float *x, // not restrict: its loads stay above the copies
+                                                       float *y, int outer, int nblk, int rpc,
+                                                       ArgPart *__restrict__ parts,
+                                                       const float *resid)
+{
+    using F = SFmt<FMT>;
+    // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
+    // segment re-read its last 16 bytes into the slot's tail), so the number of
+    // copies in flight is a compile-time count and the compiler's own waits for x
+    // need not drain the ring
+    constexpr int IPR = (F::SEG_BYTES / 16 + 63) / 64; // copy instructions per row
+    constexpr int SLOT = IPR * 1024;
+    static_assert(SLOT >= F::SEG_BYTES + 16, "Q8_0 / IQ4_NL read one dword past a segment");
+    __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * SLOT];
+    __shared__ float part[kSdigMaxRows][8];
+    __shared__ unsigned long long wkey[NW];
+    __shared__ uint32_t wflag[NW];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bb = block_bytes(FMT);
+    const size_t row_bytes = (size_t)nblk * bb;
+    const int nseg = (nblk + F::SEG_BLOCKS - 1) / F::SEG_BLOCKS; // <= NW (host-checked)
+    const int wps = NW / nseg;                                   // waves per segment
+    const int sg = w % nseg, rl = w / nseg;
+    const bool worker = rl < wps; // waves past nseg * wps only join the barriers
+    const int nchunks = (outer + rpc - 1) / rpc;
+    const int seg_blocks = min(F::SEG_BLOCKS, nblk - sg * F::SEG_BLOCKS);
+    const int chunks16 = seg_blocks * bb / 16; // whole 8-block groups: host-checked
+    const uint32_t my_ring = (uint32_t)(w * D * SLOT);
+    const uint8_t *seg0 = W + (size_t)sg * F::SEG_BYTES;
+
+    // this wave's rows: items k = 0, 1, ... over its chunks; m rows per full chunk
+    const int m = worker ? (rpc - rl + wps - 1) / wps : 0;
+    const int my_chunks = blockIdx.x < nchunks ? (nchunks - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    int nitems = my_chunks * m;
+    if (worker && my_chunks > 0 && blockIdx.x + (my_chunks - 1) * gridDim.x == nchunks - 1) {
+        const int last = outer - (nchunks - 1) * rpc; // rows of the last chunk
+        nitems = (my_chunks - 1) * m + max(0, (last - rl + wps - 1) / wps);
+    }
+    const int mm = max(m, 1);
+    auto item_row = [&](int k) { // global row of item k (clamped: always a row of W)
+        const int ci = k / mm, rr = k - ci * mm;
+        return min((blockIdx.x + ci * gridDim.x) * rpc + rl + rr * wps, outer - 1);
+    };
+    // item k's row segment into slot k % D (k past the wave's items: its last
+    // item's row again, into a slot no remaining item uses)
+    auto issue = [&](int k) {
+        const int kk = max(0, min(k, nitems - 1));
+        const uint8_t *src = seg0 + (size_t)item_row(kk) * row_bytes;
+        uint8_t *dst = ring + my_ring + (k % D) * SLOT;
+#pragma unroll
+        for (int i = 0; i < IPR; ++i) {
+            const int c = min(64 * i + lane, chunks16 - 1);
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(src + 16 * (size_t)c),
+                (__attribute__((address_space(3))) void *)(dst + 1024 * i), 16, 0, 0);
+        }
+    };
+
+    // x first, then the first D rows' copies, so the copies are in flight while
+    // the digits are formed (the compiler's wait before the first use of x
+    // counts the younger copies and lets them run)
+    float4 xv[8];
+    const bool xact = staged_dig_load<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
+    asm volatile("" ::: "memory");     // x loads stay ahead of the copies (in-order vmcnt)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        issue(k);
+    __builtin_amdgcn_sched_barrier(0);
+    SXD X;
+    staged_dig_x<FMT>(xv, xact, X);
+
+    unsigned long long key = 0;
+    uint32_t fl = 0;
+    int k = 0;
+    for (int ci = 0; ci < my_chunks; ++ci) {
+        const int chunk = blockIdx.x + ci * gridDim.x;
+        const int row0 = chunk * rpc;
+        const int nrows = min(rpc, outer - row0);
+        const int mine = worker ? max(0, min(m, (nrows - rl + wps - 1) / wps)) : 0;
+        for (int rr = 0; rr < mine; ++rr, ++k) {
+            // items issued after item k: k + 1 .. max(D, nitems) - 1, at most D - 1
+            // of them; younger epilogue loads and stores only lengthen the wait
+            wait_vmcnt(IPR * min(D - 1, max(D, nitems) - 1 - k));
+            const uint32_t slot = my_ring + (uint32_t)((k % D) * SLOT);
+            float v = 0.0f;
+            if constexpr (FMT == kQ6_K) {
+                const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+                if (bs < seg_blocks)
+                    v = q6_dot_dig(ring, slot + (uint32_t)(210 * bs), n, l0, X);
+            } else if constexpr (FMT == kIQ4_NL) {
+                if (lane < seg_blocks)
+                    v = iq4nl_dot_dig(ring + slot, 18u * lane, X);
+            } else {
+                if (lane < seg_blocks)
+                    v = q80_dot_dig(ring + slot, 34u * lane, X);
+            }
+            v = wave_sum(v);
+            if (nseg == 1) { // the wave holds the whole row: finish it here
+                const int row = row0 + rl + rr * wps;
+                if constexpr (RESID)
+                    v += resid[row]; // wave-uniform: a scalar load
+                if (y && lane == 0)
+                    y[row] = v;
+                if constexpr (ARGMAX)
+                    argmax_fold(v, (uint32_t)row, key, fl); // every lane folds the same row
+            } else if (lane == 0) {
+                part[rl + rr * wps][sg] = v;
+            }
+            if (k + D < nitems)
+                issue(k + D); // slot k % D has been read
+        }
+        if (nseg == 1) // wave-uniform for the whole workgroup: no exchange, no barriers
+            continue;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); // part[] writes done
+        lds_barrier();
+        for (int i = tid; i < nrows; i += NW * 64) {
+            float v = 0.0f;
+            for (int q = 0; q < nseg; ++q)
+                v += part[i][q];
+            if constexpr (RESID)
+                v += resid[row0 + i]; // resid may be y
+            if (y)
+                y[row0 + i] = v;
+            if constexpr (ARGMAX)
+                argmax_fold(v, (uint32_t)(row0 + i), key, fl);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier(); // part[] is free for the next chunk
+    }
+    if constexpr (ARGMAX) {
+        argmax_wave_reduce(key, fl);
+        if (lane == 0) {
+            wkey[w] = key;
+            wflag[w] = fl;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (tid == 0) {
+            unsigned long long kk = wkey[0];
+            uint32_t f = wflag[0];
+#pragma unroll
+            for (int i = 1; i < NW; ++i) {
+                kk = wkey[i] > kk ? wkey[i] : kk;
+                f |= wflag[i];
+            }
+            parts[blockIdx.x].key = kk;
+            parts[blockIdx.x].flags = f;
+            parts[blockIdx.x].pad = 0;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0); // every copy has landed before the workgroup ends
+}
+
 // ------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------
@@ -996,6 +1496,12 @@ static int g_rows_gateup = 0; // fused gate/up (default 1)
 static int g_stream_rows = 0; // Q6_K/Q8_0 rows per chunk (default: see stream_rows())
 static int g_wide_fp32 = 0;   // Q4_K/Q5_K: 1 = fp32 activations instead of integer digits
 static int g_wide_waves = 0;  // Q4_K/Q5_K waves per workgroup (4 or 8; default 8)
+static int g_wide_persist = 0; // Q4_K/Q5_K persistent kernel: 1 = always, -1 = never, 0 = by size
+static int g_pers_wg_per_cu = 1; // workgroups per CU of the persistent kernel
+static int g_pers_bufs = 0;      // register buffers per wave of the persistent kernel (2..4)
+static int g_stream_wg_per_cu = 0; // streamed kernel: cap on workgroups per CU (0 = one per chunk)
+// persistent digit streamed kernel: rows per chunk, ring depth (0 = default), 1 = not used
+static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0;
 
 void set_tuning(const char *name, int value)
 {
@@ -1004,6 +1510,14 @@ void set_tuning(const char *name, int value)
     if (!__builtin_strcmp(name, "stream_rows")) g_stream_rows = value;
     if (!__builtin_strcmp(name, "wide_fp32")) g_wide_fp32 = value;
     if (!__builtin_strcmp(name, "wide_waves")) g_wide_waves = value;
+    if (!__builtin_strcmp(name, "wide_persist")) g_wide_persist = value;
+    if (!__builtin_strcmp(name, "pers_wg_per_cu")) g_pers_wg_per_cu = value > 0 ? value : 1;
+    if (!__builtin_strcmp(name, "pers_bufs")) g_pers_bufs = value;
+    if (!__builtin_strcmp(name, "stream_wg_per_cu")) g_stream_wg_per_cu = value;
+    if (!__builtin_strcmp(name, "sdig_rows")) g_sdig_rows = value;
+    if (!__builtin_strcmp(name, "sdig_depth")) g_sdig_depth = value;
+    if (!__builtin_strcmp(name, "sdig_off")) g_sdig_off = value;
+    if (!__builtin_strcmp(name, "sdig_wg_per_cu")) g_sdig_wg_per_cu = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -1032,7 +1546,31 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
             if (R == 1) IHIP_KW(1, DG, EX, 4); else if (R == 4) IHIP_KW(4, DG, EX, 4); else IHIP_KW(2, DG, EX, 4); \
         }                                                                                    \
     } while (0)
-    if (dig) {
+    // the persistent kernel once every wave has at least four rows (measured on
+    // MI355X: 2 x 12288 x 4096 gate/up 12.7 us against 13.9 us; at 4096 x 4096
+    // one row group per wave is all there is and the plain kernel is faster)
+    const bool pers = dig && nblk <= 16 && (g_wide_persist > 0 || (g_wide_persist == 0 && outer >= 4 * nwv * 256));
+    if (pers) {
+        int dev = 0, ncu = 256;
+        if (hipGetDevice(&dev) == hipSuccess)
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        const int nbuf = g_pers_bufs >= 2 && g_pers_bufs <= 4 ? g_pers_bufs : 2;
+        const int grid = max(1, min(ncu * g_pers_wg_per_cu, (outer + nwv - 1) / nwv));
+#define IHIP_KP(RR, EX, NV, NBB)                                                             \
+    hipLaunchKernelGGL((k_gemv_kpers<FMT, RR, GATEUP, EX, NV, NBB>), dim3(grid), dim3(NV * 64), 0, s, \
+                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid)
+#define IHIP_KP_R(EX)                                                                        \
+    do {                                                                                     \
+        if (nwv == 8) {                                                                      \
+            if (nbuf == 2) IHIP_KP(1, EX, 8, 2); else if (nbuf == 3) IHIP_KP(1, EX, 8, 3); else IHIP_KP(1, EX, 8, 4); \
+        } else {                                                                             \
+            if (nbuf == 2) IHIP_KP(1, EX, 4, 2); else if (nbuf == 3) IHIP_KP(1, EX, 4, 3); else IHIP_KP(1, EX, 4, 4); \
+        }                                                                                    \
+    } while (0)
+        if (ext) IHIP_KP_R(true); else IHIP_KP_R(false);
+#undef IHIP_KP_R
+#undef IHIP_KP
+    } else if (dig) {
         if (ext) IHIP_KW_R(true, true); else IHIP_KW_R(true, false);
     } else {
         if (ext) IHIP_KW_R(false, true); else IHIP_KW_R(false, false);
@@ -1063,12 +1601,85 @@ static int stream_rows(int outer, bool argmax)
     return r;
 }
 
-static int stream_grid(int outer, int rpc) { return (outer + rpc - 1) / rpc; }
+// One workgroup per chunk, or at most g_stream_wg_per_cu workgroups per CU that
+// walk the chunks grid-stride (each keeps its x slice across its chunks).
+static int stream_grid(int outer, int rpc)
+{
+    const int nchunks = (outer + rpc - 1) / rpc;
+    if (g_stream_wg_per_cu <= 0)
+        return nchunks;
+    int dev = 0, ncu = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    return max(1, min(nchunks, g_stream_wg_per_cu * ncu));
+}
+
+// The persistent digit kernel: nseg <= 8 segments of 2048 columns.
+static int sdig_waves(int nseg) { return (nseg == 3 || nseg == 6) ? 6 : 8; }
+
+template <int FMT, bool ARGMAX, int NWV, int DD>
+static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer, int rpc,
+                           int grid, void *parts, hipStream_t s, const float *resid)
+{
+    if (resid)
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, true>), dim3(grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
+    else
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, false>), dim3(grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
+}
+
+
+// Rows per chunk (measured on MI355X: 151936 x 2048 Q6_K lm_head, 4096 x 4096
+// Q8_0, 4096 x 12288 Q6_K): rows of one segment finish inside their wave and
+// take long chunks; rows of several segments meet in LDS once per chunk and
+// take short ones, which spread a small matrix over more workgroups.
+static int sdig_rows(int nseg)
+{
+    const int r = g_sdig_rows > 0 ? g_sdig_rows : nseg == 1 ? 32 : nseg == 2 ? 16 : 4;
+    return min(r, kSdigMaxRows);
+}
+
+static bool sdig_usable(int fmt, int nblk)
+{
+    const int seg = SFmtSegBlocks(fmt);
+    const int nseg = (nblk + seg - 1) / seg;
+    return g_sdig_off <= 0 && nseg >= 1 && nseg <= 8;
+}
+
+static int sdig_grid(int outer, int nseg)
+{
+    const int nchunks = (outer + sdig_rows(nseg) - 1) / sdig_rows(nseg);
+    int dev = 0, ncu = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    return max(1, min(nchunks, ncu * (g_sdig_wg_per_cu > 0 ? g_sdig_wg_per_cu : 4)));
+}
+
+template <int FMT, bool ARGMAX>
+static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner, int outer,
+                              void *parts, hipStream_t s, const float *resid)
+{
+    const int nblk = inner / block_elems(FMT);
+    const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
+    const int rpc = sdig_rows(nseg), grid = sdig_grid(outer, nseg);
+    const int dd = g_sdig_depth >= 4 ? 4 : 2; // ring depth (4 x 8 waves x 3 KB Q8_0 slots is 96 KB)
+    if (sdig_waves(nseg) == 6) {
+        if (dd == 2) launch_sdig_nd<FMT, ARGMAX, 6, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+        else launch_sdig_nd<FMT, ARGMAX, 6, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+    } else {
+        if (dd == 2) launch_sdig_nd<FMT, ARGMAX, 8, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+        else launch_sdig_nd<FMT, ARGMAX, 8, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+    }
+    return hipGetLastError();
+}
 
 template <int FMT, bool ARGMAX>
 static hipError_t launch_stream(const void *w, const float *x, float *y, int inner, int outer,
                                 void *parts, hipStream_t s, const float *resid = nullptr)
 {
+    if (sdig_usable(FMT, inner / block_elems(FMT)))
+        return launch_sdig<FMT, ARGMAX>(w, x, y, inner, outer, parts, s, resid);
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int nw = stream_waves(nseg);
@@ -1125,7 +1736,9 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
     }
     if (e != hipSuccess)
         return e;
-    const int nparts = stream_grid(vocab, stream_rows(vocab, true));
+    const int nblk = hidden / block_elems(type), seg = SFmtSegBlocks(type);
+    const int nparts = sdig_usable(type, nblk) ? sdig_grid(vocab, (nblk + seg - 1) / seg)
+                                               : stream_grid(vocab, stream_rows(vocab, true));
     hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(1024), 0, s, (const ArgPart *)ws, nparts,
                        token, flags);
     return hipGetLastError();

@@ -194,58 +194,76 @@ def test_gemv_host_mirror_and_weight_cache(t):
                   oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), "after forget")
 
 
+STREAM_SHAPES = ((synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144), (synth.Q6_K, 300, 24576),
+                 (synth.Q6_K, 33, 10240), (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304),
+                 (synth.Q8_0, 19, 256), (synth.IQ4_NL, 517, 4608))
+
 TUNING_CASES = [
-    ("rows_wide", r, t, outer, inner)
+    ({"rows_wide": r}, t, outer, inner)
     for r in (1, 2, 4) for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608))
 ] + [
     # Q4_K/Q5_K: fp32 activations instead of integer digits; four waves per workgroup
-    (knob, 1 if knob == "wide_fp32" else 4, t, outer, inner)
+    ({knob: 1 if knob == "wide_fp32" else 4}, t, outer, inner)
     for knob in ("wide_fp32", "wide_waves")
     for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608), (synth.Q4_K, 9, 8448))
 ] + [
-    # streamed Q6_K / Q8_0 kernel: rows per chunk x (waves per workgroup = segments, up to 8;
-    # 12 and 5 segments give waves that own two segments)
-    ("stream_rows", r, t, outer, inner)
-    for r in (4, 17, 64) for t, outer, inner in ((synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144),
-                                                 (synth.Q6_K, 300, 24576), (synth.Q6_K, 33, 10240),
-                                                 (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304),
-                                                 (synth.Q8_0, 19, 256))
+    # Q4_K/Q5_K persistent digit kernel (register-buffered row groups), forced on
+    ({"wide_persist": 1, "pers_bufs": nb, "wide_waves": nw}, t, outer, inner)
+    for nb, nw in ((2, 8), (3, 4), (4, 8))
+    for t, outer, inner in ((synth.Q4_K, 4099, 4096), (synth.Q5_K, 2051, 2560), (synth.Q4_K, 7, 256))
+] + [
+    # fp32 streamed Q6_K / Q8_0 / IQ4_NL kernel: rows per chunk x (waves per workgroup =
+    # segments, up to 8; 12 and 5 segments give waves that own two segments)
+    ({"sdig_off": 1, "stream_rows": r}, t, outer, inner)
+    for r in (4, 17, 64) for t, outer, inner in STREAM_SHAPES
+] + [
+    # persistent digit streamed kernel: ring depth, rows per chunk (1 and 7: chunks that
+    # split unevenly over the waves of a segment), workgroups per CU (1: many chunks each)
+    ({"sdig_depth": dd, "sdig_rows": r, "sdig_wg_per_cu": wg}, t, outer, inner)
+    for dd, r, wg in ((2, 0, 0), (4, 1, 1), (8, 7, 2), (2, 64, 1), (4, 33, 3))
+    for t, outer, inner in STREAM_SHAPES
 ]
 
 
-@pytest.mark.parametrize("knob,value,t,outer,inner", TUNING_CASES)
-def test_gemv_every_kernel_variant(knob, value, t, outer, inner):
-    from inferno_hip import _lib, device as D
-    say(f"gemv {knob}={value} type={t} {outer}x{inner}")
-    rng = synth.rng_for(value * 131 + t + inner + outer)
+def _tuned(knobs, fn):
+    from inferno_hip import _lib
+    for k, v in knobs.items():
+        _lib.set_tuning(k, v)
+    try:
+        return fn()
+    finally:
+        for k in knobs:
+            _lib.set_tuning(k, 0)
+
+
+@pytest.mark.parametrize("knobs,t,outer,inner", TUNING_CASES)
+def test_gemv_every_kernel_variant(knobs, t, outer, inner):
+    from inferno_hip import device as D
+    say(f"gemv {knobs} type={t} {outer}x{inner}")
+    rng = synth.rng_for(sum(knobs.values()) * 131 + t + inner + outer)
     w = synth.weight(rng, t, outer, inner)
     x = synth.activations(rng, inner)
-    _lib.set_tuning(knob, value)
-    try:
-        y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
-    finally:
-        _lib.set_tuning(knob, 0)
+    y = _tuned(knobs, lambda: D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy())
     ref = oracle.gemv_f64(t, w, x, inner, outer)
     tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
-    assert_within(y, ref, tol, f"{knob}={value} type {t} {outer}x{inner}")
+    assert_within(y, ref, tol, f"{knobs} type {t} {outer}x{inner}")
 
 
-@pytest.mark.parametrize("value", [1, 2, 4])
+@pytest.mark.parametrize("knobs", [{"rows_gateup": 1}, {"rows_gateup": 2}, {"rows_gateup": 4},
+                                   {"wide_fp32": 1}, {"wide_persist": 1},
+                                   {"wide_persist": 1, "pers_bufs": 2, "wide_waves": 4},
+                                   {"wide_persist": -1}])
 @pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K])
-def test_gate_up_every_kernel_variant(value, t):
-    from inferno_hip import _lib, device as D
+def test_gate_up_every_kernel_variant(knobs, t):
+    from inferno_hip import device as D
     hidden, inter = 4096, 1030
-    say(f"gate/up rows_gateup={value} type={t}")
-    rng = synth.rng_for(value + 17 * t)
+    say(f"gate/up {knobs} type={t}")
+    rng = synth.rng_for(sum(knobs.values()) + 17 * t)
     wg = synth.weight(rng, t, inter, hidden)
     wu = synth.weight(rng, t, inter, hidden)
     x = synth.activations(rng, hidden)
-    _lib.set_tuning("rows_gateup", value)
-    try:
-        h = D.gate_up_swiglu(dweight(wg, t, hidden, inter), dweight(wu, t, hidden, inter),
-                             dev(x)).cpu().numpy()
-    finally:
-        _lib.set_tuning("rows_gateup", 0)
+    h = _tuned(knobs, lambda: D.gate_up_swiglu(dweight(wg, t, hidden, inter), dweight(wu, t, hidden, inter),
+                                               dev(x)).cpu().numpy())
     g = oracle.gemv_f64(t, wg, x, hidden, inter)
     u = oracle.gemv_f64(t, wu, x, hidden, inter)
     hb = _h_bound(g, u, oracle.row_norms(t, wg, hidden, inter), oracle.row_norms(t, wu, hidden, inter), x)
@@ -413,8 +431,20 @@ def test_fused_elementwise_kernels():
     (synth.Q8_0, 32000, 2048, 6),
     (synth.Q4_K, 5003, 1024, 7),       # GEMV + standalone argmax path
 ])
-def test_lm_head_argmax(t, vocab, hidden, seed):
-    say(f"lm_head type={t} vocab={vocab} hidden={hidden} seed={seed}")
+@pytest.mark.parametrize("knobs", [{}, {"sdig_off": 1}, {"sdig_wg_per_cu": 1, "sdig_rows": 7}])
+def test_lm_head_argmax(t, vocab, hidden, seed, knobs):
+    from inferno_hip import _lib
+    for k, v in knobs.items():
+        _lib.set_tuning(k, v)
+    try:
+        _lm_head_case(t, vocab, hidden, seed, knobs)
+    finally:
+        for k in knobs:
+            _lib.set_tuning(k, 0)
+
+
+def _lm_head_case(t, vocab, hidden, seed, knobs):
+    say(f"lm_head type={t} vocab={vocab} hidden={hidden} seed={seed} {knobs}")
     rng = synth.rng_for(seed)
     w = synth.weight(rng, t, vocab, hidden)
     x = synth.activations(rng, hidden)
