@@ -1501,7 +1501,7 @@ static int g_pers_wg_per_cu = 1; // workgroups per CU of the persistent kernel
 static int g_pers_bufs = 0;      // register buffers per wave of the persistent kernel (2..4)
 static int g_stream_wg_per_cu = 0; // streamed kernel: cap on workgroups per CU (0 = one per chunk)
 // persistent digit streamed kernel: rows per chunk, ring depth (0 = default), 1 = not used
-static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0;
+static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0, g_sdig_waves = 0;
 
 void set_tuning(const char *name, int value)
 {
@@ -1518,6 +1518,7 @@ void set_tuning(const char *name, int value)
     if (!__builtin_strcmp(name, "sdig_depth")) g_sdig_depth = value;
     if (!__builtin_strcmp(name, "sdig_off")) g_sdig_off = value;
     if (!__builtin_strcmp(name, "sdig_wg_per_cu")) g_sdig_wg_per_cu = value;
+    if (!__builtin_strcmp(name, "sdig_waves")) g_sdig_waves = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -1614,8 +1615,16 @@ static int stream_grid(int outer, int rpc)
     return max(1, min(nchunks, g_stream_wg_per_cu * ncu));
 }
 
-// The persistent digit kernel: nseg <= 8 segments of 2048 columns.
-static int sdig_waves(int nseg) { return (nseg == 3 || nseg == 6) ? 6 : 8; }
+// The persistent digit kernel: nseg <= 8 segments of 2048 columns; waves per
+// workgroup a multiple of nseg where possible (knob: 12 or 16 waves).
+static int sdig_waves(int nseg)
+{
+    if ((g_sdig_waves == 6 || g_sdig_waves == 8 || g_sdig_waves == 12 || g_sdig_waves == 16) &&
+        g_sdig_waves >= nseg)
+        return g_sdig_waves;
+    // measured on MI355X (4096 x 12288 Q6_K: 12 waves 12.8 us, 6 waves 14.3 us)
+    return (nseg == 3 || nseg == 6) ? 12 : 8;
+}
 
 template <int FMT, bool ARGMAX, int NWV, int DD>
 static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer, int rpc,
@@ -1636,7 +1645,8 @@ static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, in
 // take short ones, which spread a small matrix over more workgroups.
 static int sdig_rows(int nseg)
 {
-    const int r = g_sdig_rows > 0 ? g_sdig_rows : nseg == 1 ? 32 : nseg == 2 ? 16 : 4;
+    const int r = g_sdig_rows > 0 ? g_sdig_rows : nseg == 1 ? 32 : nseg == 2 ? 16
+                                                : (nseg == 3 || nseg == 6) ? 16 : 4;
     return min(r, kSdigMaxRows);
 }
 
@@ -1664,7 +1674,12 @@ static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int rpc = sdig_rows(nseg), grid = sdig_grid(outer, nseg);
     const int dd = g_sdig_depth >= 4 ? 4 : 2; // ring depth (4 x 8 waves x 3 KB Q8_0 slots is 96 KB)
-    if (sdig_waves(nseg) == 6) {
+    const int nwv = sdig_waves(nseg);
+    if (nwv == 12) {
+        launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+    } else if (nwv == 16) {
+        launch_sdig_nd<FMT, ARGMAX, 16, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+    } else if (nwv == 6) {
         if (dd == 2) launch_sdig_nd<FMT, ARGMAX, 6, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
         else launch_sdig_nd<FMT, ARGMAX, 6, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
     } else {

@@ -219,8 +219,9 @@ TUNING_CASES = [
 ] + [
     # persistent digit streamed kernel: ring depth, rows per chunk (1 and 7: chunks that
     # split unevenly over the waves of a segment), workgroups per CU (1: many chunks each)
-    ({"sdig_depth": dd, "sdig_rows": r, "sdig_wg_per_cu": wg}, t, outer, inner)
-    for dd, r, wg in ((2, 0, 0), (4, 1, 1), (8, 7, 2), (2, 64, 1), (4, 33, 3))
+    ({"sdig_depth": dd, "sdig_rows": r, "sdig_wg_per_cu": wg, "sdig_waves": nw}, t, outer, inner)
+    for dd, r, wg, nw in ((2, 0, 0, 0), (4, 1, 1, 8), (8, 7, 2, 16), (2, 64, 1, 12), (4, 33, 3, 6),
+                          (2, 5, 2, 16))
     for t, outer, inner in STREAM_SHAPES
 ]
 
