@@ -1333,7 +1333,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
                                                        const float *x, // not restrict: its loads stay above the copies
                                                        float *y, int outer, int nblk, int rpc,
                                                        ArgPart *__restrict__ parts,
-                                                       const float *resid)
+                                                       const float *resid, int xfirst)
 {
     using F = SFmt<FMT>;
     // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
@@ -1390,12 +1390,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
         }
     };
 
-    // x first, then the first D rows' copies, so the copies are in flight while
-    // the digits are formed (the compiler's wait before the first use of x
-    // counts the younger copies and lets them run)
+    // x first and waited for on its own, then the first D rows' copies, then
+    // the digits: with copies in flight the compiler's wait before the first
+    // use of x would be a full vmcnt(0) (it treats LDS-DMA and register loads
+    // as completing out of order), which holds the digits until every
+    // prologue copy has landed; x comes from L2 in a fraction of that.
     float4 xv[8];
     const bool xact = staged_dig_load<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
-    asm volatile("" ::: "memory");     // x loads stay ahead of the copies (in-order vmcnt)
+    if (xfirst)
+        __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < D; ++k)
@@ -1502,6 +1506,7 @@ static int g_pers_bufs = 0;      // register buffers per wave of the persistent 
 static int g_stream_wg_per_cu = 0; // streamed kernel: cap on workgroups per CU (0 = one per chunk)
 // persistent digit streamed kernel: rows per chunk, ring depth (0 = default), 1 = not used
 static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0, g_sdig_waves = 0;
+static int g_sdig_xfirst = 0; // -1: issue the ring prologue before x has landed
 
 void set_tuning(const char *name, int value)
 {
@@ -1519,6 +1524,7 @@ void set_tuning(const char *name, int value)
     if (!__builtin_strcmp(name, "sdig_off")) g_sdig_off = value;
     if (!__builtin_strcmp(name, "sdig_wg_per_cu")) g_sdig_wg_per_cu = value;
     if (!__builtin_strcmp(name, "sdig_waves")) g_sdig_waves = value;
+    if (!__builtin_strcmp(name, "sdig_xfirst")) g_sdig_xfirst = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -1615,6 +1621,14 @@ static int stream_grid(int outer, int rpc)
     return max(1, min(nchunks, g_stream_wg_per_cu * ncu));
 }
 
+// Whether NW waves with D ring slots fit the 160 KB of LDS (slot: whole 1 KB copies).
+template <int FMT>
+constexpr bool sdig_fits(int nw, int d)
+{
+    return nw * d * ((SFmt<FMT>::SEG_BYTES / 16 + 63) / 64) * 1024 + kSdigMaxRows * 8 * 4 + 2048 <=
+           160 * 1024;
+}
+
 // The persistent digit kernel: nseg <= 8 segments of 2048 columns; waves per
 // workgroup a multiple of nseg where possible (knob: 12 or 16 waves).
 static int sdig_waves(int nseg)
@@ -1630,12 +1644,13 @@ template <int FMT, bool ARGMAX, int NWV, int DD>
 static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer, int rpc,
                            int grid, void *parts, hipStream_t s, const float *resid)
 {
+    const int xfirst = g_sdig_xfirst >= 0 ? 1 : 0;
     if (resid)
         hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, true>), dim3(grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
+                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid, xfirst);
     else
         hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, false>), dim3(grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
+                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid, xfirst);
 }
 
 
@@ -1673,10 +1688,13 @@ static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int rpc = sdig_rows(nseg), grid = sdig_grid(outer, nseg);
-    const int dd = g_sdig_depth >= 4 ? 4 : 2; // ring depth (4 x 8 waves x 3 KB Q8_0 slots is 96 KB)
+    // ring depth (4 x 8 waves x 3 KB Q8_0 slots is 96 KB; 6 only where it fits)
+    const int dd = g_sdig_depth >= 6 ? 6 : g_sdig_depth >= 4 ? 4 : 2;
     const int nwv = sdig_waves(nseg);
     if (nwv == 12) {
-        launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+        if (dd == 6 && sdig_fits<FMT>(12, 6)) launch_sdig_nd<FMT, ARGMAX, 12, sdig_fits<FMT>(12, 6) ? 6 : 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+        else if (dd == 4) launch_sdig_nd<FMT, ARGMAX, 12, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+        else launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
     } else if (nwv == 16) {
         launch_sdig_nd<FMT, ARGMAX, 16, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
     } else if (nwv == 6) {

@@ -146,42 +146,47 @@ __device__ __forceinline__ half8 pf_dequant8(uint2 bytes, bool high, half2v dsc,
     return r;
 }
 
-// Reduce sub-block pair j of one ring slot into the accumulators.  This
-// lane's A operands are weight rows `blk0` and `blk1` (rows li and li + 32 of
-// the wave's 64), 8 k of every 16-wide step; its B operands are tokens li
-// and li + 32.  acc[u][t] is the 32 x 32 tile (weight rows 32u.., tokens
-// 32t..): lane l, register r hold token 32t + l % 32, weight row
-// 32u + 8 (r / 4) + 4 (l / 32) + r % 4.
-__device__ __forceinline__ void pf_pair(const uint8_t *sa, const uint8_t *blk0,
-                                        const uint8_t *blk1, int j, int h, int li,
-                                        float16v (&acc)[2][2])
-{
-    // every LDS read of the column first (one wait instead of one per step)
+// One column's operands of this lane, read from a ring slot: the block
+// headers and 2 x 8 quant bytes of weight rows `blk0` / `blk1` (rows li and
+// li + 32 of the wave's 64) for sub-block pair j, and the 16-byte fp16
+// activation chunks of tokens li and li + 32 for the four 16-wide K steps
+// (k = 64j + 16s + 8h + (0..7), chunk 8j + 2s + h).
+struct PfOps {
     uint4 hd[2];
     uint2 q0[2], q1[2];
     half8 x[4][2];
+};
+
+__device__ __forceinline__ void pf_read(const uint8_t *sa, const uint8_t *blk0, const uint8_t *blk1,
+                                        int j, int h, int li, PfOps &o)
+{
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const uint8_t *blk = u ? blk1 : blk0;
-        hd[u] = *reinterpret_cast<const uint4 *>(blk);
-        q0[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
-        q1[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
+        o.hd[u] = *reinterpret_cast<const uint4 *>(blk);
+        o.q0[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
+        o.q1[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
     }
-    // four 16-wide K steps: k = 64j + 16s + 8h + (0..7), 16-byte chunk 8j + 2s + h
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int m = 32 * t + li, c = 8 * j + 2 * s + h;
-            x[s][t] = *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
+            o.x[s][t] = *reinterpret_cast<const half8 *>(sa + m * PF_ROW_BYTES + 16 * (c ^ (m & 15)));
         }
-    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Dequantize the column's weights into matrix-core operands and accumulate.
+// acc[u][t] is the 32 x 32 tile (weight rows 32u.., tokens 32t..): lane l,
+// register r hold token 32t + l % 32, weight row 32u + 8 (r / 4) + 4 (l / 32) + r % 4.
+__device__ __forceinline__ void pf_mma(const PfOps &o, int j, float16v (&acc)[2][2])
+{
     half2v dsA[2], dmA[2], dsB[2], dmB[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const float d = h2f(hd[u].x & 0xffffu), dmin = h2f(hd[u].x >> 16);
+        const float d = h2f(o.hd[u].x & 0xffffu), dmin = h2f(o.hd[u].x >> 16);
         float scA, mA, scB, mB;
-        k_scale_min_pair(hd[u].y, hd[u].z, hd[u].w, j, scA, mA, scB, mB);
+        k_scale_min_pair(o.hd[u].y, o.hd[u].z, o.hd[u].w, j, scA, mA, scB, mB);
         const _Float16 a = (_Float16)(d * scA), ma = (_Float16)(-(dmin * mA));
         const _Float16 bb = (_Float16)(d * scB), mb = (_Float16)(-(dmin * mB));
         dsA[u] = half2v{a, a};
@@ -193,12 +198,24 @@ __device__ __forceinline__ void pf_pair(const uint8_t *sa, const uint8_t *blk0,
     for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const half8 wq = pf_dequant8((s & 1) ? q1[u] : q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
+            const half8 wq = pf_dequant8((s & 1) ? o.q1[u] : o.q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
                                          s >= 2 ? dmB[u] : dmA[u]);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-                acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, x[s][t], acc[u][t], 0, 0, 0);
+                acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, o.x[s][t], acc[u][t], 0, 0, 0);
         }
+}
+
+// Reduce sub-block pair j of one ring slot into the accumulators (all LDS
+// reads of the column first: one wait instead of one per step).
+__device__ __forceinline__ void pf_pair(const uint8_t *sa, const uint8_t *blk0,
+                                        const uint8_t *blk1, int j, int h, int li,
+                                        float16v (&acc)[2][2])
+{
+    PfOps o;
+    pf_read(sa, blk0, blk1, j, h, li, o);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_mma(o, j, acc);
 }
 
 // Wait for this wave's copies: n is 0 or one column's copy count (6 or 7).

@@ -221,8 +221,12 @@ TUNING_CASES = [
     # split unevenly over the waves of a segment), workgroups per CU (1: many chunks each)
     ({"sdig_depth": dd, "sdig_rows": r, "sdig_wg_per_cu": wg, "sdig_waves": nw}, t, outer, inner)
     for dd, r, wg, nw in ((2, 0, 0, 0), (4, 1, 1, 8), (8, 7, 2, 16), (2, 64, 1, 12), (4, 33, 3, 6),
-                          (2, 5, 2, 16))
+                          (2, 5, 2, 16), (6, 16, 2, 12))
     for t, outer, inner in STREAM_SHAPES
+] + [
+    # ring prologue issued before x has landed (the compiler's full wait then covers the copies)
+    ({"sdig_xfirst": -1, "sdig_rows": r}, t, outer, inner)
+    for r in (0, 3) for t, outer, inner in STREAM_SHAPES
 ]
 
 
