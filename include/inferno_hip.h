@@ -83,7 +83,7 @@ int ihip_shutdown(void);
  * (1 always / -1 never use the persistent kernel), "pers_bufs" (its register
  * buffers, 2..4), "wide_fp32" (1: fp32 activations instead of the default
  * integer digits).  Q6_K/Q8_0/IQ4_NL: "sdig_rows" (rows per chunk, 1..64),
- * "sdig_depth" (LDS ring slots, 2 or 4), "sdig_wg_per_cu", "sdig_waves" (6, 8,
+ * "sdig_depth" (LDS ring slots per wave, 2, 4 or 6), "sdig_wg_per_cu", "sdig_waves" (6, 8,
  * 12, 16), "sdig_off" (1: the fp32-activation streamed kernel, whose
  * "stream_rows" and "stream_wg_per_cu" then apply). */
 int ihip_set_tuning(const char *name, int value);

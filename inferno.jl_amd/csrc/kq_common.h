@@ -114,6 +114,19 @@ __device__ __forceinline__ uint32_t lds_read_u16(const uint8_t *lds, uint32_t of
     return *reinterpret_cast<const uint16_t *>(lds + off);
 }
 
+// One direct-to-LDS copy: lane l's 16 bytes at `src` land at LDS byte address
+// lds + 16 l.  Inline assembly, so that the compiler does not track it: as a
+// compiler-visible LDS write it would make later LDS reads it cannot prove
+// disjoint wait for every copy in flight (vmcnt(0)), including copies issued
+// ahead for later rows; kernels using it wait with explicit s_waitcnt vmcnt.
+__device__ __forceinline__ void lds_copy16(const void *src, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+
 // Workgroup execution barrier without a memory fence.  __syncthreads()
 // carries a workgroup-scope release fence, which makes the compiler wait for
 // every outstanding direct-to-LDS copy (they count as LDS writes), including

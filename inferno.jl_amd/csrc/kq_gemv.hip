@@ -1149,11 +1149,36 @@ struct SXD {
     float poison;     // 0, or NaN when the lane's x slice holds a non-finite value
 };
 
-// Load the lane's 32 elements of x; returns false for a lane past the
-// segment's blocks (its loads read block 0 and staged_dig_x zeroes them).
+// Issue the loads of the lane's 32 elements of x; returns false for a lane
+// past the segment's blocks (its loads read block 0 and staged_dig_x zeroes
+// them).  The loads are inline assembly the compiler does not track: the
+// caller issues them ahead of the ring's direct-to-LDS copies, waits for them
+// with an explicit s_waitcnt vmcnt(copies issued since) and then releases the
+// registers with staged_dig_pin.  (The compiler's own wait before the first
+// use of x would be a vmcnt(0): it treats direct-to-LDS copies and register
+// loads as completing out of order, so the digits would wait for every copy.)
+typedef float sdig_f4 __attribute__((ext_vector_type(4))); // a register quad for asm operands
+
+__device__ __forceinline__ float4 sdig_gload16(const float *base, int byte_off)
+{
+    sdig_f4 v;
+    switch (byte_off) { // compile-time after unrolling: the immediate offset form
+#define IHIP_XL(O)                                                                             \
+    case O:                                                                                    \
+        asm volatile("global_load_dwordx4 %0, %1, off offset:" #O : "=v"(v) : "v"(base) : "memory"); \
+        break;
+        IHIP_XL(0) IHIP_XL(16) IHIP_XL(32) IHIP_XL(48) IHIP_XL(64) IHIP_XL(80) IHIP_XL(96) IHIP_XL(112)
+        IHIP_XL(128) IHIP_XL(144) IHIP_XL(256) IHIP_XL(272) IHIP_XL(384) IHIP_XL(400)
+#undef IHIP_XL
+    default:
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(base + byte_off / 4) : "memory");
+    }
+    return __builtin_bit_cast(float4, v);
+}
+
 template <int FMT>
-__device__ __forceinline__ bool staged_dig_load(const float *xseg, int lane,
-                                                int seg_blocks, float4 (&v)[8])
+__device__ __forceinline__ bool staged_dig_issue(const float *xseg, int lane,
+                                                 int seg_blocks, float4 (&v)[8])
 {
     bool active;
     if constexpr (FMT == kQ6_K) {
@@ -1162,17 +1187,28 @@ __device__ __forceinline__ bool staged_dig_load(const float *xseg, int lane,
         const float *base = xseg + (active ? 256 * bs + 128 * n + l0 : 0);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float4 *q = reinterpret_cast<const float4 *>(base + 32 * g);
-            v[2 * g] = q[0];
-            v[2 * g + 1] = q[1];
+            v[2 * g] = sdig_gload16(base, 128 * g);
+            v[2 * g + 1] = sdig_gload16(base, 128 * g + 16);
         }
     } else {
         active = lane < seg_blocks;
-        const float4 *q = reinterpret_cast<const float4 *>(xseg + (active ? 32 * lane : 0));
+        const float *base = xseg + (active ? 32 * lane : 0);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) v[t] = q[t];
+        for (int t = 0; t < 8; ++t) v[t] = sdig_gload16(base, 16 * t);
     }
     return active;
+}
+
+// After the explicit wait for the loads of staged_dig_issue: the registers may
+// be read from here on (an empty statement the compiler cannot move them across).
+__device__ __forceinline__ void staged_dig_pin(float4 (&v)[8])
+{
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        sdig_f4 r = __builtin_bit_cast(sdig_f4, v[t]);
+        asm volatile("" : "+v"(r));
+        v[t] = __builtin_bit_cast(float4, r);
+    }
 }
 
 // The lane's digits, exponent and accumulator starts from its loaded x.
@@ -1219,14 +1255,13 @@ __device__ __forceinline__ void staged_dig_x(float4 (&v)[8], bool active, SXD &X
     }
 }
 
-// a * b + c for a, b in the signed 24-bit range (v_mad_i32_i24, full rate;
-// the compiler cannot prove the range and would use the quarter-rate 32-bit
-// multiply).
+// a * b + c for a, b in the signed 24-bit range.  The shifts state the range
+// to the compiler, which then selects the full-rate v_mad_i32_i24 (it takes
+// the low 24 bits of each factor, so the shifts fold away) instead of the
+// quarter-rate 32-bit multiply.
 __device__ __forceinline__ int mad_i24(int a, int b, int c)
 {
-    int d;
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
+    return ((a << 8) >> 8) * ((b << 8) >> 8) + c;
 }
 
 // Q6_K block at byte `bo` of the LDS tile (lane geometry of q6_dot).
@@ -1333,7 +1368,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
                                                        const float *x, // not restrict: its loads stay above the copies
                                                        float *y, int outer, int nblk, int rpc,
                                                        ArgPart *__restrict__ parts,
-                                                       const float *resid, int xfirst)
+                                                       const float *resid)
 {
     using F = SFmt<FMT>;
     // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
@@ -1377,33 +1412,26 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     };
     // item k's row segment into slot k % D (k past the wave's items: its last
     // item's row again, into a slot no remaining item uses)
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
     auto issue = [&](int k) {
         const int kk = max(0, min(k, nitems - 1));
         const uint8_t *src = seg0 + (size_t)item_row(kk) * row_bytes;
-        uint8_t *dst = ring + my_ring + (k % D) * SLOT;
+        const uint32_t dst = ring_lds + my_ring + (uint32_t)((k % D) * SLOT);
 #pragma unroll
-        for (int i = 0; i < IPR; ++i) {
-            const int c = min(64 * i + lane, chunks16 - 1);
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(src + 16 * (size_t)c),
-                (__attribute__((address_space(3))) void *)(dst + 1024 * i), 16, 0, 0);
-        }
+        for (int i = 0; i < IPR; ++i)
+            lds_copy16(src + 16 * (size_t)min(64 * i + lane, chunks16 - 1), dst + 1024 * i);
     };
 
-    // x first and waited for on its own, then the first D rows' copies, then
-    // the digits: with copies in flight the compiler's wait before the first
-    // use of x would be a full vmcnt(0) (it treats LDS-DMA and register loads
-    // as completing out of order), which holds the digits until every
-    // prologue copy has landed; x comes from L2 in a fraction of that.
+    // x first, then the first D rows' copies, all in flight together; the
+    // digits wait only for x (vmcnt counts completions in issue order)
     float4 xv[8];
-    const bool xact = staged_dig_load<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
-    if (xfirst)
-        __builtin_amdgcn_s_waitcnt(0);
-    asm volatile("" ::: "memory");
+    const bool xact = staged_dig_issue<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < D; ++k)
         issue(k);
+    wait_vmcnt(D * IPR);
+    staged_dig_pin(xv);
     __builtin_amdgcn_sched_barrier(0);
     SXD X;
     staged_dig_x<FMT>(xv, xact, X);
@@ -1416,11 +1444,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
         const int row0 = chunk * rpc;
         const int nrows = min(rpc, outer - row0);
         const int mine = worker ? max(0, min(m, (nrows - rl + wps - 1) / wps)) : 0;
-        for (int rr = 0; rr < mine; ++rr, ++k) {
-            // items issued after item k: k + 1 .. max(D, nitems) - 1, at most D - 1
-            // of them; younger epilogue loads and stores only lengthen the wait
-            wait_vmcnt(IPR * min(D - 1, max(D, nitems) - 1 - k));
-            const uint32_t slot = my_ring + (uint32_t)((k % D) * SLOT);
+        // the lane's share of the dot product of the row in ring slot `slot`
+        auto dot_at = [&](uint32_t slot) {
             float v = 0.0f;
             if constexpr (FMT == kQ6_K) {
                 const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
@@ -1433,7 +1458,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
                 if (lane < seg_blocks)
                     v = q80_dot_dig(ring + slot, 34u * lane, X);
             }
-            v = wave_sum(v);
+            return v;
+        };
+        auto finish = [&](int rr, float v) {
             if (nseg == 1) { // the wave holds the whole row: finish it here
                 const int row = row0 + rl + rr * wps;
                 if constexpr (RESID)
@@ -1445,6 +1472,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
             } else if (lane == 0) {
                 part[rl + rr * wps][sg] = v;
             }
+        };
+        for (int rr = 0; rr < mine; ++rr, ++k) {
+            // items issued after item k: k + 1 .. max(D, nitems) - 1, at most D - 1
+            // of them; younger epilogue loads and stores only lengthen the wait
+            wait_vmcnt(IPR * min(D - 1, max(D, nitems) - 1 - k));
+            finish(rr, wave_sum(dot_at(my_ring + (uint32_t)((k % D) * SLOT))));
             if (k + D < nitems)
                 issue(k + D); // slot k % D has been read
         }
@@ -1506,7 +1539,6 @@ static int g_pers_bufs = 0;      // register buffers per wave of the persistent 
 static int g_stream_wg_per_cu = 0; // streamed kernel: cap on workgroups per CU (0 = one per chunk)
 // persistent digit streamed kernel: rows per chunk, ring depth (0 = default), 1 = not used
 static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0, g_sdig_waves = 0;
-static int g_sdig_xfirst = 0; // -1: issue the ring prologue before x has landed
 
 void set_tuning(const char *name, int value)
 {
@@ -1524,7 +1556,6 @@ void set_tuning(const char *name, int value)
     if (!__builtin_strcmp(name, "sdig_off")) g_sdig_off = value;
     if (!__builtin_strcmp(name, "sdig_wg_per_cu")) g_sdig_wg_per_cu = value;
     if (!__builtin_strcmp(name, "sdig_waves")) g_sdig_waves = value;
-    if (!__builtin_strcmp(name, "sdig_xfirst")) g_sdig_xfirst = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -1644,13 +1675,12 @@ template <int FMT, bool ARGMAX, int NWV, int DD>
 static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer, int rpc,
                            int grid, void *parts, hipStream_t s, const float *resid)
 {
-    const int xfirst = g_sdig_xfirst >= 0 ? 1 : 0;
     if (resid)
         hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, true>), dim3(grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid, xfirst);
+                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
     else
         hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, false>), dim3(grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid, xfirst);
+                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
 }
 
 

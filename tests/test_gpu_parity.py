@@ -223,10 +223,6 @@ TUNING_CASES = [
     for dd, r, wg, nw in ((2, 0, 0, 0), (4, 1, 1, 8), (8, 7, 2, 16), (2, 64, 1, 12), (4, 33, 3, 6),
                           (2, 5, 2, 16), (6, 16, 2, 12))
     for t, outer, inner in STREAM_SHAPES
-] + [
-    # ring prologue issued before x has landed (the compiler's full wait then covers the copies)
-    ({"sdig_xfirst": -1, "sdig_rows": r}, t, outer, inner)
-    for r in (0, 3) for t, outer, inner in STREAM_SHAPES
 ]
 
 
@@ -545,6 +541,7 @@ def test_argmax_errors_and_large_ties():
     (512, 4096, 4096, 24),   # the batched prefill workload, sampled tokens
     (70, 300, 2048, None),   # ragged tiles, every token checked
     (1, 128, 256, None),
+    (33, 129, 1792, None),   # 7 block columns: the ring wraps twice, ragged tiles
 ])
 def test_prefill_q4k(T, outer, inner, check_rows):
     say(f"prefill T={T} {outer}x{inner}")
