@@ -1365,16 +1365,16 @@ constexpr int kSdigMaxRows = 64; // rows per chunk of the persistent streamed ke
 
 template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
 __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
-                                                       const float *x, // not restrict: its loads stay above the copies
-                                                       float *y, int outer, int nblk, int rpc,
-                                                       ArgPart *__restrict__ parts,
+                                                       const float *x, float *y, int outer, int nblk,
+                                                       int rpc, ArgPart *__restrict__ parts,
                                                        const float *resid)
 {
     using F = SFmt<FMT>;
     // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
     // segment re-read its last 16 bytes into the slot's tail), so the number of
-    // copies in flight is a compile-time count and the compiler's own waits for x
-    // need not drain the ring
+    // copies in flight is a compile-time count and the explicit s_waitcnt vmcnt
+    // waits below are exact (x and the copies are inline assembly the compiler
+    // does not wait on by itself)
     constexpr int IPR = (F::SEG_BYTES / 16 + 63) / 64; // copy instructions per row
     constexpr int SLOT = IPR * 1024;
     static_assert(SLOT >= F::SEG_BYTES + 16, "Q8_0 / IQ4_NL read one dword past a segment");
