@@ -1363,6 +1363,48 @@ __device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t 
 
 constexpr int kSdigMaxRows = 64; // rows per chunk of the persistent streamed kernel
 
+// Staged digits of one segment in LDS: per lane 24 digit-plane dwords, 12
+// accumulator starts, the exponent and the poison value (10 quads, quad-major
+// so that a wave's 16-byte reads and writes are conflict-free).
+constexpr int kDigQuads = 10;
+constexpr int sdig_share_cap(int nw) { return nw == 12 ? 6 : nw == 8 ? 2 : 0; }
+
+__device__ __forceinline__ void sxd_store(const SXD &X, uint32_t (*d)[64][4], int lane)
+{
+    uint32_t dw[4 * kDigQuads];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dw[8 * p + t] = X.p[p][t];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) dw[24 + 4 * p + g] = (uint32_t)X.init[p][g];
+    dw[36] = (uint32_t)X.e;
+    dw[37] = __float_as_uint(X.poison);
+    dw[38] = dw[39] = 0;
+#pragma unroll
+    for (int q = 0; q < kDigQuads; ++q)
+        *reinterpret_cast<uint4 *>(d[q][lane]) = make_uint4(dw[4 * q], dw[4 * q + 1], dw[4 * q + 2], dw[4 * q + 3]);
+}
+
+__device__ __forceinline__ void sxd_load(SXD &X, const uint32_t (*d)[64][4], int lane)
+{
+#pragma unroll
+    for (int q = 0; q < kDigQuads; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(d[q][lane]);
+        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q + e;
+            if (i < 24) X.p[i / 8][i % 8] = vv[e];
+            else if (i < 36) X.init[(i - 24) / 4][(i - 24) % 4] = (int)vv[e];
+            else if (i == 36) X.e = (int)vv[e];
+            else if (i == 37) X.poison = __uint_as_float(vv[e]);
+        }
+    }
+}
+
 template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
 __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
                                                        const float *x, float *y, int outer, int nblk,
@@ -1378,7 +1420,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     constexpr int IPR = (F::SEG_BYTES / 16 + 63) / 64; // copy instructions per row
     constexpr int SLOT = IPR * 1024;
     static_assert(SLOT >= F::SEG_BYTES + 16, "Q8_0 / IQ4_NL read one dword past a segment");
+    // segments whose digits can be staged in LDS (none for the lm_head: its 32 KB
+    // workgroups run four to a CU, which the staging area would halve)
+    constexpr int SHC = ARGMAX ? 0 : sdig_share_cap(NW);
     __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * SLOT];
+    __shared__ __attribute__((aligned(16))) uint32_t digs[SHC > 0 ? SHC : 1][kDigQuads][64][4];
     __shared__ float part[kSdigMaxRows][8];
     __shared__ unsigned long long wkey[NW];
     __shared__ uint32_t wflag[NW];
@@ -1391,6 +1437,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     const int wps = NW / nseg;                                   // waves per segment
     const int sg = w % nseg, rl = w / nseg;
     const bool worker = rl < wps; // waves past nseg * wps only join the barriers
+    // several waves per segment: the first loads x and forms the digits, the
+    // others take them from LDS (x crosses L2 -> CU once per segment, not per wave)
+    const bool share = SHC > 0 && nseg <= SHC && wps >= 2; // workgroup-uniform
+    const bool producer = !share || rl == 0;
     const int nchunks = (outer + rpc - 1) / rpc;
     const int seg_blocks = min(F::SEG_BLOCKS, nblk - sg * F::SEG_BLOCKS);
     const int chunks16 = seg_blocks * bb / 16; // whole 8-block groups: host-checked
@@ -1425,16 +1475,28 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     // x first, then the first D rows' copies, all in flight together; the
     // digits wait only for x (vmcnt counts completions in issue order)
     float4 xv[8];
-    const bool xact = staged_dig_issue<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
+    bool xact = false;
+    if (producer) // wave-uniform
+        xact = staged_dig_issue<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < D; ++k)
         issue(k);
-    wait_vmcnt(D * IPR);
-    staged_dig_pin(xv);
-    __builtin_amdgcn_sched_barrier(0);
     SXD X;
-    staged_dig_x<FMT>(xv, xact, X);
+    if (producer) {
+        wait_vmcnt(D * IPR);
+        staged_dig_pin(xv);
+        __builtin_amdgcn_sched_barrier(0);
+        staged_dig_x<FMT>(xv, xact, X);
+        if (share)
+            sxd_store(X, digs[sg], lane);
+    }
+    if (share) { // workgroup-uniform
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (!producer)
+            sxd_load(X, digs[sg], lane);
+    }
 
     unsigned long long key = 0;
     uint32_t fl = 0;
@@ -1656,8 +1718,8 @@ static int stream_grid(int outer, int rpc)
 template <int FMT>
 constexpr bool sdig_fits(int nw, int d)
 {
-    return nw * d * ((SFmt<FMT>::SEG_BYTES / 16 + 63) / 64) * 1024 + kSdigMaxRows * 8 * 4 + 2048 <=
-           160 * 1024;
+    return nw * d * ((SFmt<FMT>::SEG_BYTES / 16 + 63) / 64) * 1024 + sdig_share_cap(nw) * kDigQuads * 1024 +
+               kSdigMaxRows * 8 * 4 + 2048 <= 160 * 1024;
 }
 
 // The persistent digit kernel: nseg <= 8 segments of 2048 columns; waves per
@@ -1723,7 +1785,7 @@ static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner
     const int nwv = sdig_waves(nseg);
     if (nwv == 12) {
         if (dd == 6 && sdig_fits<FMT>(12, 6)) launch_sdig_nd<FMT, ARGMAX, 12, sdig_fits<FMT>(12, 6) ? 6 : 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-        else if (dd == 4) launch_sdig_nd<FMT, ARGMAX, 12, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+        else if (dd == 4) launch_sdig_nd<FMT, ARGMAX, 12, sdig_fits<FMT>(12, 4) ? 4 : 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
         else launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
     } else if (nwv == 16) {
         launch_sdig_nd<FMT, ARGMAX, 16, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
