@@ -1264,16 +1264,50 @@ __device__ __forceinline__ int mad_i24(int a, int b, int c)
     return ((a << 8) >> 8) * ((b << 8) >> 8) + c;
 }
 
-// Q6_K block at byte `bo` of the LDS tile (lane geometry of q6_dot).
-__device__ __forceinline__ float q6_dot_dig(const uint8_t *tile, uint32_t bo, int n, int l0,
+// A lane's place in a Q6_K segment (lane geometry of q6_dot): the dword-aligned
+// LDS offsets of its ql, qh and scale bytes and of d within a ring slot, and
+// the byte phase they share (210-byte blocks leave odd blocks 2 bytes past a
+// dword boundary).  Computed once, so a row costs one address add per array.
+struct Q6DigLane {
+    uint32_t a, h, s, d, sh;
+    int c; // which 16 of the lane's 32 elements' scale: l0 >> 4
+};
+
+__device__ __forceinline__ Q6DigLane q6_dig_lane(int lane)
+{
+    const uint32_t bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+    const uint32_t bo = 210u * bs;
+    Q6DigLane L;
+    L.a = (bo + 64 * n + l0) & ~3u;
+    L.h = (bo + 128 + 32 * n + l0) & ~3u;
+    L.s = (bo + 192 + 8 * n) & ~3u;
+    L.d = bo + 208;
+    L.sh = bo & 3u;
+    L.c = (int)(l0 >> 4);
+    return L;
+}
+
+// 8 bytes starting `sh` bytes past the dword-aligned LDS address p.
+__device__ __forceinline__ void lds_read8_at(const uint8_t *p, uint32_t sh, uint32_t &a,
+                                             uint32_t &b)
+{
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+    a = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    b = __builtin_amdgcn_alignbyte(w2, w1, sh);
+}
+
+// The lane's share of one Q6_K block of the ring slot starting at `slot`
+// (dword-aligned).
+__device__ __forceinline__ float q6_dot_dig(const uint8_t *slot, const Q6DigLane &L,
                                             const SXD &X)
 {
     uint32_t A[2], B[2], H[2], S[2];
-    lds_read8_even(tile, bo + 64 * n + l0, A[0], A[1]);
-    lds_read8_even(tile, bo + 64 * n + 32 + l0, B[0], B[1]);
-    lds_read8_even(tile, bo + 128 + 32 * n + l0, H[0], H[1]);
-    lds_read8_even(tile, bo + 192 + 8 * n, S[0], S[1]);
-    const float d = h2f(lds_read_u16(tile, bo + 208));
+    lds_read8_at(slot + L.a, L.sh, A[0], A[1]);
+    lds_read8_at(slot + L.a + 32, L.sh, B[0], B[1]);
+    lds_read8_at(slot + L.h, L.sh, H[0], H[1]);
+    lds_read8_at(slot + L.s, L.sh, S[0], S[1]);
+    const float d = h2f(*reinterpret_cast<const uint16_t *>(slot + L.d));
     int acc[3][4];
 #pragma unroll
     for (int p = 0; p < 3; ++p)
@@ -1295,7 +1329,7 @@ __device__ __forceinline__ float q6_dot_dig(const uint8_t *tile, uint32_t bo, in
         }
     }
     // scale-weighted sums per plane: |acc| <= 8 * 63 * 255, |sc| <= 128 (24-bit products)
-    const int c = l0 >> 4;
+    const int c = L.c;
     int T[3] = {0, 0, 0};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -1458,7 +1492,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     const int mm = max(m, 1);
     auto item_row = [&](int k) { // global row of item k (clamped: always a row of W)
         const int ci = k / mm, rr = k - ci * mm;
-        return min((blockIdx.x + ci * gridDim.x) * rpc + rl + rr * wps, outer - 1);
+        return min(((int)blockIdx.x + ci * (int)gridDim.x) * rpc + rl + rr * wps, outer - 1);
     };
     // item k's row segment into slot k % D (k past the wave's items: its last
     // item's row again, into a slot no remaining item uses)
@@ -1498,6 +1532,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
             sxd_load(X, digs[sg], lane);
     }
 
+    const Q6DigLane q6l = q6_dig_lane(lane); // used by Q6_K only
     unsigned long long key = 0;
     uint32_t fl = 0;
     int k = 0;
@@ -1510,9 +1545,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
         auto dot_at = [&](uint32_t slot) {
             float v = 0.0f;
             if constexpr (FMT == kQ6_K) {
-                const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-                if (bs < seg_blocks)
-                    v = q6_dot_dig(ring, slot + (uint32_t)(210 * bs), n, l0, X);
+                if ((lane >> 3) < seg_blocks)
+                    v = q6_dot_dig(ring + slot, q6l, X);
             } else if constexpr (FMT == kIQ4_NL) {
                 if (lane < seg_blocks)
                     v = iq4nl_dot_dig(ring + slot, 18u * lane, X);
