@@ -1492,6 +1492,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     const int mm = max(m, 1);
     auto item_row = [&](int k) { // global row of item k (clamped: always a row of W)
         const int ci = k / mm, rr = k - ci * mm;
+        // int operands throughout: with an unsigned blockIdx.x the call resolves to
+        // the double overload of min and the row is formed in f64 VALU code
         return min(((int)blockIdx.x + ci * (int)gridDim.x) * rpc + rl + rr * wps, outer - 1);
     };
     // item k's row segment into slot k % D (k past the wave's items: its last
