@@ -85,7 +85,8 @@ int ihip_shutdown(void);
  * integer digits).  Q6_K/Q8_0/IQ4_NL: "sdig_rows" (rows per chunk, 1..64),
  * "sdig_depth" (LDS ring slots per wave, 2, 4 or 6), "sdig_wg_per_cu", "sdig_waves" (6, 8,
  * 12, 16), "sdig_off" (1: the fp32-activation streamed kernel, whose
- * "stream_rows" and "stream_wg_per_cu" then apply). */
+ * "stream_rows" and "stream_wg_per_cu" then apply).  Argmax: "argmax_threads"
+ * (64, 256 or 1024 threads in the kernel that reduces the partials). */
 int ihip_set_tuning(const char *name, int value);
 
 /* ---- weight registry (host entry points use it implicitly) ------------ */

@@ -930,47 +930,53 @@ __device__ __forceinline__ void argmax_store_partial(unsigned long long key, uin
     }
 }
 
-// Reduce `nparts` partials; writes the 0-based token and the IHIP_FLAG_* bits.
-__global__ __launch_bounds__(1024) void k_argmax_finalize(const ArgPart *__restrict__ parts,
-                                                          int nparts, int32_t *token,
-                                                          uint32_t *flags_out)
+// Reduce `nparts` partials with NT threads, U 16-byte partials in flight per
+// thread; writes the 0-based token and the IHIP_FLAG_* bits.  With NT = 64
+// there is no LDS exchange and no barrier; NT = 256 (four partials per thread
+// for the lm_head's ~1000) is the default.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_argmax_finalize(const ArgPart *__restrict__ parts,
+                                                        int nparts, int32_t *token,
+                                                        uint32_t *flags_out)
 {
-    __shared__ unsigned long long wkey[16];
-    __shared__ uint32_t wflag[16];
+    constexpr int NWV = NT / 64, U = NT >= 1024 ? 4 : 16;
     unsigned long long key = 0;
     uint32_t fl = 0;
-    // four 16-byte partials in flight per thread
-    for (int i0 = threadIdx.x; i0 < nparts; i0 += 4 * 1024) {
-        uint4 p[4];
+    for (int i0 = threadIdx.x; i0 < nparts; i0 += U * NT) {
+        uint4 p[U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + 1024 * u;
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + NT * u;
             p[u] = i < nparts ? reinterpret_cast<const uint4 *>(parts)[i] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
             const unsigned long long k = ((unsigned long long)p[u].y << 32) | p[u].x;
             key = k > key ? k : key;
             fl |= p[u].z;
         }
     }
     argmax_wave_reduce(key, fl);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        wkey[wave] = key;
-        wflag[wave] = fl;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long k = wkey[0];
-        uint32_t f = wflag[0];
-        for (int w = 1; w < 16; ++w) {
-            k = wkey[w] > k ? wkey[w] : k;
-            f |= wflag[w];
+    if constexpr (NWV > 1) {
+        __shared__ unsigned long long wkey[NWV];
+        __shared__ uint32_t wflag[NWV];
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (lane == 0) {
+            wkey[wave] = key;
+            wflag[wave] = fl;
         }
-        uint32_t out = f & 3u;
-        int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
-        if (!(f & 4u)) { // every logit was -Inf: index 0 (src/CommonOps.jl:143-161)
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w = 1; w < NWV; ++w) {
+                key = wkey[w] > key ? wkey[w] : key;
+                fl |= wflag[w];
+            }
+        }
+    }
+    if (threadIdx.x == 0) {
+        uint32_t out = fl & 3u;
+        int32_t tok = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+        if (!(fl & 4u)) { // every logit was -Inf: index 0 (src/CommonOps.jl:143-161)
             out |= 4u;
             tok = 0;
         }
@@ -1637,6 +1643,7 @@ static int g_pers_bufs = 0;      // register buffers per wave of the persistent 
 static int g_stream_wg_per_cu = 0; // streamed kernel: cap on workgroups per CU (0 = one per chunk)
 // persistent digit streamed kernel: rows per chunk, ring depth (0 = default), 1 = not used
 static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0, g_sdig_waves = 0;
+static int g_argmax_threads = 0; // argmax finalize: 64, 256 or 1024 threads (0 = 256)
 
 void set_tuning(const char *name, int value)
 {
@@ -1654,6 +1661,7 @@ void set_tuning(const char *name, int value)
     if (!__builtin_strcmp(name, "sdig_off")) g_sdig_off = value;
     if (!__builtin_strcmp(name, "sdig_wg_per_cu")) g_sdig_wg_per_cu = value;
     if (!__builtin_strcmp(name, "sdig_waves")) g_sdig_waves = value;
+    if (!__builtin_strcmp(name, "argmax_threads")) g_argmax_threads = value;
 }
 
 template <int FMT, bool GATEUP>
@@ -1883,6 +1891,27 @@ hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const
 
 bool lm_head_fusable(int vocab) { return stream_rows(vocab, true) <= kStreamMaxRows; }
 
+static void launch_argmax_finalize(const void *ws, int nparts, int32_t *token, uint32_t *flags,
+                                   hipStream_t s)
+{
+    // 256 measured fastest for the lm_head's 1024 partials (against 1024 threads:
+    // -0.9 us per call; a single wave gains nothing)
+    int nt = g_argmax_threads;
+    if (nt != 64 && nt != 256 && nt != 1024)
+        nt = 256;
+    const ArgPart *parts = (const ArgPart *)ws;
+    switch (nt) {
+    case 64:
+        hipLaunchKernelGGL(k_argmax_finalize<64>, dim3(1), dim3(64), 0, s, parts, nparts, token, flags);
+        break;
+    case 256:
+        hipLaunchKernelGGL(k_argmax_finalize<256>, dim3(1), dim3(256), 0, s, parts, nparts, token, flags);
+        break;
+    default:
+        hipLaunchKernelGGL(k_argmax_finalize<1024>, dim3(1), dim3(1024), 0, s, parts, nparts, token, flags);
+    }
+}
+
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s)
@@ -1900,8 +1929,7 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
     const int nblk = hidden / block_elems(type), seg = SFmtSegBlocks(type);
     const int nparts = sdig_usable(type, nblk) ? sdig_grid(vocab, (nblk + seg - 1) / seg)
                                                : stream_grid(vocab, stream_rows(vocab, true));
-    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(1024), 0, s, (const ArgPart *)ws, nparts,
-                       token, flags);
+    launch_argmax_finalize(ws, nparts, token, flags, s);
     return hipGetLastError();
 }
 
@@ -1913,8 +1941,7 @@ hipError_t launch_argmax(const float *v, int64_t n, int32_t *token, uint32_t *fl
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(k_argmax_partials, dim3((unsigned)blocks), dim3(256), 0, s, v, n,
                        (ArgPart *)ws);
-    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(1024), 0, s, (const ArgPart *)ws,
-                       (int)blocks, token, flags);
+    launch_argmax_finalize(ws, (int)blocks, token, flags, s);
     return hipGetLastError();
 }
 

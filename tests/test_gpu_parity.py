@@ -432,7 +432,8 @@ def test_fused_elementwise_kernels():
     (synth.Q8_0, 32000, 2048, 6),
     (synth.Q4_K, 5003, 1024, 7),       # GEMV + standalone argmax path
 ])
-@pytest.mark.parametrize("knobs", [{}, {"sdig_off": 1}, {"sdig_wg_per_cu": 1, "sdig_rows": 7}])
+@pytest.mark.parametrize("knobs", [{}, {"sdig_off": 1}, {"sdig_wg_per_cu": 1, "sdig_rows": 7},
+                                   {"argmax_threads": 64}, {"argmax_threads": 256}])
 def test_lm_head_argmax(t, vocab, hidden, seed, knobs):
     from inferno_hip import _lib
     for k, v in knobs.items():
@@ -519,8 +520,17 @@ def test_argmax_reference_cases(name):
     assert oracle.argmax(v)[0] == want
 
 
-def test_argmax_errors_and_large_ties():
+@pytest.mark.parametrize("threads", [0, 64, 256, 1024])
+def test_argmax_errors_and_large_ties(threads):
     from inferno_hip import FusedKernels as FK, _lib
+    _lib.set_tuning("argmax_threads", threads)
+    try:
+        _argmax_errors_and_large_ties(FK, _lib)
+    finally:
+        _lib.set_tuning("argmax_threads", 0)
+
+
+def _argmax_errors_and_large_ties(FK, _lib):
     for bad in ([1, np.inf], [1, np.nan], [np.nan, np.nan]):
         say(f"argmax error case {bad}")
         with pytest.raises(_lib.IHIPArgumentError):
