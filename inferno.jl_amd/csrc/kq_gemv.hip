@@ -1773,8 +1773,10 @@ static int sdig_waves(int nseg)
     if ((g_sdig_waves == 6 || g_sdig_waves == 8 || g_sdig_waves == 12 || g_sdig_waves == 16) &&
         g_sdig_waves >= nseg)
         return g_sdig_waves;
-    // measured on MI355X (4096 x 12288 Q6_K: 12 waves 12.8 us, 6 waves 14.3 us)
-    return (nseg == 3 || nseg == 6) ? 12 : 8;
+    // measured on MI355X (4096 x 12288 Q6_K: 12 waves 12.8 us, 6 waves 14.3 us;
+    // 4096 x 4096, two segments, 12 against 8 waves: Q8_0 5.98 / 6.26 us, Q6_K
+    // 6.04 / 6.45 us, IQ4_NL 5.79 / 5.99 us)
+    return (nseg == 2 || nseg == 3 || nseg == 6) ? 12 : 8;
 }
 
 template <int FMT, bool ARGMAX, int NWV, int DD>
