@@ -2,27 +2,36 @@
 """Decode hot-path benchmark of the MI355X K-quant library (one GPU).
 
 Headline: Q4_K dequant-fused GEMV, 4096 rows x 4096 columns, batch 1, fp32
-activations (16 Q4_K super-blocks of 144 B per row).  One step = one GEMV
-launch over one weight matrix with x already resident in HBM.
+activations (16 Q4_K super-blocks of 144 B per row), weights and x resident
+in HBM.
 
-Timing.  The 9.4 MB weight fits in the 256 MB Infinity Cache, so the timed
-loop cycles through 64 device copies of the weight (604 MB), the way a
-decode step walks distinct layers; every launch must come from HBM.  The
-launches are captured in a HIP graph (one replay = 64 launches) so that the
-host's per-call cost does not starve the GPU, and the timed region is a pair
-of HIP events recorded on the stream the graph replays on.  `value` is
-algorithmic bytes (weight + x + y, each touched once) x steps / elapsed.
+Step.  The 9.4 MB weight fits in the 256 MB Infinity Cache, so the benchmark
+keeps 64 device copies of it (604 MB) and one step is one sweep over all of
+them: 64 GEMV launches back to back, each on a different copy, the way a
+decode step walks distinct layers; every launch reads its weight from HBM.
+A sweep is one replay of a HIP graph of the 64 launches (so the host's
+per-call cost does not starve the GPU); `--steps K` times K whole sweeps
+between two HIP events recorded on the stream the graph replays on.
+`value` = algorithmic bytes (weight + x + y, each touched once) x 64 x K /
+elapsed; the per-launch time is elapsed / (64 K), reported as
+config.us_per_launch and used for the roofline.
 
-Also reported (the `extras` object): the decode FFN block (gate/up Q4_K
-12288x4096 with the SwiGLU epilogue, then the Q6_K 4096x12288 down
-projection) in microseconds, Q8_0 4096x4096 dequant and GEMV, the Q6_K
-151936x2048 lm_head with fused argmax, the 512-token Q4_K prefill GEMM,
-single-launch latency and the cache-resident rate, each labelled.
+Also reported (`extras`): the floors a single launch of this size cannot
+beat (an empty launch of the same grid, and a fully coalesced read of the
+same 9.4 MB that discards the bytes), the host-pointer drop-in's per-call
+time (x in, y out over PCIe: what a Julia caller of q4_k_gemv! sees), the
+decode FFN block (gate/up Q4_K 12288x4096 with the SwiGLU epilogue, then the
+Q6_K 4096x12288 down projection) in microseconds, Q8_0 4096x4096 dequant and
+GEMV, the int8-activation variant, the Q6_K 151936x2048 lm_head with fused
+argmax, the 512-token Q4_K prefill GEMM, single-launch latency and the
+cache-resident rate, each labelled.
 
-cpu_baseline: the reference's own C kernel (src/kernels/quant_kernels.c,
-compiled from source into oracle/_ref) -- q4_k_gemv on the same workload,
-timed on this host's cores; the oracle's restatement of it when oracle/_ref
-is absent.
+cpu_baseline: the reference's own C kernels (src/kernels/quant_kernels.c,
+compiled from source into oracle/_ref) -- q4_k_gemv on the same workload at
+the reference's default thread count and on all of this host's cores -- and
+the oracle's restatement of the single-threaded fp32 fallback
+(src/ModelCPU.jl:290-306), weights rotated through more than twice the last
+level cache, median and spread of 7 repetitions.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv]
 """
@@ -47,6 +56,7 @@ PEAK_HBM_GBS = 8000.0
 PEAK_FP16_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 WARM_S = 0.05  # seconds of the same launches run before each timed region
+NCOPY = 64     # weight copies of the headline GEMV = launches per step
 
 
 def log(*a):
@@ -56,20 +66,19 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=6400)
-    ap.add_argument("--warmup", type=int, default=640)
+    ap.add_argument("--steps", type=int, default=100, help="timed sweeps of 64 GEMV launches")
+    ap.add_argument("--warmup", type=int, default=10, help="untimed sweeps before timing")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="gemv: the headline GEMV only")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-workload", action="store_true",
-                    help="run the short program the rocprofv3 --pmc traffic runs profile")
+                    help="run the short program the rocprofv3 --pmc runs profile")
     return ap.parse_args()
 
 
 def traffic_bytes():
-    """HBM bytes per Q4_K GEMV launch from the committed FETCH_SIZE / WRITE_SIZE
-    measurement (each counter scaled by what it reads for a plain copy of
-    known size), or None when that record is absent."""
+    """HBM bytes per headline GEMV launch from the committed FETCH_SIZE /
+    WRITE_SIZE measurement (each counter scaled by what it reads for a plain
+    copy of known size), or None when that record is absent."""
     p = ROOT / "profiles" / "q4k_gemv_4096x4096_traffic.json"
     if not p.exists():
         return None
@@ -78,22 +87,16 @@ def traffic_bytes():
     return int(round((g["FETCH_SIZE_KiB"] * d["fetch_factor"] + g["WRITE_SIZE_KiB"] * d["write_factor"]) * 1024))
 
 
-def pmc_workload(torch, synth, D):
-    src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    w = synth.weight(synth.rng_for(0xC0), synth.Q4_K, 4096, 4096)
-    base = torch.from_numpy(w).cuda()
-    ws = [D.DeviceWeight(base.clone(), synth.Q4_K, 4096, 4096) for _ in range(64)]
-    x = torch.from_numpy(synth.activations(synth.rng_for(0xC0 + 1), 4096)).cuda()
-    ys = torch.empty(64, 4096, device="cuda")
-    for _ in range(3):
-        for i in range(64):
-            D.gemv(ws[i], x, ys[i])
-    torch.cuda.synchronize()
-    print("pmc workload done: 3 x 64 MiB copy, 192 Q4_K 4096x4096 GEMV launches", flush=True)
+def floors_lib():
+    import ctypes as C
+    p = ROOT / "inferno.jl_amd" / "lib" / "libinferno_floors.so"
+    if not p.exists():
+        return None
+    L = C.CDLL(str(p))
+    L.ifl_empty.argtypes = [C.c_int, C.c_int, C.c_void_p]
+    L.ifl_read.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_int, C.c_void_p]
+    L.ifl_empty.restype = L.ifl_read.restype = C.c_int
+    return L
 
 
 # ------------------------------------------------------------------ timing --
@@ -121,30 +124,27 @@ class GraphLoop:
                 self.graph.replay()
 
 
-def time_steps(torch, stream, launch, n_rot, steps, warmup):
-    """Time exactly `steps` launches cycling through n_rot operand sets;
-    returns ms for the whole timed region (HIP events on `stream`)."""
-    full = GraphLoop(torch, stream, n_rot, launch)
-    rem = steps % n_rot
-    part = GraphLoop(torch, stream, rem, launch) if rem else None
-    full.replay(max(1, warmup // n_rot))
+def time_sweeps(torch, stream, launch, n_rot, sweeps, warmup):
+    """Time `sweeps` whole replays of a graph of launch(0..n_rot-1) (one sweep
+    over n_rot operand sets); returns the ms of the timed region, measured by
+    HIP events on `stream`."""
+    g = GraphLoop(torch, stream, n_rot, launch)
+    g.replay(max(1, warmup))
     torch.cuda.synchronize()
     # The GPU's clock drops while the host sets a workload up (graph capture,
     # uploads) and ramps back over milliseconds of work: keep replaying the
     # same launches until about WARM_S seconds of them have run, so the timed
     # region sees the steady-state clock.
     w0 = time.perf_counter()
-    full.replay(1)
+    g.replay(1)
     torch.cuda.synchronize()
     per_replay = max(time.perf_counter() - w0, 1e-6)
-    full.replay(int(WARM_S / per_replay) + 1)
+    g.replay(int(WARM_S / per_replay) + 1)
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    full.replay(steps // n_rot)
-    if part:
-        part.replay(1)
+    g.replay(sweeps)
     t1.record(stream)
     torch.cuda.synchronize()
     return t0.elapsed_time(t1)
@@ -177,12 +177,11 @@ def q4k_gemv(torch, stream, synth, D, oracle, steps, warmup):
     w = synth.weight(rng, synth.Q4_K, outer, inner)
     x = synth.activations(rng, inner)
     nbytes = w.size + 4 * inner + 4 * outer
-    ncopy = 64
     base = torch.from_numpy(w).cuda()
-    ws = [D.DeviceWeight(base.clone(), synth.Q4_K, inner, outer) for _ in range(ncopy)]
+    ws = [D.DeviceWeight(base.clone(), synth.Q4_K, inner, outer) for _ in range(NCOPY)]
     del base
     xd = torch.from_numpy(x).cuda()
-    ys = torch.empty(ncopy, outer, device="cuda")
+    ys = torch.empty(NCOPY, outer, device="cuda")
 
     # parity of the benched configuration (copy 0) against the oracle
     with torch.cuda.stream(stream):
@@ -195,19 +194,48 @@ def q4k_gemv(torch, stream, synth, D, oracle, steps, warmup):
         raise SystemExit(f"Q4_K GEMV parity failed before timing: max err/tol {ratio:.3g}")
 
     def launch(i):
-        D.gemv(ws[i % ncopy], xd, ys[i % ncopy])
+        D.gemv(ws[i % NCOPY], xd, ys[i % NCOPY])
 
-    ms = time_steps(torch, stream, launch, ncopy, steps, warmup)
-    us_per = ms * 1e3 / steps
+    ms = time_sweeps(torch, stream, launch, NCOPY, steps, warmup)
+    us_per = ms * 1e3 / (steps * NCOPY)
     res = dict(bytes=nbytes, ms=ms, us_per_launch=us_per, gbs=nbytes / (us_per * 1e-6) / 1e9,
-               parity_max_err_over_tol=ratio, copies=ncopy)
+               parity_max_err_over_tol=ratio, copies=NCOPY)
     res["single_launch_us"] = single_launch_us(torch, stream, launch)
-    ms_res = time_steps(torch, stream, lambda i: D.gemv(ws[0], xd, ys[0]), 64, 640, 64)
-    res["cache_resident_gbs"] = nbytes / (ms_res * 1e3 / 640 * 1e-6) / 1e9
+    ms_res = time_sweeps(torch, stream, lambda i: D.gemv(ws[0], xd, ys[0]), NCOPY, 10, 2)
+    res["cache_resident_gbs"] = nbytes / (ms_res * 1e3 / (10 * NCOPY) * 1e-6) / 1e9
+
+    # the floors of one launch of this size, measured the same way
+    F = floors_lib()
+    if F is not None:
+        grid = outer // 16  # the headline kernel's grid: 8 waves x 2 rows per workgroup
+        out = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+        def empty(i):
+            assert F.ifl_empty(grid, 512, torch.cuda.current_stream().cuda_stream) == 0
+
+        def read(i):
+            assert F.ifl_read(ws[i % NCOPY].data.data_ptr(), w.size, 0x9E3779B9, out.data_ptr(),
+                              grid, torch.cuda.current_stream().cuda_stream) == 0
+        n = 10
+        res["floor_empty_us"] = time_sweeps(torch, stream, empty, NCOPY, n, 2) * 1e3 / (n * NCOPY)
+        res["floor_read_us"] = time_sweeps(torch, stream, read, NCOPY, n, 2) * 1e3 / (n * NCOPY)
+
+    # the host-pointer drop-in (ihip_q4_k_gemv: x in and y out over PCIe,
+    # synchronous, the weight uploaded once and found in the cache)
+    from inferno_hip import QuantizedKernels as QK
+    out = np.zeros(outer, np.float32)
+    QK.q4_k_gemv_(out, w, x, inner, outer)
+    reps = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(100):
+            QK.q4_k_gemv_(out, w, x, inner, outer)
+        reps.append((time.perf_counter() - t0) / 100 * 1e6)
+    res["host_pointer_us"] = float(np.median(reps))
     return res
 
 
-def ffn_block(torch, stream, synth, D, steps=600):
+def ffn_block(torch, stream, synth, D, sweeps=100):
     hidden, inter = 4096, 12288
     rng = synth.rng_for(0xC3)
     wg = synth.weight(rng, synth.Q4_K, inter, hidden)
@@ -229,9 +257,8 @@ def ffn_block(torch, stream, synth, D, steps=600):
         k = i % ncopy
         D.ffn_swiglu(*sets[k], xd, h=hs[k], y=ys[k])
 
-    steps = steps - steps % ncopy
-    ms = time_steps(torch, stream, launch, ncopy, steps, 4 * ncopy)
-    us = ms * 1e3 / steps
+    ms = time_sweeps(torch, stream, launch, ncopy, sweeps, 4)
+    us = ms * 1e3 / (sweeps * ncopy)
     # the same block with the post-attention norm folded into gate/up and the
     # residual add into the down projection (x updated in place: the values
     # drift over the steps, the bytes and launches do not)
@@ -242,10 +269,10 @@ def ffn_block(torch, stream, synth, D, steps=600):
         k = i % ncopy
         D.ffn_block(*sets[k], nw, 1e-6, xs[k], h=hs[k])
 
-    ms_n = time_steps(torch, stream, launch_norm, ncopy, steps, 4 * ncopy)
+    ms_n = time_sweeps(torch, stream, launch_norm, ncopy, sweeps, 4)
     return dict(us=us, bytes=nbytes, gbs=nbytes / (us * 1e-6) / 1e9, copies=ncopy,
                 single_launch_us=single_launch_us(torch, stream, launch, 20),
-                norm_residual_us=ms_n * 1e3 / steps)
+                norm_residual_us=ms_n * 1e3 / (sweeps * ncopy))
 
 
 def q8_0_workloads(torch, stream, synth, D):
@@ -261,24 +288,25 @@ def q8_0_workloads(torch, stream, synth, D):
     outs = [torch.empty(outer * inner, device="cuda") for _ in range(ncopy)]
     xd = torch.from_numpy(x).cuda()
     ys = torch.empty(ncopy, outer, device="cuda")
-    n = 8 * ncopy
-    ms = time_steps(torch, stream, lambda i: D.dequantize(ws[i % ncopy], outs[i % ncopy]),
-                    ncopy, n, 2 * ncopy)
-    deq_us = ms * 1e3 / n
+    n = 8
+    ms = time_sweeps(torch, stream, lambda i: D.dequantize(ws[i % ncopy], outs[i % ncopy]),
+                     ncopy, n, 2)
+    deq_us = ms * 1e3 / (n * ncopy)
     gcopy = copies_for(gemv_bytes)
     gws = ws + [D.DeviceWeight(base.clone(), synth.Q8_0, inner, outer)
                 for _ in range(max(0, gcopy - ncopy))]
-    n = 16 * gcopy
-    ms = time_steps(torch, stream, lambda i: D.gemv(gws[i % gcopy], xd, ys[i % ncopy]),
-                    gcopy, n, 2 * gcopy)
-    gemv_us = ms * 1e3 / n
+    n = 16
+    ms = time_sweeps(torch, stream, lambda i: D.gemv(gws[i % gcopy], xd, ys[i % ncopy]),
+                     gcopy, n, 2)
+    gemv_us = ms * 1e3 / (n * gcopy)
     return dict(dequant_us=deq_us, dequant_gbs=deq_bytes / (deq_us * 1e-6) / 1e9,
                 gemv_us=gemv_us, gemv_gbs=gemv_bytes / (gemv_us * 1e-6) / 1e9)
 
 
 def q8k_gemv(torch, stream, synth, D):
     """The int8-activation variant (the reference C numerics) at 4096x4096
-    Q4_K: one step = quantize x to Q8_K + the GEMV, weights rotated through HBM."""
+    Q4_K: one launch pair = quantize x to Q8_K + the GEMV, weights rotated
+    through HBM."""
     outer = inner = 4096
     rng = synth.rng_for(0xC0)
     w = synth.weight(rng, synth.Q4_K, outer, inner)
@@ -294,9 +322,9 @@ def q8k_gemv(torch, stream, synth, D):
     def step(i):
         D.quantize_row_q8k(xd, q8)
         D.gemv_q8k(ws[i % ncopy], q8, ys[i % ncopy])
-    n = 16 * ncopy
-    ms = time_steps(torch, stream, step, ncopy, n, 2 * ncopy)
-    us = ms * 1e3 / n
+    n = 16
+    ms = time_sweeps(torch, stream, step, ncopy, n, 2)
+    us = ms * 1e3 / (n * ncopy)
     return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9)
 
 
@@ -319,9 +347,9 @@ def lm_head(torch, stream, synth, D):
         k = i % ncopy
         D.lm_head_argmax(ws[k], xd, aws[k], logits=logits[k])
 
-    n = 60
-    ms = time_steps(torch, stream, launch, ncopy, n, 4 * ncopy)
-    us = ms * 1e3 / n
+    n = 20
+    ms = time_sweeps(torch, stream, launch, ncopy, n, 4)
+    us = ms * 1e3 / (n * ncopy)
     tok = aws[0].result()
     return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9, token=tok)
 
@@ -335,59 +363,187 @@ def prefill(torch, stream, synth, D):
     Xd = torch.from_numpy(X).cuda()
     Y = torch.empty(T, outer, device="cuda")
     xh = torch.empty(T * inner, dtype=torch.float16, device="cuda")
-    n = 50
-    ms = time_steps(torch, stream, lambda i: D.prefill_q4_k(dw, Xd, Y, xh), 10, n, 40)
-    us = ms * 1e3 / n
+    n = 5
+    ms = time_sweeps(torch, stream, lambda i: D.prefill_q4_k(dw, Xd, Y, xh), 10, n, 4)
+    us = ms * 1e3 / (n * 10)
     flops = 2.0 * T * outer * inner
     return dict(us=us, tflops=flops / (us * 1e-6) / 1e12,
                 mfma_frac=flops / (us * 1e-6) / 1e12 / PEAK_FP16_TFLOPS)
 
 
+def pmc_workload(torch, synth, D):
+    """The program the rocprofv3 --pmc runs profile: a device copy of known
+    size (to calibrate FETCH_SIZE / WRITE_SIZE) and a few launches of each
+    benched kernel with its weights rotated through HBM."""
+    src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    w = synth.weight(synth.rng_for(0xC0), synth.Q4_K, 4096, 4096)
+    base = torch.from_numpy(w).cuda()
+    ws = [D.DeviceWeight(base.clone(), synth.Q4_K, 4096, 4096) for _ in range(NCOPY)]
+    x = torch.from_numpy(synth.activations(synth.rng_for(0xC0 + 1), 4096)).cuda()
+    ys = torch.empty(NCOPY, 4096, device="cuda")
+    for _ in range(3):
+        for i in range(NCOPY):
+            D.gemv(ws[i], x, ys[i])
+    torch.cuda.synchronize()
+    del ws, base
+    # FFN block: 6 sets of gate/up + down
+    hidden, inter = 4096, 12288
+    rng = synth.rng_for(0xC3)
+    wg, wu = (synth.weight(rng, synth.Q4_K, inter, hidden) for _ in range(2))
+    wd = synth.weight(rng, synth.Q6_K, hidden, inter)
+    g0, u0, d0 = (torch.from_numpy(a).cuda() for a in (wg, wu, wd))
+    sets = [(D.DeviceWeight(g0.clone(), synth.Q4_K, hidden, inter),
+             D.DeviceWeight(u0.clone(), synth.Q4_K, hidden, inter),
+             D.DeviceWeight(d0.clone(), synth.Q6_K, inter, hidden)) for _ in range(6)]
+    h = torch.empty(inter, device="cuda")
+    y = torch.empty(hidden, device="cuda")
+    for _ in range(4):
+        for s in sets:
+            D.ffn_swiglu(*s, x, h=h, y=y)
+    torch.cuda.synchronize()
+    del sets, g0, u0, d0
+    # lm_head: 3 copies
+    vocab = 151936
+    wl = synth.weight(synth.rng_for(0xC2), synth.Q6_K, vocab, 2048)
+    b = torch.from_numpy(wl).cuda()
+    del wl
+    ls = [D.DeviceWeight(b.clone(), synth.Q6_K, 2048, vocab) for _ in range(3)]
+    del b
+    xl = x[:2048].contiguous()
+    logits = torch.empty(vocab, device="cuda")
+    aw = D.ArgmaxWorkspace()
+    for _ in range(4):
+        for lw in ls:
+            D.lm_head_argmax(lw, xl, aw, logits=logits)
+    torch.cuda.synchronize()
+    del ls
+    # prefill 512 x 4096 x 4096
+    dw = D.DeviceWeight(torch.from_numpy(w).cuda(), synth.Q4_K, 4096, 4096)
+    X = torch.randn(512, 4096, device="cuda")
+    Y = torch.empty(512, 4096, device="cuda")
+    xh = torch.empty(512 * 4096, dtype=torch.float16, device="cuda")
+    for _ in range(10):
+        D.prefill_q4_k(dw, X, Y, xh)
+    torch.cuda.synchronize()
+    print("pmc workload done: 3 x 64 MiB copy, 192 Q4_K 4096x4096 GEMVs, 24 FFN blocks, "
+          "12 lm_heads, 10 prefills", flush=True)
+
+
 # --------------------------------------------------------------- CPU baseline --
 
-def cpu_baseline(synth, oracle, seconds):
+def _host_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = nproc
+    l3 = 0
+    base = Path("/sys/devices/system/cpu/cpu0/cache")
+    for idx in sorted(base.glob("index*")) if base.exists() else []:
+        try:
+            if (idx / "level").read_text().strip() == "3":
+                s = (idx / "size").read_text().strip()
+                mul = {"K": 1024, "M": 1 << 20, "G": 1 << 30}.get(s[-1], 1)
+                l3 = int(s.rstrip("KMG")) * mul
+                ids = {c.read_text().strip() for c in Path("/sys/devices/system/cpu").glob(
+                    "cpu[0-9]*/cache/" + idx.name + "/shared_cpu_list")}
+                l3 *= max(1, len(ids))  # every distinct L3 slice of the host
+        except (OSError, ValueError):
+            pass
+    return model, nproc, avail, l3
+
+
+def cpu_baseline(synth, oracle):
+    """BASELINE plan: the reference C int8 path at the reference's default
+    thread count and on all cores, the fp32 fallback single-threaded; weights
+    rotated through more than twice the L3; median and spread of 7 runs."""
     import ctypes
     outer = inner = 4096
     rng = synth.rng_for(0xC0)
     w = synth.weight(rng, synth.Q4_K, outer, inner)
     x = synth.activations(rng, inner)
     nbytes = w.size + 8 * inner
-    ncopy = 16  # 151 MB: larger than the host's last-level cache
+    model, nproc, avail, l3 = _host_info()
+    ncopy = max(16, -(-2 * max(l3, 64 << 20) // w.size) + 1)
     ws = [w.copy() for _ in range(ncopy)]
+    # the box's CPU share: OMP_NUM_THREADS when set, else the affinity mask
     env = os.environ.get("OMP_NUM_THREADS")
-    # the reference's default when OMP_NUM_THREADS is unset (src/QuantizedKernels.jl:40-41)
-    threads = int(env) if env and env.isdigit() else max(2, min(8, (os.cpu_count() or 2) // 2))
+    all_cores = int(env) if env and env.isdigit() else avail
+    default_threads = max(2, min(8, nproc // 2))  # src/QuantizedKernels.jl:40-41
     try:
-        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(threads)
+        gomp = ctypes.CDLL("libgomp.so.1")
     except OSError:
-        pass
+        gomp = None
     ref = oracle.ref_lib()
     kind = "reference" if ref is not None else "port"
     out = np.empty(outer, np.float32)
     q8 = np.zeros(inner // 256 * oracle.Q8K_BYTES, np.uint8)
     if ref is not None:
-        def call(k):
+        def int8_call(k):
             ref.q4_k_gemv(ws[k], x, out, q8, inner, outer)
     else:
-        def call(k):
+        def int8_call(k):
             oracle.lib().orc_gemv_q8k(synth.Q4_K, ws[k], x, out, q8, inner, outer)
-    for k in range(ncopy):
-        call(k)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        call(n % ncopy)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= ncopy:
-            break
-    gbs = nbytes * n / el / 1e9
+
+    def f32_call(k):
+        oracle.lib().orc_gemv_f32_serial(synth.Q4_K, ws[k], x, out, inner, outer)
+
+    def runs(call, calls_per_rep, reps=7):
+        k = 0
+        for _ in range(min(ncopy, calls_per_rep)):   # warm-up
+            call(k % ncopy)
+            k += 1
+        ms = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            for _ in range(calls_per_rep):
+                call(k % ncopy)
+                k += 1
+            ms.append((time.perf_counter() - t0) / calls_per_rep * 1e3)
+        return ms
+
+    results = []
+    for label, threads, call in (("int8 reference C, default threads", default_threads, int8_call),
+                                 ("int8 reference C, all cores", all_cores, int8_call),
+                                 ("fp32 fallback, one thread", 1, f32_call)):
+        if gomp is not None:
+            gomp.omp_set_num_threads(threads)
+        t0 = time.perf_counter()
+        call(0)
+        one = time.perf_counter() - t0
+        per_rep = max(3, int(0.6 / max(one, 1e-5)))  # about 0.6 s per repetition
+        ms = runs(call, per_rep)
+        med = float(np.median(ms))
+        results.append(dict(path=label, threads=threads, median_ms=med, min_ms=float(min(ms)),
+                            max_ms=float(max(ms)), calls_per_rep=per_rep, reps=len(ms),
+                            gbs=nbytes / (med * 1e-3) / 1e9))
+        log(f"  {label} ({threads} thr): {med:.3f} ms median [{min(ms):.3f}, {max(ms):.3f}]")
+    if gomp is not None:
+        gomp.omp_set_num_threads(all_cores)
+    head = results[0]
     what = ("the reference's src/kernels/quant_kernels.c q4_k_gemv compiled from source"
             if kind == "reference" else "the oracle's restatement of quant_kernels.c q4_k_gemv")
-    return dict(value=gbs, unit="GB/s", cores=threads, kind=kind,
-                sample=(f"{what} (int8-activation path, OpenMP {threads} threads): "
-                        f"{n} calls of the 4096x4096 Q4_K GEMV over {ncopy} rotated weight "
-                        f"copies in {el:.1f} s, {el / n * 1e3:.3f} ms per call"))
+    return dict(value=head["gbs"], unit="GB/s", cores=head["threads"], kind=kind,
+                sample=(f"{what} (int8-activation path) on the 4096x4096 Q4_K GEMV at the "
+                        f"reference's default clamp(nproc/2, 2, 8) = {head['threads']} threads: "
+                        f"median {head['median_ms']:.3f} ms per call over 7 repetitions of "
+                        f"{head['calls_per_rep']} calls, {ncopy} rotated weight copies "
+                        f"({ncopy * w.size / 2**20:.0f} MiB, > 2x the {l3 / 2**20:.0f} MiB L3)"),
+                cpu_model=model, nproc=nproc, affinity=avail, l3_bytes=l3, copies=ncopy,
+                runs=results)
 
 
 # ----------------------------------------------------------------------- main --
@@ -412,13 +568,21 @@ def main():
     stream = torch.cuda.Stream()
     steps, warmup = max(1, args.steps), max(0, args.warmup)
 
-    log(f"Q4_K GEMV 4096x4096: warmup {warmup}, steps {steps}")
+    log(f"Q4_K GEMV 4096x4096: warmup {warmup} sweeps, {steps} timed sweeps of {NCOPY} launches")
     g = q4k_gemv(torch, stream, synth, D, oracle, steps, warmup)
     log(f"  {g['us_per_launch']:.3f} us/launch, {g['gbs']:.1f} GB/s, single {g['single_launch_us']:.2f} us")
-    extras = {"q4k_gemv_single_launch_us": g["single_launch_us"],
+    extras = {"q4k_gemv_us_per_launch": g["us_per_launch"],
+              "q4k_gemv_single_launch_us": g["single_launch_us"],
               "q4k_gemv_cache_resident_gbs": g["cache_resident_gbs"],
               "q4k_gemv_parity_max_err_over_tol": g["parity_max_err_over_tol"],
-              "q4k_gemv_weight_copies": g["copies"]}
+              "q4k_gemv_weight_copies": g["copies"],
+              "q4k_gemv_host_pointer_us": g["host_pointer_us"]}
+    if "floor_empty_us" in g:
+        log(f"  floors: empty launch {g['floor_empty_us']:.3f} us, coalesced read of the weight "
+            f"{g['floor_read_us']:.3f} us; host-pointer call {g['host_pointer_us']:.1f} us")
+        extras.update(floor_empty_launch_us=g["floor_empty_us"],
+                      floor_read_9437184B_us=g["floor_read_us"],
+                      floor_read_gbs=9437184 / (g["floor_read_us"] * 1e-6) / 1e9)
     if args.only != "gemv":
         log("FFN block 4096/12288")
         f = ffn_block(torch, stream, synth, D)
@@ -446,11 +610,10 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(synth, oracle, args.cpu_seconds)
-        log(f"  {cpu['value']:.2f} GB/s on {cpu['cores']} threads ({cpu['kind']})")
+        log("CPU baseline")
+        cpu = cpu_baseline(synth, oracle)
+        log(f"  {cpu['cpu_model']}, nproc {cpu['nproc']}, L3 {cpu['l3_bytes'] >> 20} MiB")
 
-    ms_per_step = g["ms"] / steps
     line = {
         "metric": METRIC,
         "value": round(g["gbs"], 2),
@@ -458,16 +621,20 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": g["ms"] / steps,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "Q4_K dequant-fused GEMV 4096x4096, batch 1, fp32 x; "
-                               "64 rotated weight copies (HBM-resident, not cache-resident)",
+        "config": {"workload": "Q4_K dequant-fused GEMV 4096x4096, batch 1, fp32 x; one step = "
+                               f"one sweep of {NCOPY} launches over {NCOPY} weight copies "
+                               "(HBM-resident, not cache-resident)",
                    "rows": 4096, "cols": 4096, "weight_bytes": 9437184,
-                   "algorithmic_bytes_per_step": g["bytes"]},
+                   "launches_per_step": NCOPY,
+                   "us_per_launch": round(g["us_per_launch"], 4),
+                   "algorithmic_bytes_per_launch": g["bytes"],
+                   "algorithmic_bytes_per_step": g["bytes"] * NCOPY},
         "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes()},
         "cpu_baseline": cpu,

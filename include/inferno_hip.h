@@ -26,13 +26,24 @@
  *   - Functions without a suffix take HOST pointers and are synchronous,
  *     like the reference.  Weights passed by host pointer are uploaded once
  *     and cached by address (they are immutable after load in the
- *     reference); call ihip_weight_release before freeing or changing one.
+ *     reference).  Every call checks the cached entry against the buffer's
+ *     size, type, shape and sampled content fingerprint
+ *     (ihip_weight_fingerprint) and uploads again on a mismatch, so a freed
+ *     buffer whose address returns with other bytes, or a weight rewritten in
+ *     place, is not served stale.  A rewrite that leaves every sampled
+ *     window unchanged is not seen: call ihip_weight_forget after changing
+ *     a weight in place.
  *   - *_dev functions take DEVICE pointers and an `ihip_stream` (a
  *     hipStream_t passed as void*, NULL = the null stream) and are
  *     asynchronous.  Device weight pointers must be 16-byte aligned.
  *   - Token ids are 0-based (Julia callers add 1).
  *   - Calls from several threads are serialized inside the library; two
  *     *_dev calls that share a workspace must not overlap on the GPU.
+ *   - *_dev functions use no library-owned device memory: scratch, where a
+ *     path needs it, is the caller's (h, xn, workspace arguments), so calls
+ *     on different streams never share a buffer.  The host-pointer entry
+ *     points stage through library buffers on the library's own stream and
+ *     are synchronous.
  */
 #ifndef INFERNO_HIP_H
 #define INFERNO_HIP_H
@@ -96,6 +107,10 @@ int ihip_weight_register(const void *host, size_t bytes, int ggml_type, int inne
 int ihip_weight_release(uint64_t handle);
 /* Release the cache entry of a host pointer (no-op if not cached). */
 int ihip_weight_forget(const void *host);
+/* The fingerprint the host-pointer cache checks: the size and 64 windows of
+ * 16 bytes at evenly spaced offsets (first and last included), hashed.
+ * Needs no device. */
+int ihip_weight_fingerprint(const void *host, size_t bytes, uint64_t *fp);
 /* Device address of a registered weight (for the *_dev entry points). */
 int ihip_weight_device_ptr(uint64_t handle, const void **dev);
 
@@ -197,7 +212,9 @@ int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int 
                   int outer, ihip_stream stream);
 int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n,
                         ihip_stream stream);
-/* h = silu(Wg x) .* (Wu x), one pass over both weights (h: inter floats). */
+/* h = silu(Wg x) .* (Wu x) (h: inter floats).  A matching Q4_K or Q5_K pair
+ * (16-byte aligned) runs as one pass over both weights; any other pair writes
+ * Wg x into h and the up GEMV turns it into silu(h) * (Wu x) in place. */
 int ihip_gate_up_swiglu_dev(int gate_type, const void *wg, int up_type, const void *wu,
                             const float *x, float *h, int hidden, int inter,
                             ihip_stream stream);
@@ -209,12 +226,18 @@ int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *
  * memory (per-workgroup partial maxima; no initialisation needed).  Calls
  * that share a workspace must not overlap on the GPU. */
 #define IHIP_ARGMAX_WS_BYTES 262144
-/* GEMV + fused greedy argmax.  logits may be NULL.  *token and *flags are
- * device int32s (flags: IHIP_FLAG_* bits; the token is meaningless when
- * NAN or POSINF is set). */
+/* GEMV + fused greedy argmax.  *token and *flags are device int32s (flags:
+ * IHIP_FLAG_* bits; the token is meaningless when NAN or POSINF is set).
+ * logits may be NULL when the argmax is fused into the GEMV
+ * (ihip_lm_head_fused: Q6_K or Q8_0, 16-byte aligned w and x, hidden a
+ * multiple of 2048 or 256); otherwise the GEMV writes logits and a second
+ * kernel reduces them, and NULL logits is IHIP_ERR_INVALID. */
 int ihip_lm_head_argmax_dev(int ggml_type, const void *w, const float *x, float *logits,
                             int32_t *token, uint32_t *flags, int hidden, int vocab,
                             void *workspace, ihip_stream stream);
+/* 1 when ihip_lm_head_argmax_dev with these arguments fuses the argmax into
+ * the GEMV (logits may then be NULL), else 0. */
+int ihip_lm_head_fused(int ggml_type, const void *w, const float *x, int hidden, int vocab);
 /* gpu_argmax! (FusedKernels.jl:271-311) with _validate_logits semantics. */
 int ihip_argmax_dev(const float *logits, int64_t n, int32_t *token, uint32_t *flags,
                     void *workspace, ihip_stream stream);
@@ -234,10 +257,14 @@ int ihip_rmsnorm_dev(const float *x, const float *w, float eps, float *out, int 
                      ihip_stream stream);
 /* ihip_ffn_block on device pointers: the norm is folded into the fused gate/up
  * pass (its scale multiplies the row sums) and the residual add into the down
- * projection's epilogue.  h: inter floats of caller scratch. */
+ * projection's epilogue.  h: caller scratch of ihip_ffn_block_scratch_floats()
+ * floats -- inter for a matching Q4_K or Q5_K gate/up pair (which must then be
+ * 16-byte aligned, as must x and norm_w), inter + hidden for any other pair
+ * (the normed input goes to h + inter). */
 int ihip_ffn_block_dev(int gate_type, const void *wg, int up_type, const void *wu, int down_type,
                        const void *wd, const float *norm_w, float eps, float *x, float *h,
                        int hidden, int inter, ihip_stream stream);
+size_t ihip_ffn_block_scratch_floats(int gate_type, int up_type, int hidden, int inter);
 /* Final norm + lm_head + greedy token (src/ModelCPU.jl:1014-1015): xn
  * (hidden floats of caller scratch) receives rmsnorm(x) .* norm_w; the rest
  * is ihip_lm_head_argmax_dev on xn. */

@@ -54,7 +54,37 @@ struct Weight {
     size_t bytes = 0;
     int type = 0, inner = 0, outer = 0;
     const void *host = nullptr;
+    uint64_t fp = 0; // content fingerprint of a weight cached by host address
 };
+
+// Sampled content fingerprint of a host buffer: its size and 64 windows of 16
+// bytes at evenly spaced offsets (the first and the last 16 bytes included),
+// mixed by a 64-bit multiply / xor-shift hash.  About 1 KB is read whatever
+// the size, so it is checked on every host-pointer call.
+constexpr int kFpWindows = 64;
+
+uint64_t fp_mix(uint64_t h, uint64_t v)
+{
+    h ^= v + 0x9e3779b97f4a7c15ull + (h << 6) + (h >> 2);
+    h *= 0xff51afd7ed558ccdull;
+    return h ^ (h >> 33);
+}
+
+uint64_t fingerprint(const void *p, size_t n)
+{
+    const uint8_t *b = (const uint8_t *)p;
+    uint64_t h = fp_mix(0x243f6a8885a308d3ull, (uint64_t)n);
+    if (n == 0)
+        return h;
+    const size_t span = n > 16 ? n - 16 : 0;
+    for (int i = 0; i < kFpWindows; ++i) {
+        const size_t off = span * (size_t)i / (kFpWindows - 1);
+        uint64_t w[2] = {0, 0};
+        memcpy(w, b + off, n < 16 ? n : 16);
+        h = fp_mix(fp_mix(h, w[0]), w[1]);
+    }
+    return h;
+}
 
 struct DevBuf {
     void *p = nullptr;
@@ -108,12 +138,17 @@ int check_shape(int type, int inner, int outer)
 
 bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Grow a host-path staging buffer.  Only the host-pointer entry points use
+// these buffers, on the library stream; work still queued there (an earlier
+// call that failed half-way) finishes before the old buffer is freed.
 int ensure(DevBuf &b, size_t need)
 {
     if (b.cap >= need)
         return IHIP_OK;
-    if (b.p)
+    if (b.p) {
+        HIPCHK(hipStreamSynchronize(ctx().stream));
         HIPCHK(hipFree(b.p));
+    }
     b.p = nullptr;
     b.cap = 0;
     const size_t cap = need < 4096 ? 4096 : need;
@@ -188,6 +223,7 @@ int upload_locked(const void *host, size_t bytes, int type, int inner, int outer
     w.inner = inner;
     w.outer = outer;
     w.host = cache_by_host ? host : nullptr;
+    w.fp = cache_by_host ? fingerprint(host, bytes) : 0;
     HIPCHK(hipMalloc(&w.dev, bytes));
     hipError_t e = hipMemcpy(w.dev, host, bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -203,7 +239,10 @@ int upload_locked(const void *host, size_t bytes, int type, int inner, int outer
 }
 
 // Device copy of a host weight, uploaded on first sight and cached by its
-// host address (weights are immutable after load in the reference).
+// host address (weights are immutable after load in the reference).  The
+// entry is reused only while the shape, type and sampled content fingerprint
+// still match: a buffer freed and its address reused for other bytes, or a
+// weight rewritten in place, is uploaded again.
 int resolve_locked(const void *host, int type, int inner, int outer, const void **dev)
 {
     Ctx &c = ctx();
@@ -211,11 +250,15 @@ int resolve_locked(const void *host, int type, int inner, int outer, const void 
     auto hi = c.by_host.find(host);
     if (hi != c.by_host.end()) {
         const Weight &w = c.by_handle[hi->second];
-        if (w.bytes == bytes && w.type == type && w.inner == inner && w.outer == outer) {
+        if (w.bytes == bytes && w.type == type && w.inner == inner && w.outer == outer &&
+            w.fp == fingerprint(host, bytes)) {
             *dev = w.dev;
             return IHIP_OK;
         }
-        RET_IF(release_handle_locked(hi->second)); // same address, new shape: re-upload
+        // same address, new shape or new bytes: drop the stale copy (after any
+        // queued host-path work that reads it) and upload again
+        HIPCHK(hipStreamSynchronize(c.stream));
+        RET_IF(release_handle_locked(hi->second));
     }
     uint64_t h = 0;
     RET_IF(upload_locked(host, bytes, type, inner, outer, true, &h));
@@ -238,54 +281,65 @@ bool fast_ok(int type, const void *w, const float *x, int inner)
     return true;
 }
 
-// resid != nullptr: out = resid + W x (resid may be out)
+// resid != nullptr: out = epi_apply(resid, W x, epi) row by row: the residual
+// add (resid may be out) or the SwiGLU against the gate row in out.
 int gemv_dev_locked(int type, const void *w, const float *x, float *out, int inner, int outer,
-                    hipStream_t s, const float *resid = nullptr)
+                    hipStream_t s, const float *resid = nullptr, int epi = kEpiAdd)
 {
     RET_IF(check_shape(type, inner, outer));
     if (!w || !x || !out)
         return fail(IHIP_ERR_INVALID, "null pointer");
     hipError_t e = fast_ok(type, w, x, inner)
-                       ? launch_gemv(type, w, x, out, inner, outer, s, resid)
-                       : launch_gemv_generic(type, w, x, out, inner, outer, s, resid);
+                       ? launch_gemv(type, w, x, out, inner, outer, s, resid, epi)
+                       : launch_gemv_generic(type, w, x, out, inner, outer, s, resid, epi);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "gemv launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;
 }
 
-// norm_w != nullptr: the input is rmsnorm(x) .* norm_w (folded into the fused
-// kernel; a one-workgroup norm kernel ahead of the unfused path)
+bool gate_up_fused(int gt, const void *wg, int ut, const void *wu, const float *x, int hidden,
+                   const float *norm_w)
+{
+    return gate_up_fusable(gt, ut) && fast_ok(gt, wg, x, hidden) && al16(wu) &&
+           (!norm_w || al16(norm_w));
+}
+
+// h = silu(Wg n) .* (Wu n) with n = x, or n = rmsnorm(x) .* norm_w when norm_w
+// is given.  A matching Q4_K/Q5_K pair runs as one fused pass (the norm folded
+// in).  Any other pair writes g into h, and the up GEMV's epilogue turns h
+// into silu(h) * u in place; a norm then goes first into xn (hidden floats
+// of caller scratch).  No library buffer is touched.
 int gate_up_dev_locked(int gt, const void *wg, int ut, const void *wu, const float *x, float *h,
                        int hidden, int inter, hipStream_t s, const float *norm_w = nullptr,
-                       float eps = 0.0f)
+                       float eps = 0.0f, float *xn = nullptr)
 {
     RET_IF(check_shape(gt, hidden, inter));
     RET_IF(check_shape(ut, hidden, inter));
     if (!wg || !wu || !x || !h)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    if (gate_up_fusable(gt, ut) && fast_ok(gt, wg, x, hidden) && al16(wu) &&
-        (!norm_w || al16(norm_w))) {
+    if (gate_up_fused(gt, wg, ut, wu, x, hidden, norm_w)) {
         hipError_t e = launch_gate_up_swiglu(gt, wg, wu, x, h, hidden, inter, s, norm_w, eps);
         if (e != hipSuccess)
             return fail(IHIP_ERR_HIP, "gate/up launch failed: %s", hipGetErrorString(e));
         return IHIP_OK;
     }
-    Ctx &c = ctx();
     if (norm_w) {
-        RET_IF(ensure(c.nrm, sizeof(float) * (size_t)hidden));
-        hipError_t e = launch_rmsnorm(x, norm_w, eps, (float *)c.nrm.p, hidden, s);
+        if (!xn)
+            return fail(IHIP_ERR_INVALID, "the norm of an unfused gate/up pair needs scratch");
+        hipError_t e = launch_rmsnorm(x, norm_w, eps, xn, hidden, s);
         if (e != hipSuccess)
             return fail(IHIP_ERR_HIP, "rmsnorm launch failed: %s", hipGetErrorString(e));
-        x = (const float *)c.nrm.p;
+        x = xn;
     }
-    // unfused: g -> h, u -> scratch, then h = silu(h) * u
-    RET_IF(ensure(c.t, sizeof(float) * (size_t)inter));
     RET_IF(gemv_dev_locked(gt, wg, x, h, hidden, inter, s));
-    RET_IF(gemv_dev_locked(ut, wu, x, (float *)c.t.p, hidden, inter, s));
-    hipError_t e = launch_mlp_gate_mul(h, (const float *)c.t.p, inter, s);
-    if (e != hipSuccess)
-        return fail(IHIP_ERR_HIP, "swiglu launch failed: %s", hipGetErrorString(e));
-    return IHIP_OK;
+    return gemv_dev_locked(ut, wu, x, h, hidden, inter, s, h, kEpiSwiglu);
+}
+
+// Whether the lm_head runs with the argmax fused into its GEMV (no logits
+// buffer needed).
+bool lm_head_fused(int type, const void *w, const float *x, int hidden, int vocab)
+{
+    return (type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden) && lm_head_fusable(vocab);
 }
 
 int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, int32_t *token,
@@ -294,19 +348,18 @@ int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, i
     RET_IF(check_shape(type, hidden, vocab));
     if (!w || !x || !token || !flags || !ws)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    if ((type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden) && lm_head_fusable(vocab)) {
+    if (lm_head_fused(type, w, x, hidden, vocab)) {
         hipError_t e = launch_lm_head_argmax(type, w, x, logits, token, flags, hidden, vocab, ws, s);
         if (e != hipSuccess)
             return fail(IHIP_ERR_HIP, "lm_head launch failed: %s", hipGetErrorString(e));
         return IHIP_OK;
     }
-    float *lg = logits;
-    if (!lg) {
-        RET_IF(ensure(ctx().t, sizeof(float) * (size_t)vocab));
-        lg = (float *)ctx().t.p;
-    }
-    RET_IF(gemv_dev_locked(type, w, x, lg, hidden, vocab, s));
-    hipError_t e = launch_argmax(lg, vocab, token, flags, ws, s);
+    if (!logits)
+        return fail(IHIP_ERR_INVALID,
+                    "this lm_head (type %d, %d x %d) runs the GEMV and the argmax separately: "
+                    "pass a logits buffer (ihip_lm_head_fused tells)", type, vocab, hidden);
+    RET_IF(gemv_dev_locked(type, w, x, logits, hidden, vocab, s));
+    hipError_t e = launch_argmax(logits, vocab, token, flags, ws, s);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "argmax launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;
@@ -472,6 +525,20 @@ int ihip_set_tuning(const char *name, int value)
     return IHIP_OK;
 }
 
+size_t ihip_ffn_block_scratch_floats(int gate_type, int up_type, int hidden, int inter)
+{
+    if (hidden <= 0 || inter <= 0)
+        return 0;
+    return gate_up_fusable(gate_type, up_type) ? (size_t)inter : (size_t)inter + (size_t)hidden;
+}
+
+int ihip_lm_head_fused(int ggml_type, const void *w, const float *x, int hidden, int vocab)
+{
+    if (!known_type(ggml_type) || hidden <= 0 || vocab <= 0 || hidden % block_elems(ggml_type))
+        return 0;
+    return lm_head_fused(ggml_type, w, x, hidden, vocab) ? 1 : 0;
+}
+
 int ihip_weight_register(const void *host, size_t bytes, int ggml_type, int inner, int outer,
                          uint64_t *handle)
 {
@@ -502,6 +569,14 @@ int ihip_weight_forget(const void *host)
     if (it == c.by_host.end())
         return IHIP_OK;
     return release_handle_locked(it->second);
+}
+
+int ihip_weight_fingerprint(const void *host, size_t bytes, uint64_t *fp)
+{
+    if (!fp || (!host && bytes))
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    *fp = fingerprint(host, bytes);
+    return IHIP_OK;
 }
 
 int ihip_weight_device_ptr(uint64_t handle, const void **dev)
@@ -674,8 +749,10 @@ int ihip_ffn_block(int gate_type, const uint8_t *wg, int up_type, const uint8_t 
     RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)hidden));
     RET_IF(copy_in(c.src, norm_w, sizeof(float) * (size_t)hidden));
     RET_IF(ensure(c.h, sizeof(float) * (size_t)inter));
+    RET_IF(ensure(c.nrm, sizeof(float) * (size_t)hidden));
     RET_IF(gate_up_dev_locked(gate_type, dg, up_type, du, (const float *)c.x.p, (float *)c.h.p,
-                              hidden, inter, c.stream, (const float *)c.src.p, eps));
+                              hidden, inter, c.stream, (const float *)c.src.p, eps,
+                              (float *)c.nrm.p));
     RET_IF(gemv_dev_locked(down_type, dd, (const float *)c.h.p, (float *)c.x.p, inter, hidden,
                            c.stream, (const float *)c.x.p));
     HIPCHK(hipMemcpyAsync(x, c.x.p, sizeof(float) * (size_t)hidden, hipMemcpyDeviceToHost, c.stream));
@@ -943,8 +1020,15 @@ int ihip_ffn_block_dev(int gate_type, const void *wg, int up_type, const void *w
     RET_IF(check_shape(down_type, inter, hidden));
     if (!wd || !norm_w || !x || !h)
         return fail(IHIP_ERR_INVALID, "null pointer");
+    float *xn = nullptr;
+    if (!gate_up_fused(gate_type, wg, up_type, wu, x, hidden, norm_w)) {
+        if (gate_up_fusable(gate_type, up_type)) // h was sized for the fused pass
+            return fail(IHIP_ERR_INVALID, "a Q4_K/Q5_K gate/up pair takes 16-byte aligned wg, wu, "
+                                          "x and norm_w");
+        xn = h + inter; // h holds inter + hidden floats for other pairs
+    }
     RET_IF(gate_up_dev_locked(gate_type, wg, up_type, wu, x, h, hidden, inter, (hipStream_t)stream,
-                              norm_w, eps));
+                              norm_w, eps, xn));
     return gemv_dev_locked(down_type, wd, h, x, inter, hidden, (hipStream_t)stream, x);
 }
 

@@ -179,6 +179,18 @@ __device__ __forceinline__ void k_scale_min_pair(uint32_t s0, uint32_t s1, uint3
     mB = ubyte_f(m, 1);
 }
 
+// Row epilogues of the GEMV kernels that read one value r per output row
+// (r may be the output row itself):
+//   kEpiAdd:    y = r + v, the residual add of src/ModelCPU.jl:913-920;
+//   kEpiSwiglu: y = silu(r) * v = r / (1 + exp(-r)) * v, the SwiGLU of an
+//               unfused gate/up pair (r: the gate row already in y, v: the up
+//               row), src/ModelCPU.jl:492-503.
+constexpr int kEpiAdd = 0, kEpiSwiglu = 1;
+__device__ __forceinline__ float epi_apply(float r, float v, int epi)
+{
+    return epi == kEpiSwiglu ? (r / (1.0f + expf(-r))) * v : r + v;
+}
+
 // Wait until at most n of this wave's vector-memory operations are
 // outstanding (n <= 31; expcnt and lgkmcnt are not waited on).
 __device__ __forceinline__ void wait_vmcnt(int n)

@@ -72,7 +72,7 @@ template <int FMT>
 __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t *__restrict__ W,
                                                       const float *__restrict__ x,
                                                       float *y, int outer, int inner,
-                                                      const float *resid)
+                                                      const float *resid, int epi)
 {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t *__restrict_
         acc = fmaf(elem<FMT>(rp + (size_t)(c / BE) * BB, c % BE), x[c], acc);
     acc = wave_sum(acc);
     if (lane == 0)
-        y[row] = resid ? resid[row] + acc : acc; // resid may be y
+        y[row] = resid ? epi_apply(resid[row], acc, epi) : acc; // resid may be y
 }
 
 template <int FMT>
@@ -232,16 +232,16 @@ static unsigned grid_for(int64_t n, int64_t per_block, int64_t cap = 65535)
 }
 
 hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y, int inner,
-                               int outer, hipStream_t s, const float *resid)
+                               int outer, hipStream_t s, const float *resid, int epi)
 {
     const dim3 grid((outer + 3) / 4), block(256);
     const uint8_t *W = (const uint8_t *)w;
     switch (type) {
-    case kQ4_K: hipLaunchKernelGGL(k_gemv_generic<kQ4_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
-    case kQ5_K: hipLaunchKernelGGL(k_gemv_generic<kQ5_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
-    case kQ6_K: hipLaunchKernelGGL(k_gemv_generic<kQ6_K>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
-    case kQ8_0: hipLaunchKernelGGL(k_gemv_generic<kQ8_0>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
-    case kIQ4_NL: hipLaunchKernelGGL(k_gemv_generic<kIQ4_NL>, grid, block, 0, s, W, x, y, outer, inner, resid); break;
+    case kQ4_K: hipLaunchKernelGGL(k_gemv_generic<kQ4_K>, grid, block, 0, s, W, x, y, outer, inner, resid, epi); break;
+    case kQ5_K: hipLaunchKernelGGL(k_gemv_generic<kQ5_K>, grid, block, 0, s, W, x, y, outer, inner, resid, epi); break;
+    case kQ6_K: hipLaunchKernelGGL(k_gemv_generic<kQ6_K>, grid, block, 0, s, W, x, y, outer, inner, resid, epi); break;
+    case kQ8_0: hipLaunchKernelGGL(k_gemv_generic<kQ8_0>, grid, block, 0, s, W, x, y, outer, inner, resid, epi); break;
+    case kIQ4_NL: hipLaunchKernelGGL(k_gemv_generic<kIQ4_NL>, grid, block, 0, s, W, x, y, outer, inner, resid, epi); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -30,6 +30,7 @@
 #include "inferno_hip.h"
 #include "kq_common.h"
 #include "kq_launch.h"
+#include "kq_sdig_plan.h"
 
 namespace ihip {
 
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
                                                     const float *__restrict__ x,
                                                     float *y, int outer, int nblk,
                                                     const float *__restrict__ nw, float eps,
-                                                    const float *resid)
+                                                    const float *resid, int epi)
 {
     using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
         }
         const int row = row0 + r;
         if (lane == 0 && row < outer)
-            y[row] = RESID ? rv[r] + v : v;
+            y[row] = RESID ? epi_apply(rv[r], v, epi) : v;
     }
 }
 
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
                                                          const float *__restrict__ x,
                                                          float *y, int outer, int nblk,
                                                          const float *__restrict__ nw, float eps,
-                                                         const float *resid)
+                                                         const float *resid, int epi)
 {
     using F = KFmt<FMT>;
     constexpr int NM = GATEUP ? 2 : 1;
@@ -613,7 +614,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
                 o = (v[0] / (1.0f + expf(-v[0]))) * v[1]; // src/ModelCPU.jl:492-503
             // every lane holds the row's value: an unpredicated store (a row
             // past `outer` re-reads and rewrites row outer - 1 with its own value)
-            y[min(row, outer - 1)] = RESID ? RVq[r] + o : o;
+            y[min(row, outer - 1)] = RESID ? epi_apply(RVq[r], o, epi) : o;
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -863,7 +864,6 @@ struct ArgPart {
     uint32_t pad;
 };
 static_assert(sizeof(ArgPart) == 16, "ArgPart layout");
-constexpr int kArgMaxParts = 16384; // IHIP_ARGMAX_WS_BYTES / sizeof(ArgPart)
 static_assert(kArgMaxParts * sizeof(ArgPart) == IHIP_ARGMAX_WS_BYTES, "argmax workspace size");
 
 __device__ __forceinline__ uint32_t ordered_bits(float v)
@@ -1015,7 +1015,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
                                                          float *y, int outer,
                                                          int nblk, int rpc,
                                                          ArgPart *__restrict__ parts,
-                                                         const float *resid)
+                                                         const float *resid, int epi)
 {
     using F = SFmt<FMT>;
     constexpr int SLOT = F::SEG_BYTES + 16; // Q8_0 reads one dword past a segment
@@ -1104,7 +1104,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restri
             for (int k = 0; k < NW; ++k)
                 v += part[i][k];
             if (y)
-                y[row0 + i] = resid ? rv + v : v; // i == tid; resid may be y
+                y[row0 + i] = resid ? epi_apply(rv, v, epi) : v; // i == tid; resid may be y
             if constexpr (ARGMAX)
                 argmax_fold(v, (uint32_t)(row0 + i), key, fl);
         }
@@ -1187,21 +1187,10 @@ __device__ __forceinline__ bool staged_dig_issue(const float *xseg, int lane,
                                                  int seg_blocks, float4 (&v)[8])
 {
     bool active;
-    if constexpr (FMT == kQ6_K) {
-        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-        active = bs < seg_blocks;
-        const float *base = xseg + (active ? 256 * bs + 128 * n + l0 : 0);
+    const float *base = xseg + sdig_x_lane(FMT, lane, seg_blocks, active);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            v[2 * g] = sdig_gload16(base, 128 * g);
-            v[2 * g + 1] = sdig_gload16(base, 128 * g + 16);
-        }
-    } else {
-        active = lane < seg_blocks;
-        const float *base = xseg + (active ? 32 * lane : 0);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) v[t] = sdig_gload16(base, 16 * t);
-    }
+    for (int t = 0; t < 8; ++t)
+        v[t] = sdig_gload16(base, sdig_x_load_byte(FMT, t));
     return active;
 }
 
@@ -1270,29 +1259,6 @@ __device__ __forceinline__ int mad_i24(int a, int b, int c)
     return ((a << 8) >> 8) * ((b << 8) >> 8) + c;
 }
 
-// A lane's place in a Q6_K segment (lane geometry of q6_dot): the dword-aligned
-// LDS offsets of its ql, qh and scale bytes and of d within a ring slot, and
-// the byte phase they share (210-byte blocks leave odd blocks 2 bytes past a
-// dword boundary).  Computed once, so a row costs one address add per array.
-struct Q6DigLane {
-    uint32_t a, h, s, d, sh;
-    int c; // which 16 of the lane's 32 elements' scale: l0 >> 4
-};
-
-__device__ __forceinline__ Q6DigLane q6_dig_lane(int lane)
-{
-    const uint32_t bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-    const uint32_t bo = 210u * bs;
-    Q6DigLane L;
-    L.a = (bo + 64 * n + l0) & ~3u;
-    L.h = (bo + 128 + 32 * n + l0) & ~3u;
-    L.s = (bo + 192 + 8 * n) & ~3u;
-    L.d = bo + 208;
-    L.sh = bo & 3u;
-    L.c = (int)(l0 >> 4);
-    return L;
-}
-
 // 8 bytes starting `sh` bytes past the dword-aligned LDS address p.
 __device__ __forceinline__ void lds_read8_at(const uint8_t *p, uint32_t sh, uint32_t &a,
                                              uint32_t &b)
@@ -1355,9 +1321,10 @@ __device__ __forceinline__ float q80_dot_dig(const uint8_t *row_lds, uint32_t of
     const uint32_t o = off + 2;
     const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
     const uint32_t sh = o & 3u;
-    uint32_t w[9];
+    constexpr int NDW = sdig_blk_dwords(kQ8_0);
+    uint32_t w[NDW];
 #pragma unroll
-    for (int i = 0; i < 9; ++i) w[i] = p[i];
+    for (int i = 0; i < NDW; ++i) w[i] = p[i];
     uint32_t a0 = (uint32_t)X.init[0][0], a1 = (uint32_t)X.init[1][0];
     int a2 = 0;
 #pragma unroll
@@ -1380,9 +1347,10 @@ __device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t 
     const uint32_t o = off + 2;
     const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
     const uint32_t sh = o & 3u;
-    uint32_t w[5];
+    constexpr int NDW = sdig_blk_dwords(kIQ4_NL);
+    uint32_t w[NDW];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) w[i] = p[i];
+    for (int i = 0; i < NDW; ++i) w[i] = p[i];
     uint32_t a0 = (uint32_t)X.init[0][0], a1 = (uint32_t)X.init[1][0];
     int a2 = 0;
 #pragma unroll
@@ -1401,13 +1369,9 @@ __device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t 
     return d * __builtin_ldexpf(v + X.poison, X.e - 22);
 }
 
-constexpr int kSdigMaxRows = 64; // rows per chunk of the persistent streamed kernel
-
 // Staged digits of one segment in LDS: per lane 24 digit-plane dwords, 12
 // accumulator starts, the exponent and the poison value (10 quads, quad-major
 // so that a wave's 16-byte reads and writes are conflict-free).
-constexpr int kDigQuads = 10;
-constexpr int sdig_share_cap(int nw) { return nw == 12 ? 6 : nw == 8 ? 2 : 0; }
 
 __device__ __forceinline__ void sxd_store(const SXD &X, uint32_t (*d)[64][4], int lane)
 {
@@ -1449,7 +1413,7 @@ template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
 __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
                                                        const float *x, float *y, int outer, int nblk,
                                                        int rpc, ArgPart *__restrict__ parts,
-                                                       const float *resid)
+                                                       const float *resid, int epi)
 {
     using F = SFmt<FMT>;
     // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
@@ -1457,8 +1421,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     // copies in flight is a compile-time count and the explicit s_waitcnt vmcnt
     // waits below are exact (x and the copies are inline assembly the compiler
     // does not wait on by itself)
-    constexpr int IPR = (F::SEG_BYTES / 16 + 63) / 64; // copy instructions per row
-    constexpr int SLOT = IPR * 1024;
+    constexpr int IPR = sdig_ipr(FMT); // copy instructions per row
+    constexpr int SLOT = sdig_slot(FMT);
+    static_assert(sdig_seg_bytes(FMT) == F::SEG_BYTES && sdig_seg_blocks(FMT) == F::SEG_BLOCKS,
+                  "segment geometry");
     static_assert(SLOT >= F::SEG_BYTES + 16, "Q8_0 / IQ4_NL read one dword past a segment");
     // segments whose digits can be staged in LDS (none for the lm_head: its 32 KB
     // workgroups run four to a CU, which the staging area would halve)
@@ -1471,47 +1437,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int bb = block_bytes(FMT);
-    const size_t row_bytes = (size_t)nblk * bb;
-    const int nseg = (nblk + F::SEG_BLOCKS - 1) / F::SEG_BLOCKS; // <= NW (host-checked)
-    const int wps = NW / nseg;                                   // waves per segment
-    const int sg = w % nseg, rl = w / nseg;
-    const bool worker = rl < wps; // waves past nseg * wps only join the barriers
-    // several waves per segment: the first loads x and forms the digits, the
-    // others take them from LDS (x crosses L2 -> CU once per segment, not per wave)
-    const bool share = SHC > 0 && nseg <= SHC && wps >= 2; // workgroup-uniform
-    const bool producer = !share || rl == 0;
-    const int nchunks = (outer + rpc - 1) / rpc;
-    const int seg_blocks = min(F::SEG_BLOCKS, nblk - sg * F::SEG_BLOCKS);
-    const int chunks16 = seg_blocks * bb / 16; // whole 8-block groups: host-checked
-    const uint32_t my_ring = (uint32_t)(w * D * SLOT);
-    const uint8_t *seg0 = W + (size_t)sg * F::SEG_BYTES;
+    const int bid = (int)blockIdx.x, grid = (int)gridDim.x;
+    const SdigWave g = sdig_wave(FMT, NW, D, SHC, outer, nblk, rpc, bid, grid, w);
+    const int nseg = g.nseg, sg = g.sg;
+    const bool share = g.share, producer = g.producer;
+    const int seg_blocks = g.seg_blocks, nitems = g.nitems;
 
-    // this wave's rows: items k = 0, 1, ... over its chunks; m rows per full chunk
-    const int m = worker ? (rpc - rl + wps - 1) / wps : 0;
-    const int my_chunks = blockIdx.x < nchunks ? (nchunks - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    int nitems = my_chunks * m;
-    if (worker && my_chunks > 0 && blockIdx.x + (my_chunks - 1) * gridDim.x == nchunks - 1) {
-        const int last = outer - (nchunks - 1) * rpc; // rows of the last chunk
-        nitems = (my_chunks - 1) * m + max(0, (last - rl + wps - 1) / wps);
-    }
-    const int mm = max(m, 1);
-    auto item_row = [&](int k) { // global row of item k (clamped: always a row of W)
-        const int ci = k / mm, rr = k - ci * mm;
-        // int operands throughout: with an unsigned blockIdx.x the call resolves to
-        // the double overload of min and the row is formed in f64 VALU code
-        return min(((int)blockIdx.x + ci * (int)gridDim.x) * rpc + rl + rr * wps, outer - 1);
-    };
-    // item k's row segment into slot k % D (k past the wave's items: its last
-    // item's row again, into a slot no remaining item uses)
+    // item k's row segment into slot k % D
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
     auto issue = [&](int k) {
-        const int kk = max(0, min(k, nitems - 1));
-        const uint8_t *src = seg0 + (size_t)item_row(kk) * row_bytes;
-        const uint32_t dst = ring_lds + my_ring + (uint32_t)((k % D) * SLOT);
+        const uint8_t *src = W + sdig_copy_row(g, FMT, k, bid, grid, rpc, outer);
 #pragma unroll
         for (int i = 0; i < IPR; ++i)
-            lds_copy16(src + 16 * (size_t)min(64 * i + lane, chunks16 - 1), dst + 1024 * i);
+            lds_copy16(src + sdig_copy_lane(g, i, lane), ring_lds + sdig_copy_dst(g, FMT, D, k, i));
     };
 
     // x first, then the first D rows' copies, all in flight together; the
@@ -1544,11 +1482,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     unsigned long long key = 0;
     uint32_t fl = 0;
     int k = 0;
-    for (int ci = 0; ci < my_chunks; ++ci) {
-        const int chunk = blockIdx.x + ci * gridDim.x;
-        const int row0 = chunk * rpc;
-        const int nrows = min(rpc, outer - row0);
-        const int mine = worker ? max(0, min(m, (nrows - rl + wps - 1) / wps)) : 0;
+    for (int ci = 0; ci < g.my_chunks; ++ci) {
+        const SdigChunk c = sdig_chunk(g, ci, bid, grid, rpc, outer);
+        const int row0 = c.row0, nrows = c.nrows, mine = c.mine;
         // the lane's share of the dot product of the row in ring slot `slot`
         auto dot_at = [&](uint32_t slot) {
             float v = 0.0f;
@@ -1557,31 +1493,29 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
                     v = q6_dot_dig(ring + slot, q6l, X);
             } else if constexpr (FMT == kIQ4_NL) {
                 if (lane < seg_blocks)
-                    v = iq4nl_dot_dig(ring + slot, 18u * lane, X);
+                    v = iq4nl_dot_dig(ring + slot, sdig_blk_off(FMT, lane), X);
             } else {
                 if (lane < seg_blocks)
-                    v = q80_dot_dig(ring + slot, 34u * lane, X);
+                    v = q80_dot_dig(ring + slot, sdig_blk_off(FMT, lane), X);
             }
             return v;
         };
         auto finish = [&](int rr, float v) {
             if (nseg == 1) { // the wave holds the whole row: finish it here
-                const int row = row0 + rl + rr * wps;
+                const int row = row0 + sdig_chunk_row(g, rr);
                 if constexpr (RESID)
-                    v += resid[row]; // wave-uniform: a scalar load
+                    v = epi_apply(resid[row], v, epi); // wave-uniform: a scalar load
                 if (y && lane == 0)
                     y[row] = v;
                 if constexpr (ARGMAX)
                     argmax_fold(v, (uint32_t)row, key, fl); // every lane folds the same row
             } else if (lane == 0) {
-                part[rl + rr * wps][sg] = v;
+                part[sdig_chunk_row(g, rr)][sg] = v;
             }
         };
         for (int rr = 0; rr < mine; ++rr, ++k) {
-            // items issued after item k: k + 1 .. max(D, nitems) - 1, at most D - 1
-            // of them; younger epilogue loads and stores only lengthen the wait
-            wait_vmcnt(IPR * min(D - 1, max(D, nitems) - 1 - k));
-            finish(rr, wave_sum(dot_at(my_ring + (uint32_t)((k % D) * SLOT))));
+            wait_vmcnt(IPR * sdig_wait_items(g, D, k));
+            finish(rr, wave_sum(dot_at(sdig_copy_dst(g, FMT, D, k, 0))));
             if (k + D < nitems)
                 issue(k + D); // slot k % D has been read
         }
@@ -1594,7 +1528,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
             for (int q = 0; q < nseg; ++q)
                 v += part[i][q];
             if constexpr (RESID)
-                v += resid[row0 + i]; // resid may be y
+                v = epi_apply(resid[row0 + i], v, epi); // resid may be y
             if (y)
                 y[row0 + i] = v;
             if constexpr (ARGMAX)
@@ -1667,7 +1601,7 @@ void set_tuning(const char *name, int value)
 template <int FMT, bool GATEUP>
 static hipError_t launch_kwide(const void *w, const void *w2, const float *x, float *y,
                                int inner, int outer, hipStream_t s, const float *nw = nullptr,
-                               float eps = 0.0f, const float *resid = nullptr)
+                               float eps = 0.0f, const float *resid = nullptr, int epi = kEpiAdd)
 {
     const int nblk = inner / 256;
     int R = GATEUP ? g_rows_gateup : g_rows_wide;
@@ -1681,7 +1615,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
 #define IHIP_KW(RR, DG, EX, NV)                                                              \
     hipLaunchKernelGGL((k_gemv_kwide<FMT, RR, GATEUP, DG, EX, NV>),                          \
                        dim3((outer + NV * RR - 1) / (NV * RR)), dim3(NV * 64), 0, s,          \
-                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid)
+                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid, epi)
 #define IHIP_KW_R(DG, EX)                                                                    \
     do {                                                                                     \
         if (nwv == 8) {                                                                      \
@@ -1702,7 +1636,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
         const int grid = max(1, min(ncu * g_pers_wg_per_cu, (outer + nwv - 1) / nwv));
 #define IHIP_KP(RR, EX, NV, NBB)                                                             \
     hipLaunchKernelGGL((k_gemv_kpers<FMT, RR, GATEUP, EX, NV, NBB>), dim3(grid), dim3(NV * 64), 0, s, \
-                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid)
+                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid, epi)
 #define IHIP_KP_R(EX)                                                                        \
     do {                                                                                     \
         if (nwv == 8) {                                                                      \
@@ -1758,122 +1692,93 @@ static int stream_grid(int outer, int rpc)
     return max(1, min(nchunks, g_stream_wg_per_cu * ncu));
 }
 
-// Whether NW waves with D ring slots fit the 160 KB of LDS (slot: whole 1 KB copies).
-template <int FMT>
-constexpr bool sdig_fits(int nw, int d)
+static SdigKnobs sdig_knobs()
 {
-    return nw * d * ((SFmt<FMT>::SEG_BYTES / 16 + 63) / 64) * 1024 + sdig_share_cap(nw) * kDigQuads * 1024 +
-               kSdigMaxRows * 8 * 4 + 2048 <= 160 * 1024;
+    SdigKnobs k;
+    k.rows = g_sdig_rows;
+    k.depth = g_sdig_depth;
+    k.wg_per_cu = g_sdig_wg_per_cu;
+    k.waves = g_sdig_waves;
+    return k;
 }
 
-// The persistent digit kernel: nseg <= 8 segments of 2048 columns; waves per
-// workgroup a multiple of nseg where possible (knob: 12 or 16 waves).
-static int sdig_waves(int nseg)
+static int device_cus()
 {
-    if ((g_sdig_waves == 6 || g_sdig_waves == 8 || g_sdig_waves == 12 || g_sdig_waves == 16) &&
-        g_sdig_waves >= nseg)
-        return g_sdig_waves;
-    // measured on MI355X (4096 x 12288 Q6_K: 12 waves 12.8 us, 6 waves 14.3 us;
-    // 4096 x 4096, two segments, 12 against 8 waves: Q8_0 5.98 / 6.26 us, Q6_K
-    // 6.04 / 6.45 us, IQ4_NL 5.79 / 5.99 us)
-    return (nseg == 2 || nseg == 3 || nseg == 6) ? 12 : 8;
-}
-
-template <int FMT, bool ARGMAX, int NWV, int DD>
-static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer, int rpc,
-                           int grid, void *parts, hipStream_t s, const float *resid)
-{
-    if (resid)
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, true>), dim3(grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
-    else
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, false>), dim3(grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);
-}
-
-
-// Rows per chunk (measured on MI355X: 151936 x 2048 Q6_K lm_head, 4096 x 4096
-// Q8_0, 4096 x 12288 Q6_K): rows of one segment finish inside their wave and
-// take long chunks; rows of several segments meet in LDS once per chunk and
-// take short ones, which spread a small matrix over more workgroups.
-static int sdig_rows(int nseg)
-{
-    const int r = g_sdig_rows > 0 ? g_sdig_rows : nseg == 1 ? 32 : nseg == 2 ? 16
-                                                : (nseg == 3 || nseg == 6) ? 16 : 4;
-    return min(r, kSdigMaxRows);
-}
-
-static bool sdig_usable(int fmt, int nblk)
-{
-    const int seg = SFmtSegBlocks(fmt);
-    const int nseg = (nblk + seg - 1) / seg;
-    return g_sdig_off <= 0 && nseg >= 1 && nseg <= 8;
-}
-
-static int sdig_grid(int outer, int nseg)
-{
-    const int nchunks = (outer + sdig_rows(nseg) - 1) / sdig_rows(nseg);
     int dev = 0, ncu = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    // one-segment rows (the 2048-wide lm_head): 3 workgroups per CU measured
-    // 54-55 us against 57 us with 4 (151936 rows, 32 per chunk, interleaved)
-    const int per_cu = g_sdig_wg_per_cu > 0 ? g_sdig_wg_per_cu : nseg == 1 ? 3 : 4;
-    return max(1, min(nchunks, ncu * per_cu));
+    return ncu;
 }
 
+static bool sdig_usable(int fmt, int nblk) { return g_sdig_off <= 0 && sdig_rows_ok(fmt, nblk); }
+
+template <int FMT, bool ARGMAX, int NWV, int DD>
+static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer,
+                           const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
+{
+    if (resid)
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, true>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+    else
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, false>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+}
+
+// The instantiation sdig_plan chose (ring depths that do not fit the LDS are
+// never instantiated; the plan never picks them).
 template <int FMT, bool ARGMAX>
 static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner, int outer,
-                              void *parts, hipStream_t s, const float *resid)
+                              void *parts, hipStream_t s, const float *resid, int epi)
 {
     const int nblk = inner / block_elems(FMT);
-    const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
-    const int rpc = sdig_rows(nseg), grid = sdig_grid(outer, nseg);
-    // ring depth (4 x 8 waves x 3 KB Q8_0 slots is 96 KB; 6 only where it fits)
-    const int dd = g_sdig_depth >= 6 ? 6 : g_sdig_depth >= 4 ? 4 : 2;
-    const int nwv = sdig_waves(nseg);
-    if (nwv == 12) {
-        if (dd == 6 && sdig_fits<FMT>(12, 6)) launch_sdig_nd<FMT, ARGMAX, 12, sdig_fits<FMT>(12, 6) ? 6 : 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-        else if (dd == 4) launch_sdig_nd<FMT, ARGMAX, 12, sdig_fits<FMT>(12, 4) ? 4 : 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-        else launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-    } else if (nwv == 16) {
-        launch_sdig_nd<FMT, ARGMAX, 16, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-    } else if (nwv == 6) {
-        if (dd == 2) launch_sdig_nd<FMT, ARGMAX, 6, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-        else launch_sdig_nd<FMT, ARGMAX, 6, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-    } else {
-        if (dd == 2) launch_sdig_nd<FMT, ARGMAX, 8, 2>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
-        else launch_sdig_nd<FMT, ARGMAX, 8, 4>(w, x, y, nblk, outer, rpc, grid, parts, s, resid);
+    const SdigPlan p = sdig_plan(FMT, nblk, outer, ARGMAX, sdig_knobs(), device_cus());
+    switch (p.nw * 16 + p.d) {
+    case 12 * 16 + 6:
+        if constexpr (sdig_fits(FMT, 12, 6))
+            launch_sdig_nd<FMT, ARGMAX, 12, 6>(w, x, y, nblk, outer, p, parts, s, resid, epi);
+        break;
+    case 12 * 16 + 4:
+        if constexpr (sdig_fits(FMT, 12, 4))
+            launch_sdig_nd<FMT, ARGMAX, 12, 4>(w, x, y, nblk, outer, p, parts, s, resid, epi);
+        break;
+    case 12 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 16 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 16, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 6 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 6, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 6 * 16 + 4: launch_sdig_nd<FMT, ARGMAX, 6, 4>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 8 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 8, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 8 * 16 + 4: launch_sdig_nd<FMT, ARGMAX, 8, 4>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 template <int FMT, bool ARGMAX>
 static hipError_t launch_stream(const void *w, const float *x, float *y, int inner, int outer,
-                                void *parts, hipStream_t s, const float *resid = nullptr)
+                                void *parts, hipStream_t s, const float *resid = nullptr,
+                                int epi = kEpiAdd)
 {
     if (sdig_usable(FMT, inner / block_elems(FMT)))
-        return launch_sdig<FMT, ARGMAX>(w, x, y, inner, outer, parts, s, resid);
+        return launch_sdig<FMT, ARGMAX>(w, x, y, inner, outer, parts, s, resid, epi);
     const int nblk = inner / block_elems(FMT);
     const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
     const int nw = stream_waves(nseg);
     const int rpc = stream_rows(outer, ARGMAX);
     const int grid = stream_grid(outer, rpc);
-#define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid);         return hipGetLastError();                                                                }
+#define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid, epi);         return hipGetLastError();                                                                }
     IHIP_ST(1, 2) IHIP_ST(2, 2) IHIP_ST(3, 2) IHIP_ST(4, 2) IHIP_ST(6, 2) IHIP_ST(8, 2)
 #undef IHIP_ST
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
-                       hipStream_t s, const float *resid)
+                       hipStream_t s, const float *resid, int epi)
 {
     switch (type) {
-    case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid);
-    case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid);
-    case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid);
-    case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid);
-    case kIQ4_NL: return launch_stream<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid);
+    case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
+    case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
+    case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kIQ4_NL: return launch_stream<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     default: return hipErrorInvalidValue;
     }
 }
@@ -1931,9 +1836,10 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
     }
     if (e != hipSuccess)
         return e;
-    const int nblk = hidden / block_elems(type), seg = SFmtSegBlocks(type);
-    const int nparts = sdig_usable(type, nblk) ? sdig_grid(vocab, (nblk + seg - 1) / seg)
-                                               : stream_grid(vocab, stream_rows(vocab, true));
+    const int nblk = hidden / block_elems(type);
+    const int nparts = sdig_usable(type, nblk)
+                           ? sdig_plan(type, nblk, vocab, true, sdig_knobs(), device_cus()).grid
+                           : stream_grid(vocab, stream_rows(vocab, true));
     launch_argmax_finalize(ws, nparts, token, flags, s);
     return hipGetLastError();
 }

@@ -7,9 +7,10 @@
 namespace ihip {
 
 // kq_gemv.hip
-// resid != nullptr: y = resid + W x (resid may be y).
+// resid != nullptr: y = epi_apply(resid, W x, epi) per row (kq_common.h: the
+// residual add, or the SwiGLU of an unfused gate/up pair); resid may be y.
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
-                       hipStream_t s, const float *resid = nullptr);
+                       hipStream_t s, const float *resid = nullptr, int epi = 0);
 bool gate_up_fusable(int gate_type, int up_type);
 // norm_w != nullptr: the input is rmsnorm(x) .* norm_w (eps inside the root).
 hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,
@@ -26,7 +27,7 @@ void set_tuning(const char *name, int value);
 
 // kq_dequant.hip
 hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y, int inner,
-                               int outer, hipStream_t s, const float *resid = nullptr);
+                               int outer, hipStream_t s, const float *resid = nullptr, int epi = 0);
 // rmsnorm_cpu! (src/ModelCPU.jl:111-123): out = x * (1/sqrt(mean(x^2) + eps)) .* w
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, float *out, int n,
                           hipStream_t s);

@@ -1,0 +1,279 @@
+// kq_sdig_plan.h -- launch plan and index arithmetic of the streamed digit
+// GEMV (k_gemv_sdig, kq_gemv.hip): Q6_K / Q8_0 / IQ4_NL rows, the lm_head with
+// the fused argmax, the FFN down projection.
+//
+// The kernel forms every global address, LDS offset, wait count and row index
+// through these functions, and the host-side bounds check
+// (tests/native/sdig_check.hip) enumerates the same functions over every
+// workgroup, wave, item and lane of a launch, so the check runs the very
+// arithmetic the kernel runs.
+//
+// Geometry.  K is cut into segments of 2048 columns (8 Q6_K blocks of 210 B,
+// 64 Q8_0 blocks of 34 B, 64 IQ4_NL blocks of 18 B: 16-byte multiples).  A
+// workgroup of NW waves walks chunks of `rpc` rows grid-stride.  Wave w owns
+// segment w % nseg and, when there are more waves than segments, every
+// (NW / nseg)-th row of a chunk; its rows of all its chunks are numbered
+// items k = 0, 1, ... and stream through a private D-slot LDS ring (slot
+// k % D) by direct-to-LDS copies of 64 lanes x 16 bytes.
+#pragma once
+
+#include "kq_common.h"
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ihip {
+
+constexpr int kSdigMaxRows = 64;    // rows per chunk (part[] in LDS holds one chunk)
+constexpr int kArgMaxParts = 16384; // argmax partials: IHIP_ARGMAX_WS_BYTES / 16
+constexpr int kDigQuads = 10;       // staged digits per lane: 10 x 16 bytes
+
+__host__ __device__ constexpr int sd_min(int a, int b) { return a < b ? a : b; }
+__host__ __device__ constexpr int sd_max(int a, int b) { return a > b ? a : b; }
+
+// blocks and bytes per 2048-column segment
+__host__ __device__ constexpr int sdig_seg_blocks(int fmt) { return fmt == kQ6_K ? 8 : 64; }
+__host__ __device__ constexpr int sdig_seg_bytes(int fmt)
+{
+    return sdig_seg_blocks(fmt) * block_bytes(fmt);
+}
+// copy instructions per row segment (each moves 1 KB) and the ring slot size
+__host__ __device__ constexpr int sdig_ipr(int fmt) { return (sdig_seg_bytes(fmt) / 16 + 63) / 64; }
+__host__ __device__ constexpr int sdig_slot(int fmt) { return sdig_ipr(fmt) * 1024; }
+// segments whose digits can be staged in LDS for the segment's other waves
+__host__ __device__ constexpr int sdig_share_cap(int nw) { return nw == 12 ? 6 : nw == 8 ? 2 : 0; }
+
+// Whether NW waves with D ring slots fit the 160 KB of LDS: the ring, the
+// staged digits, the chunk partial sums and 2 KB for the rest.
+__host__ __device__ constexpr bool sdig_fits(int fmt, int nw, int d)
+{
+    return nw * d * sdig_slot(fmt) + sdig_share_cap(nw) * kDigQuads * 1024 + kSdigMaxRows * 8 * 4 +
+               2048 <= 160 * 1024;
+}
+
+// One wave's share of a launch.
+struct SdigWave {
+    int nseg;        // segments per row (<= NW, host-checked)
+    int wps;         // waves per segment
+    int sg, rl;      // this wave's segment and its rank among the segment's waves
+    bool worker;     // waves past nseg * wps only join the barriers
+    bool share;      // the segment's digits are staged in LDS (workgroup-uniform)
+    bool producer;   // this wave loads x and forms the digits
+    int nchunks;     // chunks of the whole matrix
+    int seg_blocks;  // blocks of this wave's segment
+    int chunks16;    // 16-byte units of the segment (whole 8-block groups: host-checked)
+    uint32_t my_ring;// LDS byte offset of this wave's ring within the ring array
+    int m;           // rows per full chunk
+    int my_chunks;   // chunks of this workgroup
+    int nitems;      // rows (items) of this wave over all its chunks
+    int mm;          // max(m, 1)
+    size_t row_bytes;
+};
+
+__host__ __device__ inline SdigWave sdig_wave(int fmt, int NW, int D, int SHC, int outer, int nblk,
+                                              int rpc, int bid, int grid, int w)
+{
+    SdigWave g;
+    const int sb = sdig_seg_blocks(fmt), bb = block_bytes(fmt);
+    g.row_bytes = (size_t)nblk * bb;
+    g.nseg = (nblk + sb - 1) / sb;
+    g.wps = NW / g.nseg;
+    g.sg = w % g.nseg;
+    g.rl = w / g.nseg;
+    g.worker = g.rl < g.wps;
+    g.share = SHC > 0 && g.nseg <= SHC && g.wps >= 2;
+    g.producer = !g.share || g.rl == 0;
+    g.nchunks = (outer + rpc - 1) / rpc;
+    g.seg_blocks = sd_min(sb, nblk - g.sg * sb);
+    g.chunks16 = g.seg_blocks * bb / 16;
+    g.my_ring = (uint32_t)(w * D * sdig_slot(fmt));
+    g.m = g.worker ? (rpc - g.rl + g.wps - 1) / g.wps : 0;
+    g.my_chunks = bid < g.nchunks ? (g.nchunks - 1 - bid) / grid + 1 : 0;
+    g.nitems = g.my_chunks * g.m;
+    if (g.worker && g.my_chunks > 0 && bid + (g.my_chunks - 1) * grid == g.nchunks - 1) {
+        const int last = outer - (g.nchunks - 1) * rpc; // rows of the last chunk
+        g.nitems = (g.my_chunks - 1) * g.m + sd_max(0, (last - g.rl + g.wps - 1) / g.wps);
+    }
+    g.mm = sd_max(g.m, 1);
+    return g;
+}
+
+// Global row of item k (clamped: always a row of W).  int operands throughout
+// (an unsigned operand would send min to its double overload in device code).
+__host__ __device__ inline int sdig_item_row(const SdigWave &g, int k, int bid, int grid, int rpc,
+                                             int outer)
+{
+    const int ci = k / g.mm, rr = k - ci * g.mm;
+    return sd_min((bid + ci * grid) * rpc + g.rl + rr * g.wps, outer - 1);
+}
+
+// Byte offset in W of the row segment copied for item k: items past the
+// wave's last re-copy its last item's row into a slot no remaining item uses.
+__host__ __device__ inline size_t sdig_copy_row(const SdigWave &g, int fmt, int k, int bid, int grid,
+                                                int rpc, int outer)
+{
+    const int kk = sd_max(0, sd_min(k, g.nitems - 1));
+    return (size_t)g.sg * sdig_seg_bytes(fmt) + (size_t)sdig_item_row(g, kk, bid, grid, rpc, outer) * g.row_bytes;
+}
+// Byte offset within the row segment of lane `lane`'s 16 bytes in copy i:
+// every copy runs with all 64 lanes on (lanes past the segment re-read its
+// last 16 bytes into the slot's tail), so the copies in flight are a
+// compile-time count.
+__host__ __device__ inline uint32_t sdig_copy_lane(const SdigWave &g, int i, int lane)
+{
+    return 16u * (uint32_t)sd_min(64 * i + lane, g.chunks16 - 1);
+}
+// LDS byte offset (within the ring array) where copy i of item k lands; lane
+// l's 16 bytes go to this + 16 l.
+__host__ __device__ inline uint32_t sdig_copy_dst(const SdigWave &g, int fmt, int D, int k, int i)
+{
+    return g.my_ring + (uint32_t)((k % D) * sdig_slot(fmt)) + 1024u * (uint32_t)i;
+}
+// Items whose copies may still be in flight when item k is read: those issued
+// after it (k + 1 .. max(D, nitems) - 1, at most D - 1).  The wait is
+// vmcnt(ipr x this); younger loads and stores only lengthen it.
+__host__ __device__ inline int sdig_wait_items(const SdigWave &g, int D, int k)
+{
+    return sd_min(D - 1, sd_max(D, g.nitems) - 1 - k);
+}
+
+// A producer lane's x slice: float offset of its first element within the
+// segment, and whether the lane covers a block of the segment (an inactive
+// lane loads the segment's first values and zeroes them).
+//   Q6_K: block bs = lane >> 3, half n = (lane >> 2) & 1, positions
+//         l0 = 8 (lane & 3) .. +7, groups g at +32 g (elements 128n + 32g + l0 + i);
+//   Q8_0 / IQ4_NL: block lane, 32 consecutive values.
+__host__ __device__ inline int sdig_x_lane(int fmt, int lane, int seg_blocks, bool &active)
+{
+    if (fmt == kQ6_K) {
+        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+        active = bs < seg_blocks;
+        return active ? 256 * bs + 128 * n + l0 : 0;
+    }
+    active = lane < seg_blocks;
+    return active ? 32 * lane : 0;
+}
+// Byte offset of the lane's load t (0..7, 16 bytes each) from its first element.
+__host__ __device__ constexpr int sdig_x_load_byte(int fmt, int t)
+{
+    return fmt == kQ6_K ? 128 * (t >> 1) + 16 * (t & 1) : 16 * t;
+}
+
+// ---- lane geometry of the ring reads --------------------------------------
+// A lane's place in a Q6_K segment: the dword-aligned LDS offsets (within a
+// ring slot) of its ql, qh and scale bytes and of d, and the byte phase they
+// share (210-byte blocks leave odd blocks 2 bytes past a dword boundary).
+// The dot reads 3 dwords at a, at a + 32, at h and at s, and 2 bytes at d.
+// Computed once, so a row costs one address add per array.
+struct Q6DigLane {
+    uint32_t a, h, s, d, sh;
+    int c; // which 16 of the lane's 32 elements' scale: l0 >> 4
+};
+
+__host__ __device__ inline Q6DigLane q6_dig_lane(int lane)
+{
+    const uint32_t bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+    const uint32_t bo = 210u * bs;
+    Q6DigLane L;
+    L.a = (bo + 64 * n + l0) & ~3u;
+    L.h = (bo + 128 + 32 * n + l0) & ~3u;
+    L.s = (bo + 192 + 8 * n) & ~3u;
+    L.d = bo + 208;
+    L.sh = bo & 3u;
+    L.c = (int)(l0 >> 4);
+    return L;
+}
+
+// Q8_0 / IQ4_NL: lane = block of the segment.  The dot reads d (2 bytes at the
+// block's offset) and sdig_blk_dwords dwords from the dword below offset + 2.
+__host__ __device__ constexpr uint32_t sdig_blk_off(int fmt, int lane)
+{
+    return (uint32_t)block_bytes(fmt) * (uint32_t)lane;
+}
+__host__ __device__ constexpr int sdig_blk_dwords(int fmt) { return fmt == kQ8_0 ? 9 : 5; }
+
+// Chunk ci of a workgroup: first row, rows, and this wave's rows in it.
+struct SdigChunk {
+    int row0, nrows, mine;
+};
+__host__ __device__ inline SdigChunk sdig_chunk(const SdigWave &g, int ci, int bid, int grid, int rpc,
+                                                int outer)
+{
+    SdigChunk c;
+    c.row0 = (bid + ci * grid) * rpc;
+    c.nrows = sd_min(rpc, outer - c.row0);
+    c.mine = g.worker ? sd_max(0, sd_min(g.m, (c.nrows - g.rl + g.wps - 1) / g.wps)) : 0;
+    return c;
+}
+// Row (within the chunk) of the wave's rr-th row of a chunk.
+__host__ __device__ inline int sdig_chunk_row(const SdigWave &g, int rr) { return g.rl + rr * g.wps; }
+
+// ---- host: the launch plan ------------------------------------------------
+// Process-wide knobs (0 = the measured default).
+struct SdigKnobs {
+    int rows = 0;      // rows per chunk (1..64)
+    int depth = 0;     // ring slots per wave (2, 4 or 6)
+    int wg_per_cu = 0; // workgroups per CU
+    int waves = 0;     // waves per workgroup (6, 8, 12, 16)
+};
+
+struct SdigPlan {
+    int nseg, nw, d, rpc, grid;
+};
+
+// Rows per chunk (measured on MI355X: 151936 x 2048 Q6_K lm_head, 4096 x 4096
+// Q8_0, 4096 x 12288 Q6_K): rows of one segment finish inside their wave and
+// take long chunks; rows of several segments meet in LDS once per chunk and
+// take short ones, which spread a small matrix over more workgroups.
+inline int sdig_rows(int nseg, const SdigKnobs &kn)
+{
+    const int r = kn.rows > 0 ? kn.rows : nseg == 1 ? 32 : nseg == 2 ? 16 : (nseg == 3 || nseg == 6) ? 16 : 4;
+    return sd_min(r, kSdigMaxRows);
+}
+
+// Waves per workgroup: a multiple of nseg where possible (measured on MI355X:
+// 4096 x 12288 Q6_K 12 waves 12.8 us, 6 waves 14.3 us; 4096 x 4096, two
+// segments, 12 against 8 waves: Q8_0 5.98 / 6.26 us, Q6_K 6.04 / 6.45 us,
+// IQ4_NL 5.79 / 5.99 us).
+inline int sdig_waves(int nseg, const SdigKnobs &kn)
+{
+    if ((kn.waves == 6 || kn.waves == 8 || kn.waves == 12 || kn.waves == 16) && kn.waves >= nseg)
+        return kn.waves;
+    return (nseg == 2 || nseg == 3 || nseg == 6) ? 12 : 8;
+}
+
+// Whether the streamed kernel takes rows of nblk blocks: 1..8 segments.
+inline bool sdig_rows_ok(int fmt, int nblk)
+{
+    const int nseg = (nblk + sdig_seg_blocks(fmt) - 1) / sdig_seg_blocks(fmt);
+    return nblk > 0 && nseg >= 1 && nseg <= 8;
+}
+
+// The launch: waves, ring depth, rows per chunk and grid.  With the fused
+// argmax every workgroup leaves one partial, so the grid stays within
+// kArgMaxParts whatever the knobs or the device's CU count.
+inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, const SdigKnobs &kn, int ncu)
+{
+    SdigPlan p;
+    p.nseg = (nblk + sdig_seg_blocks(fmt) - 1) / sdig_seg_blocks(fmt);
+    p.rpc = sdig_rows(p.nseg, kn);
+    const int nchunks = (outer + p.rpc - 1) / p.rpc;
+    // one-segment rows (the 2048-wide lm_head): 3 workgroups per CU measured
+    // 54-55 us against 57 us with 4 (151936 rows, 32 per chunk, interleaved)
+    const int per_cu = kn.wg_per_cu > 0 ? kn.wg_per_cu : p.nseg == 1 ? 3 : 4;
+    int grid = sd_max(1, sd_min(nchunks, sd_max(1, ncu) * sd_min(per_cu, 64)));
+    if (argmax)
+        grid = sd_min(grid, kArgMaxParts);
+    p.grid = grid;
+    p.nw = sdig_waves(p.nseg, kn);
+    const int dd = kn.depth >= 6 ? 6 : kn.depth >= 4 ? 4 : 2;
+    if (p.nw == 12)
+        p.d = (dd == 6 && sdig_fits(fmt, 12, 6)) ? 6 : (dd == 4 && sdig_fits(fmt, 12, 4)) ? 4 : 2;
+    else if (p.nw == 16)
+        p.d = 2;
+    else
+        p.d = dd == 2 ? 2 : 4;
+    return p;
+}
+
+} // namespace ihip

@@ -61,6 +61,7 @@ SIGNATURES = {
     "ihip_weight_release": ([_u64], _i),
     "ihip_weight_forget": ([_vp], _i),
     "ihip_weight_device_ptr": ([_u64, C.POINTER(_vp)], _i),
+    "ihip_weight_fingerprint": ([_vp, _sz, C.POINTER(_u64)], _i),
     "ihip_q4_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q5_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q6_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
@@ -95,6 +96,8 @@ SIGNATURES = {
     "ihip_gate_up_swiglu_dev": ([_i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_ffn_swiglu_dev": ([_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_lm_head_argmax_dev": ([_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp], _i),
+    "ihip_lm_head_fused": ([_i, _vp, _vp, _i, _i], _i),
+    "ihip_ffn_block_scratch_floats": ([_i, _i, _i, _i], _sz),
     "ihip_argmax_dev": ([_vp, _i64, _vp, _vp, _vp, _vp], _i),
     "ihip_fused_mlp_gate_mul_dev": ([_vp, _vp, _i64, _vp], _i),
     "ihip_fused_silu_gate_mul_dev": ([_vp, _vp, _vp, _i64, _vp], _i),

@@ -37,6 +37,10 @@ FLAGS = [
 ]
 
 
+CHECKS = PKG.parent / "tests" / "native"
+CHECK_LIB = CHECKS / "_build" / "libsdig_check.so"
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
@@ -54,6 +58,35 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({r.returncode})")
     os.replace(tmp, LIB)
     return LIB
+
+
+FLOORS_LIB = LIBDIR / "libinferno_floors.so"
+
+
+def _hipcc(out: Path, srcs, verbose: bool) -> Path:
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(tmp), *[str(s) for s in srcs]]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"hipcc failed ({r.returncode})")
+    os.replace(tmp, out)
+    return out
+
+
+def build_floors(verbose: bool = False) -> Path:
+    """The benchmark's measurement kernels (empty launch, coalesced read):
+    inferno.jl_amd/lib/libinferno_floors.so, loaded by bench.py only."""
+    return _hipcc(FLOORS_LIB, [PKG / "floors" / "floors.hip"], verbose)
+
+
+def build_checks(verbose: bool = False) -> Path:
+    """Host-side checkers of the kernels' index arithmetic (tests/native): they
+    include the headers the kernels form their indices with and run on the CPU."""
+    return _hipcc(CHECK_LIB, [CHECKS / "sdig_check.hip"], verbose)
 
 
 if __name__ == "__main__":

@@ -117,6 +117,11 @@ def ffn_swiglu(wg: DeviceWeight, wu: DeviceWeight, wd: DeviceWeight, x, h=None, 
 
 
 def lm_head_argmax(w: DeviceWeight, x, ws: ArgmaxWorkspace, logits=None, stream=None):
+    """logits may be None; where the argmax is not fused into the GEMV (other
+    types or shapes) a logits buffer is allocated for the call."""
+    if logits is None and not lib().ihip_lm_head_fused(w.ggml_type, _ptr(w.data), _ptr(x, torch.float32, "x"),
+                                                       w.inner, w.outer):
+        logits = torch.empty(w.outer, dtype=torch.float32, device=x.device)
     lp = _ptr(logits, torch.float32, "logits") if logits is not None else None
     check(lib().ihip_lm_head_argmax_dev(w.ggml_type, _ptr(w.data), _ptr(x, torch.float32, "x"), lp,
                                         ws.token.data_ptr(), ws.flags.data_ptr(), w.inner, w.outer,
@@ -180,7 +185,8 @@ def ffn_block(wg: DeviceWeight, wu: DeviceWeight, wd: DeviceWeight, norm_w: torc
     """The MLP half of a decoder layer (src/ModelCPU.jl:913-920), in place on x:
     x += Wd (silu(Wg n) * (Wu n)), n = rmsnorm(x) .* norm_w."""
     if h is None:
-        h = torch.empty(wg.outer, dtype=torch.float32, device=x.device)
+        n = lib().ihip_ffn_block_scratch_floats(wg.ggml_type, wu.ggml_type, wg.inner, wg.outer)
+        h = torch.empty(n, dtype=torch.float32, device=x.device)
     check(lib().ihip_ffn_block_dev(wg.ggml_type, _ptr(wg.data), wu.ggml_type, _ptr(wu.data),
                                    wd.ggml_type, _ptr(wd.data), _ptr(norm_w, torch.float32, "norm_w"),
                                    eps, _ptr(x, torch.float32, "x"), _ptr(h, torch.float32, "h"),
@@ -195,6 +201,9 @@ def lm_head_argmax_norm(w: DeviceWeight, norm_w: torch.Tensor, eps: float, x: to
     token and flags land in ws.token / ws.flags (device)."""
     if xn is None:
         xn = torch.empty_like(x)
+    if logits is None and not lib().ihip_lm_head_fused(w.ggml_type, _ptr(w.data), _ptr(xn, torch.float32, "xn"),
+                                                       w.inner, w.outer):
+        logits = torch.empty(w.outer, dtype=torch.float32, device=x.device)
     check(lib().ihip_lm_head_argmax_norm_dev(
         w.ggml_type, _ptr(w.data), _ptr(norm_w, torch.float32, "norm_w"), eps,
         _ptr(x, torch.float32, "x"), _ptr(xn, torch.float32, "xn"),

@@ -53,6 +53,7 @@ def lib():
         L.orc_dequant.argtypes = [C.c_int, _u8p, _f32p, C.c_int64]
         L.orc_gemv_f64.argtypes = [C.c_int, _u8p, _f32p, _f64p, C.c_int, C.c_int]
         L.orc_row_norms.argtypes = [C.c_int, _u8p, _f64p, C.c_int, C.c_int]
+        L.orc_gemm_f64.argtypes = [C.c_int, _u8p, _f32p, _f64p, C.c_int, C.c_int, C.c_int]
         L.orc_gemv_f32_serial.argtypes = [C.c_int, _u8p, _f32p, _f32p, C.c_int, C.c_int]
         L.orc_argmax.argtypes = [_f32p, C.c_int64, C.POINTER(C.c_int64), C.POINTER(C.c_int)]
         L.orc_ffn_swiglu_f64.argtypes = [C.c_int, _u8p, C.c_int, _u8p, C.c_int, _u8p, _f32p,
@@ -65,7 +66,7 @@ def lib():
         L.orc_quantize_row_q8k.argtypes = [_f32p, _u8p, C.c_int64]
         L.orc_gemv_q8k.argtypes = [C.c_int, _u8p, _f32p, _f32p, _u8p, C.c_int, C.c_int]
         L.orc_gemv_q8_0_lanes.argtypes = [_u8p, _f32p, _f32p, C.c_int, C.c_int]
-        for name in ("orc_dequant", "orc_gemv_f64", "orc_row_norms", "orc_gemv_f32_serial",
+        for name in ("orc_dequant", "orc_gemv_f64", "orc_gemm_f64", "orc_row_norms", "orc_gemv_f32_serial",
                      "orc_argmax", "orc_ffn_swiglu_f64", "orc_rmsnorm_f64", "orc_ffn_block_f64",
                      "orc_quantize_row_q8k",
                      "orc_gemv_q8k", "orc_gemv_q8_0_lanes"):
@@ -114,6 +115,17 @@ def gemv_f64(ggml_type: int, w: np.ndarray, x: np.ndarray, inner: int, outer: in
     _chk(lib().orc_gemv_f64(ggml_type, w, np.ascontiguousarray(x, np.float32), out, inner, outer),
          "gemv_f64")
     return out
+
+
+def gemm_f64(ggml_type: int, w: np.ndarray, X: np.ndarray, inner: int,
+             outer: int) -> np.ndarray:
+    """T x outer fp64 outputs of the per-token loop (row t = gemv_f64 of X[t])."""
+    X = np.ascontiguousarray(X, np.float32)
+    T = X.shape[0]
+    Y = np.empty((T, outer), dtype=np.float64)
+    _chk(lib().orc_gemm_f64(ggml_type, w, X.reshape(-1), Y.reshape(-1), T, inner, outer),
+         "gemm_f64")
+    return Y
 
 
 def row_norms(ggml_type: int, w: np.ndarray, inner: int, outer: int) -> np.ndarray:

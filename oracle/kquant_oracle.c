@@ -290,6 +290,57 @@ int orc_gemv_f64(int type, const uint8_t *w, const float *x, double *out,
     return 0;
 }
 
+/* The per-token prefill loop, src/ModelCPU.jl:1001-1017: every token t is one
+ * GEMV of the same weight, Y[t][r] = sum_c W[r][c] * X[t][c].  Each output is
+ * summed in fp64 in column order, exactly as orc_gemv_f64 sums it, so row t of
+ * Y equals orc_gemv_f64 on X[t] bit for bit; rows of W are dequantized once
+ * per group of 8 and shared by all T tokens. */
+int orc_gemm_f64(int type, const uint8_t *w, const float *X, double *Y, int T,
+                 int inner, int outer)
+{
+    if (check_dims(type, inner, outer) || T < 0)
+        return -1;
+    const deq_fn f = deq_for(type);
+    const int be = orc_block_elems(type), bb = orc_block_bytes(type);
+    const int nb = inner / be;
+    enum { RG = 8 };
+    int bad = 0;
+#pragma omp parallel
+    {
+        double *wr = (double *)malloc(sizeof(double) * (size_t)RG * (size_t)inner);
+        if (!wr) {
+#pragma omp atomic write
+            bad = 1;
+        }
+#pragma omp for schedule(dynamic, 1)
+        for (int r0 = 0; r0 < outer; r0 += RG) {
+            if (!wr)
+                continue;
+            const int nr = outer - r0 < RG ? outer - r0 : RG;
+            float blk[256];
+            for (int i = 0; i < nr; ++i)
+                for (int b = 0; b < nb; ++b) {
+                    f(w + ((size_t)(r0 + i) * nb + b) * bb, blk);
+                    for (int e = 0; e < be; ++e)
+                        wr[(size_t)i * inner + (size_t)b * be + e] = (double)blk[e];
+                }
+            for (int t = 0; t < T; ++t) {
+                const float *xt = X + (size_t)t * inner;
+                double acc[RG] = {0};
+                for (int c = 0; c < inner; ++c) {
+                    const double xc = (double)xt[c];
+                    for (int i = 0; i < nr; ++i)
+                        acc[i] += wr[(size_t)i * inner + c] * xc;
+                }
+                for (int i = 0; i < nr; ++i)
+                    Y[(size_t)t * outer + r0 + i] = acc[i];
+            }
+        }
+        free(wr);
+    }
+    return bad ? -2 : 0;
+}
+
 int orc_row_norms(int type, const uint8_t *w, double *norms, int inner, int outer)
 {
     if (check_dims(type, inner, outer))

@@ -53,6 +53,10 @@ int orc_dequant(int type, const uint8_t *src, float *dst, int64_t n);
 /* fp64-accumulated GEMV over the exact fp32 dequantized weights. */
 int orc_gemv_f64(int type, const uint8_t *w, const float *x, double *out,
                  int inner, int outer);
+/* The per-token prefill loop (src/ModelCPU.jl:1001-1017) over T tokens:
+ * Y[t*outer + r] = orc_gemv_f64 of X[t*inner ...] at row r, bit for bit. */
+int orc_gemm_f64(int type, const uint8_t *w, const float *X, double *Y, int T,
+                 int inner, int outer);
 /* ||w_row||_2 of each dequantized row (fp64). */
 int orc_row_norms(int type, const uint8_t *w, double *norms, int inner, int outer);
 /* Julia fallback semantics: serial fp32 accumulation per row. */

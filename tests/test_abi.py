@@ -93,3 +93,77 @@ def test_no_device_is_an_error_not_a_fallback():
     o = np.zeros(1, np.float32)
     with pytest.raises(_lib.IHIPError):
         QK.q4_k_gemv_(o, np.zeros(144, np.uint8), np.zeros(256, np.float32), 256, 1)
+
+
+# ---- the host-pointer weight cache's staleness guard ----------------------
+
+def _fp(buf: np.ndarray) -> int:
+    import ctypes as C
+    from inferno_hip import _lib
+    out = C.c_uint64(0)
+    _lib.check(_lib.lib().ihip_weight_fingerprint(buf.ctypes.data, buf.nbytes, C.byref(out)))
+    return out.value
+
+
+def test_weight_fingerprint_sees_new_bytes_at_the_same_address():
+    """The cache reuses a device copy only while the buffer's sampled
+    fingerprint is unchanged: a rewrite in place, or other bytes at a reused
+    address, changes it; identical bytes elsewhere do not."""
+    from inferno_hip import synth
+    rng = synth.rng_for(0xF1)
+    w = synth.weight(rng, synth.Q4_K, 256, 4096)          # 589824 bytes
+    f0 = _fp(w)
+    assert _fp(w.copy()) == f0                             # same bytes, other address
+    w2 = w.copy()
+    w2[:] = synth.weight(rng, synth.Q4_K, 256, 4096)       # another weight, same shape
+    assert _fp(w2) != f0
+    # a one-byte change inside each sampled window (first, middle, last) is seen
+    span = w.nbytes - 16
+    for i in (0, 31, 63):
+        v = w.copy()
+        v[span * i // 63 + 7] ^= 0x40
+        assert _fp(v) != f0, i
+    # the size is part of it
+    assert _fp(w[:-144]) != f0
+    # tiny buffers (shorter than one window) work
+    t = np.arange(5, dtype=np.uint8)
+    assert _fp(t) != _fp(t[:4])
+
+
+# ---- *_dev entry points use no library-owned device memory ----------------
+
+def _functions(src: str):
+    """name -> body of every top-level function definition in a C++ file."""
+    out = {}
+    for m in re.finditer(r"^[A-Za-z_][\w\s\*&:<>,]*?\b(\w+)\s*\(([^;{]*?)\)\s*\{", src, re.M):
+        depth, i = 1, m.end()
+        while depth and i < len(src):
+            depth += {"{": 1, "}": -1}.get(src[i], 0)
+            i += 1
+        out[m.group(1)] = src[m.end():i]
+    return out
+
+
+def test_dev_entry_points_touch_no_library_buffers():
+    """Scratch on a *_dev path is the caller's: no function reachable from an
+    ihip_*_dev entry point reads or writes the library's staging buffers
+    (Ctx::x, y, h, t, src, nrm) or its argmax workspace, so calls on different
+    streams never share memory and nothing is freed under queued work."""
+    src = (ROOT / "inferno.jl_amd" / "csrc" / "api.hip").read_text()
+    fns = _functions(src)
+    roots = [n for n in fns if n.startswith("ihip_") and n.endswith("_dev")]
+    assert sorted(roots) == [s for s in declared_symbols() if s.endswith("_dev")]
+    seen, todo = set(), list(roots)
+    while todo:
+        n = todo.pop()
+        if n in seen:
+            continue
+        seen.add(n)
+        for callee in re.findall(r"\b(\w+)\s*\(", fns[n]):
+            if callee in fns and callee not in seen:
+                todo.append(callee)
+    bad = re.compile(r"(\bc\.|ctx\(\)\.)(x|y|h|t|src|nrm|argmax_ws|d_token|d_flags|stream)\b|\bensure\(|\bcopy_in\(")
+    for n in sorted(seen):
+        hits = bad.findall(fns[n])
+        assert not hits, f"{n} (reachable from a *_dev entry point) uses library buffers: {hits}"
+    assert "gate_up_dev_locked" in seen and "lm_head_dev_locked" in seen

@@ -147,6 +147,44 @@ def test_gemv_f64_row_layout_matches_numpy():
         assert np.all(np.abs(s - W @ x) <= oracle.tolerance(nrm, x))
 
 
+@pytest.mark.parametrize("t", TYPES + [synth.IQ4_NL])
+def test_gemv_f32_serial_bits(t):
+    """src/ModelCPU.jl:290-306 fixes the bits of the fallback: `sum_val +=
+    block_values[i] * x[col_idx]` rounds each product to fp32 and adds it to a
+    single fp32 accumulator in column order (Julia does not contract `a += b*c`
+    into an FMA).  numpy's accumulate over fp32-rounded products is that
+    sequential sum; an fp64 accumulator, a fused multiply-add or a pairwise or
+    lane-split sum each change the last bits of some rows."""
+    rng = synth.rng_for(0x5E + t)
+    outer, inner = 96, 4096 if t != synth.Q8_0 else 2048
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner) * np.float32(rng.uniform(0.5, 8))
+    W = oracle.dequant(t, w, outer * inner).reshape(outer, inner)
+    prods = W * x[None, :]                              # fp32 products, each rounded once
+    want = np.add.accumulate(prods, axis=1, dtype=np.float32)[:, -1]
+    got = oracle.gemv_f32_serial(t, w, x, inner, outer)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the pin discriminates: an fp64 accumulator rounded once differs somewhere
+    f64 = (W.astype(np.float64) @ x.astype(np.float64)).astype(np.float32)
+    assert not np.array_equal(f64.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemm_f64_is_the_per_token_gemv():
+    """The prefill oracle (src/ModelCPU.jl:1001-1017: one GEMV per token) must
+    give, for every token, exactly the GEMV oracle's fp64 sums: same products,
+    same column order.  Ragged shapes exercise the 8-row groups' tail."""
+    rng = synth.rng_for(0x61)
+    for t, T, outer, inner in ((synth.Q4_K, 7, 37, 512), (synth.Q6_K, 5, 16, 256),
+                               (synth.Q8_0, 3, 9, 96), (synth.Q5_K, 1, 8, 256),
+                               (synth.Q4_K, 0, 8, 256)):
+        w = synth.weight(rng, t, outer, inner)
+        X = rng.standard_normal((T, inner)).astype(np.float32)
+        Y = oracle.gemm_f64(t, w, X, inner, outer)
+        assert Y.shape == (T, outer)
+        for k in range(T):
+            assert np.array_equal(Y[k], oracle.gemv_f64(t, w, X[k], inner, outer)), (t, k)
+
+
 def test_ffn_oracle_composition():
     rng = synth.rng_for(9)
     hidden, inter = 512, 768
