@@ -6,7 +6,7 @@
 // (src/kernels/quant_kernels.c:602-697 behind src/QuantizedKernels.jl:84-148
 // of Inferno.jl).  Unlike the reference they report failures through a
 // status code and ihip_last_error() instead of returning void.
-#include "../../include/inferno_hip.h"
+#include "inferno_hip.h"
 #include "kq_common.h"
 #include "kq_launch.h"
 

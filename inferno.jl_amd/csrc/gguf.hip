@@ -14,7 +14,7 @@
 // tensors); a tensor whose bytes run past the end of the file is an error;
 // versions other than 2 and 3 are refused (version 1 has 32-bit counts, which
 // the reference would misread after a warning).
-#include "../../include/inferno_hip.h"
+#include "inferno_hip.h"
 
 #include <cstdint>
 #include <cstring>

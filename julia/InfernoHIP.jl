@@ -1,0 +1,398 @@
+"""
+    InfernoHIP
+
+Drop-in for Inferno.jl's quantized-kernel call surface on the MI355X (gfx950)
+library `libinferno_hip.so` (C ABI: `include/inferno_hip.h`).  Three
+submodules carry the reference's module names, function names and argument
+meaning, so a caller switches by changing what it `using`s:
+
+* `InfernoHIP.QuantizedKernels` -- `src/QuantizedKernels.jl:14-16, 50-177`:
+  `quant_kernels_available`, `q4_k_gemv!`, `q5_k_gemv!`, `q6_k_gemv!`,
+  `q8_0_gemv!`, `quantize_q8_k!`, `vec_dot_q{4,5,6}_k_q8_k` on host
+  `Vector`s, plus `forget_weight!` for the device weight cache;
+* `InfernoHIP.Dequant` -- `src/Dequant.jl:5-6, 304-601, 655-693`:
+  `dequantize_q8_0`, `dequantize_q4_k`, `dequantize_q5_k`, `dequantize_q6_k`,
+  `dequantize_iq4_nl`;
+* `InfernoHIP.FusedKernels` -- `src/FusedKernels.jl:14-16, 203-311`:
+  `fused_mlp_gate_mul!`, `fused_silu_gate_mul!`, `gpu_argmax!` on DEVICE
+  vectors (AMDGPU.jl `ROCArray`s or anything `pointer` maps to device
+  memory), plus the fused decode calls the GPU forward makes
+  (`ffn_swiglu!`, `ffn_block!`, `lm_head_argmax!`).
+
+Errors: every library call returns a status; a non-zero status becomes an
+`ArgumentError` for bad arguments and NaN/+Inf/empty logits (the reference's
+`@assert` / `_validate_logits` cases, `src/CommonOps.jl:142-163`) and an
+`ErrorException` otherwise.  With the library missing, or `IHIP_DISABLE` set
+(the reference's `INFERNO_NO_QUANT_KERNELS`, `src/QuantizedKernels.jl:26-32`),
+`quant_kernels_available()` is `false` and every call throws
+`ErrorException("Quantized C kernel not available")`
+(`src/QuantizedKernels.jl:86`); there is no silent CPU fallback inside
+this module.
+
+Token ids come back 1-based, like the rest of the engine (the library's are
+0-based).
+"""
+module InfernoHIP
+
+const LIBIHIP = get(ENV, "INFERNO_HIP_LIB",
+                    joinpath(@__DIR__, "..", "inferno.jl_amd", "lib", "libinferno_hip.so"))
+const LIBHIP = "libamdhip64"
+
+const IHIP_ARGMAX_WS_BYTES = 262144
+const FLAG_NAN = UInt32(1)
+const FLAG_POSINF = UInt32(2)
+
+# GGML type ids (src/GGUF.jl:25-60)
+const GGML_Q8_0 = 8
+const GGML_Q4_K = 12
+const GGML_Q5_K = 13
+const GGML_Q6_K = 14
+const GGML_IQ4_NL = 20
+
+function available()
+    isfile(LIBIHIP) || return false
+    return ccall((:ihip_available, LIBIHIP), Cint, ()) == 1
+end
+
+function require()
+    available() || error("Quantized C kernel not available")
+    return nothing
+end
+
+function check(rc::Cint)
+    rc == 0 && return nothing
+    msg = unsafe_string(ccall((:ihip_last_error, LIBIHIP), Cstring, ()))
+    # -1 invalid argument, -4 NaN/+Inf logits, -7 empty logits
+    (rc == -1 || rc == -4 || rc == -7) && throw(ArgumentError(msg))
+    error("libinferno_hip: " * msg)
+end
+
+# ---- device memory for the argmax workspace (HIP runtime, no AMDGPU.jl) -----
+
+"""
+    ArgmaxWorkspace()
+
+`IHIP_ARGMAX_WS_BYTES` of device memory for the per-workgroup partial maxima
+plus the device token and flags.  Calls that share one must not overlap on
+the GPU; the memory is freed by the finalizer.
+"""
+mutable struct ArgmaxWorkspace
+    ptr::Ptr{Cvoid}
+    function ArgmaxWorkspace()
+        p = Ref{Ptr{Cvoid}}(C_NULL)
+        rc = ccall((:hipMalloc, LIBHIP), Cint, (Ref{Ptr{Cvoid}}, Csize_t), p, IHIP_ARGMAX_WS_BYTES + 64)
+        rc == 0 || error("hipMalloc of the argmax workspace failed ($rc)")
+        ws = new(p[])
+        finalizer(w -> ccall((:hipFree, LIBHIP), Cint, (Ptr{Cvoid},), w.ptr), ws)
+        return ws
+    end
+end
+token_ptr(ws::ArgmaxWorkspace) = Ptr{Int32}(ws.ptr + IHIP_ARGMAX_WS_BYTES)
+flags_ptr(ws::ArgmaxWorkspace) = Ptr{UInt32}(ws.ptr + IHIP_ARGMAX_WS_BYTES + 32)
+
+"""Wait for `stream`, read the token and flags back, return the 1-based token."""
+function read_token(ws::ArgmaxWorkspace, stream::Ptr{Cvoid})
+    ccall((:hipStreamSynchronize, LIBHIP), Cint, (Ptr{Cvoid},), stream) == 0 ||
+        error("hipStreamSynchronize failed")
+    tok = Ref{Int32}(0)
+    fl = Ref{UInt32}(0)
+    ccall((:hipMemcpy, LIBHIP), Cint, (Ref{Int32}, Ptr{Int32}, Csize_t, Cint), tok, token_ptr(ws), 4, 2) == 0 ||
+        error("hipMemcpy of the token failed")
+    ccall((:hipMemcpy, LIBHIP), Cint, (Ref{UInt32}, Ptr{UInt32}, Csize_t, Cint), fl, flags_ptr(ws), 4, 2) == 0 ||
+        error("hipMemcpy of the flags failed")
+    (fl[] & FLAG_NAN) != 0 && throw(ArgumentError("logits must not contain NaN"))
+    (fl[] & FLAG_POSINF) != 0 && throw(ArgumentError("logits must not contain +Inf"))
+    return Int(tok[]) + 1
+end
+
+# ============================================================================
+module QuantizedKernels
+# src/QuantizedKernels.jl:14-16
+export quant_kernels_available
+export q4_k_gemv!, q5_k_gemv!, q6_k_gemv!, q8_0_gemv!
+export quantize_q8_k!, vec_dot_q4_k_q8_k, vec_dot_q5_k_q8_k, vec_dot_q6_k_q8_k
+
+import ..InfernoHIP: LIBIHIP, check, require, available
+
+"""src/QuantizedKernels.jl:50-51: the kernels can run (a gfx950 device, IHIP_DISABLE unset)."""
+quant_kernels_available() = available()
+
+function check_dims(out, weight_data, x, inner_dim, outer_dim, elems, bytes)
+    inner_dim > 0 && outer_dim > 0 && inner_dim % elems == 0 ||
+        throw(ArgumentError("inner_dim=$inner_dim must be a positive multiple of $elems"))
+    length(out) >= outer_dim || throw(ArgumentError("out is shorter than outer_dim"))
+    length(x) >= inner_dim || throw(ArgumentError("x is shorter than inner_dim"))
+    length(weight_data) >= outer_dim * (inner_dim ÷ elems) * bytes ||
+        throw(ArgumentError("weight_data is too short for $outer_dim x $inner_dim"))
+    return nothing
+end
+
+"""
+    q4_k_gemv!(out, weight_data, x, inner_dim, outer_dim)
+
+src/QuantizedKernels.jl:84-96 on the GPU: `out = W x` for the Q4_K blocks of an
+`outer_dim x inner_dim` matrix, fp32 activations (within 1e-4 ||w_row|| ||x||
+of the exact sum).  The weight is uploaded on first use and cached.
+"""
+function q4_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                    x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 144)
+    check(ccall((:ihip_q4_k_gemv, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid}, Cint, Cint),
+                weight_data, x, out, C_NULL, inner_dim, outer_dim))
+    return out
+end
+
+"""src/QuantizedKernels.jl:103-115 on the GPU (Q5_K)."""
+function q5_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                    x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 176)
+    check(ccall((:ihip_q5_k_gemv, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid}, Cint, Cint),
+                weight_data, x, out, C_NULL, inner_dim, outer_dim))
+    return out
+end
+
+"""src/QuantizedKernels.jl:122-134 on the GPU (Q6_K)."""
+function q6_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                    x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 210)
+    check(ccall((:ihip_q6_k_gemv, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid}, Cint, Cint),
+                weight_data, x, out, C_NULL, inner_dim, outer_dim))
+    return out
+end
+
+"""src/QuantizedKernels.jl:141-150 on the GPU (Q8_0, fp32 x)."""
+function q8_0_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                    x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 32, 34)
+    check(ccall((:ihip_q8_0_gemv, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Cint, Cint),
+                weight_data, x, out, inner_dim, outer_dim))
+    return out
+end
+
+"""
+    quantize_q8_k!(q8_buf, x, inner_dim)
+
+src/QuantizedKernels.jl:153-158 with the reference's argument order, passed to
+the C function in ITS order (x, y, k): the reference's ccall hands
+`quantize_row_q8_K` the two pointers swapped and a 32-bit count.
+"""
+function quantize_q8_k!(q8_buf::Vector{UInt8}, x::Vector{Float32}, inner_dim::Int)
+    require()
+    inner_dim > 0 && inner_dim % 256 == 0 ||
+        throw(ArgumentError("inner_dim=$inner_dim must be a positive multiple of 256"))
+    length(q8_buf) >= (inner_dim ÷ 256) * 292 || throw(ArgumentError("q8_buf is too short"))
+    check(ccall((:ihip_quantize_row_q8_k, LIBIHIP), Cint,
+                (Ptr{Float32}, Ptr{UInt8}, Int64), x, q8_buf, inner_dim))
+    return q8_buf
+end
+
+"""src/QuantizedKernels.jl:161-165: one Q4_K row of nb blocks against nb Q8_K blocks."""
+function vec_dot_q4_k_q8_k(weight_ptr::Ptr{UInt8}, q8_ptr::Ptr{UInt8}, nb::Cint)
+    require()
+    s = Ref{Cfloat}(0)
+    check(ccall((:ihip_vec_dot_q4_k_q8_k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{UInt8}, Cint, Ref{Cfloat}), weight_ptr, q8_ptr, nb, s))
+    return s[]
+end
+
+"""src/QuantizedKernels.jl:168-172 (Q5_K)."""
+function vec_dot_q5_k_q8_k(weight_ptr::Ptr{UInt8}, q8_ptr::Ptr{UInt8}, nb::Cint)
+    require()
+    s = Ref{Cfloat}(0)
+    check(ccall((:ihip_vec_dot_q5_k_q8_k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{UInt8}, Cint, Ref{Cfloat}), weight_ptr, q8_ptr, nb, s))
+    return s[]
+end
+
+"""src/QuantizedKernels.jl:175-179 (Q6_K)."""
+function vec_dot_q6_k_q8_k(weight_ptr::Ptr{UInt8}, q8_ptr::Ptr{UInt8}, nb::Cint)
+    require()
+    s = Ref{Cfloat}(0)
+    check(ccall((:ihip_vec_dot_q6_k_q8_k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{UInt8}, Cint, Ref{Cfloat}), weight_ptr, q8_ptr, nb, s))
+    return s[]
+end
+
+"""
+    forget_weight!(weight_data)
+
+Drop the cached device copy of a host weight (a `Q*_Matrix`'s `data`).  The
+cache already re-uploads a buffer whose sampled content changed; call this
+when a weight is freed, or after an in-place rewrite that might leave every
+sampled window unchanged.  Attach it as a finalizer to keep-quantized
+matrices (src/LoaderCPU.jl:134-163).
+"""
+function forget_weight!(weight_data::Vector{UInt8})
+    check(ccall((:ihip_weight_forget, LIBIHIP), Cint, (Ptr{UInt8},), weight_data))
+    return nothing
+end
+
+end # module QuantizedKernels
+
+# ============================================================================
+module Dequant
+# src/Dequant.jl:5-6 (the K-quant, Q8_0 and IQ4_NL exports)
+export dequantize_q8_0, dequantize_q4_k, dequantize_q5_k, dequantize_q6_k, dequantize_iq4_nl
+
+import ..InfernoHIP: LIBIHIP, check, require, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_IQ4_NL
+
+function dequant(t::Int, data::Vector{UInt8}, n::Int, elems::Int, bytes::Int)
+    require()
+    n >= 0 && n % elems == 0 || throw(ArgumentError("n=$n is not a multiple of $elems"))
+    length(data) >= (n ÷ elems) * bytes || throw(ArgumentError("data is too short for $n elements"))
+    out = Vector{Float32}(undef, n)
+    check(ccall((:ihip_dequantize, LIBIHIP), Cint,
+                (Cint, Ptr{UInt8}, Ptr{Float32}, Int64), t, data, out, n))
+    return out
+end
+
+"""src/Dequant.jl:304-321, bit-exact."""
+dequantize_q8_0(data::Vector{UInt8}, n::Int) = dequant(GGML_Q8_0, data, n, 32, 34)
+"""src/Dequant.jl:325-375, bit-exact."""
+dequantize_q4_k(data::Vector{UInt8}, n::Int) = dequant(GGML_Q4_K, data, n, 256, 144)
+"""src/Dequant.jl:379-441, bit-exact."""
+dequantize_q5_k(data::Vector{UInt8}, n::Int) = dequant(GGML_Q5_K, data, n, 256, 176)
+"""src/Dequant.jl:558-601, bit-exact."""
+dequantize_q6_k(data::Vector{UInt8}, n::Int) = dequant(GGML_Q6_K, data, n, 256, 210)
+"""src/Dequant.jl:655-693, bit-exact."""
+dequantize_iq4_nl(data::Vector{UInt8}, n::Int) = dequant(GGML_IQ4_NL, data, n, 32, 18)
+
+end # module Dequant
+
+# ============================================================================
+module FusedKernels
+# src/FusedKernels.jl:14-16 (the element-wise fusions and the greedy argmax of
+# the decode path) and the fused decode calls of a device-resident forward.
+export fused_mlp_gate_mul!, fused_silu_gate_mul!, gpu_argmax!
+export ffn_swiglu!, ffn_block!, lm_head_argmax!
+
+import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
+
+"""
+    fused_mlp_gate_mul!(gate, up; stream = C_NULL)
+
+src/FusedKernels.jl:203-214: `gate .= gate / (1 + exp(-gate)) .* up` in place,
+on device vectors, asynchronous on `stream` (a hipStream_t).
+"""
+function fused_mlp_gate_mul!(gate::AbstractVector{Float32}, up::AbstractVector{Float32};
+                             stream::Ptr{Cvoid} = C_NULL)
+    require()
+    n = length(gate)
+    length(up) == n || throw(DimensionMismatch("gate and up differ in length"))
+    n == 0 && return gate
+    check(ccall((:ihip_fused_mlp_gate_mul_dev, LIBIHIP), Cint,
+                (Ptr{Float32}, Ptr{Float32}, Int64, Ptr{Cvoid}), gate, up, n, stream))
+    return gate
+end
+
+"""
+    fused_silu_gate_mul!(out, x, gate; stream = C_NULL)
+
+src/FusedKernels.jl:219-230: `out .= x / (1 + exp(-x)) .* gate`.
+"""
+function fused_silu_gate_mul!(out::AbstractVector{Float32}, x::AbstractVector{Float32},
+                              gate::AbstractVector{Float32}; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    n = length(out)
+    length(x) == n && length(gate) == n || throw(DimensionMismatch("lengths differ"))
+    n == 0 && return out
+    check(ccall((:ihip_fused_silu_gate_mul_dev, LIBIHIP), Cint,
+                (Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Int64, Ptr{Cvoid}), out, x, gate, n, stream))
+    return out
+end
+
+"""
+    gpu_argmax!(logits; ws = ArgmaxWorkspace(), stream = C_NULL) -> Int
+
+src/FusedKernels.jl:271-311: the 1-based index of the largest logit, the
+lowest index among equal maxima, reduced on the device (no per-chunk host
+pass).  Empty logits return 1 as the reference does; NaN or +Inf logits
+throw ArgumentError (`_validate_logits`, src/CommonOps.jl:142-163).
+"""
+function gpu_argmax!(logits::AbstractVector{Float32}; ws::ArgmaxWorkspace = ArgmaxWorkspace(),
+                     stream::Ptr{Cvoid} = C_NULL)
+    require()
+    n = length(logits)
+    n == 0 && return 1
+    check(ccall((:ihip_argmax_dev, LIBIHIP), Cint,
+                (Ptr{Float32}, Int64, Ptr{Int32}, Ptr{UInt32}, Ptr{Cvoid}, Ptr{Cvoid}),
+                logits, n, token_ptr(ws), flags_ptr(ws), ws.ptr, stream))
+    return read_token(ws, stream)
+end
+
+"""
+    ffn_swiglu!(y, h, gate_type, wg, up_type, wu, down_type, wd, x, hidden, inter; stream)
+
+mlp_forward (src/ModelCPU.jl:482-508) on device memory: `h = silu(Wg x) .* (Wu x)`,
+`y = Wd h`.  wg, wu, wd are device weight pointers (16-byte aligned GGML
+blocks, e.g. from ihip_gguf_upload + ihip_weight_device_ptr); h holds
+`inter` floats.
+"""
+function ffn_swiglu!(y::AbstractVector{Float32}, h::AbstractVector{Float32}, gate_type::Integer,
+                     wg::Ptr{Cvoid}, up_type::Integer, wu::Ptr{Cvoid}, down_type::Integer,
+                     wd::Ptr{Cvoid}, x::AbstractVector{Float32}, hidden::Integer, inter::Integer;
+                     stream::Ptr{Cvoid} = C_NULL)
+    require()
+    length(h) >= inter && length(y) >= hidden && length(x) >= hidden ||
+        throw(DimensionMismatch("x, h or y too short"))
+    check(ccall((:ihip_ffn_swiglu_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Cint, Ptr{Cvoid}, Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32},
+                 Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
+                gate_type, wg, up_type, wu, down_type, wd, x, h, y, hidden, inter, stream))
+    return y
+end
+
+"""
+    ffn_block!(x, h, gate_type, wg, up_type, wu, down_type, wd, norm_w, eps, hidden, inter; stream)
+
+The MLP half of a decoder layer (src/ModelCPU.jl:913-920) in place on x:
+`x += Wd (silu(Wg n) .* (Wu n))`, `n = rmsnorm_cpu!(x) .* norm_w`.  h is caller
+scratch of `ihip_ffn_block_scratch_floats` floats.
+"""
+function ffn_block!(x::AbstractVector{Float32}, h::AbstractVector{Float32}, gate_type::Integer,
+                    wg::Ptr{Cvoid}, up_type::Integer, wu::Ptr{Cvoid}, down_type::Integer,
+                    wd::Ptr{Cvoid}, norm_w::AbstractVector{Float32}, eps::Real, hidden::Integer,
+                    inter::Integer; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    need = ccall((:ihip_ffn_block_scratch_floats, LIBIHIP), Csize_t, (Cint, Cint, Cint, Cint),
+                 gate_type, up_type, hidden, inter)
+    length(h) >= need || throw(DimensionMismatch("h needs $need floats"))
+    check(ccall((:ihip_ffn_block_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Cint, Ptr{Cvoid}, Cint, Ptr{Cvoid}, Ptr{Float32}, Cfloat,
+                 Ptr{Float32}, Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
+                gate_type, wg, up_type, wu, down_type, wd, norm_w, Float32(eps), x, h, hidden,
+                inter, stream))
+    return x
+end
+
+"""
+    lm_head_argmax!(logits, w_type, w, x, hidden, vocab; ws, stream) -> Int
+
+lm_head_project! + greedy token (src/ModelCPU.jl:1091-1123, src/CommonOps.jl:142-163)
+with the argmax fused into the GEMV where the library fuses it: the 1-based
+token.  `logits` (device, vocab floats) may be `nothing` when
+`ihip_lm_head_fused` says so.
+"""
+function lm_head_argmax!(logits::Union{Nothing,AbstractVector{Float32}}, w_type::Integer,
+                         w::Ptr{Cvoid}, x::AbstractVector{Float32}, hidden::Integer, vocab::Integer;
+                         ws::ArgmaxWorkspace = ArgmaxWorkspace(), stream::Ptr{Cvoid} = C_NULL)
+    require()
+    lp = logits === nothing ? Ptr{Float32}(C_NULL) : Base.unsafe_convert(Ptr{Float32}, logits)
+    check(ccall((:ihip_lm_head_argmax_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Ptr{Int32}, Ptr{UInt32}, Cint, Cint,
+                 Ptr{Cvoid}, Ptr{Cvoid}),
+                w_type, w, x, lp, token_ptr(ws), flags_ptr(ws), hidden, vocab, ws.ptr, stream))
+    return read_token(ws, stream)
+end
+
+end # module FusedKernels
+
+end # module InfernoHIP
