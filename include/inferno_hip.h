@@ -235,6 +235,19 @@ int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *
 int ihip_lm_head_argmax_dev(int ggml_type, const void *w, const float *x, float *logits,
                             int32_t *token, uint32_t *flags, int hidden, int vocab,
                             void *workspace, ihip_stream stream);
+/* ihip_lm_head_argmax_dev without the workspace argument.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  The argmax partials go to a library array of
+ * IHIP_ARGMAX_WS_BYTES in each device's memory (one 16-byte partial per
+ * workgroup, at most 16384; a call that would need more is IHIP_ERR_INVALID),
+ * resolved once per device -- at ihip_init or at the first call on that
+ * device -- and never allocated per call.  Every call on a device shares its
+ * array: calls that overlap on one GPU race.  Same arguments, outputs and
+ * errors as ihip_lm_head_argmax_dev otherwise. */
+int ihip_lm_head_argmax_noalloc_dev(int ggml_type, const void *w, const float *x, float *logits,
+                                    int32_t *token, uint32_t *flags, int hidden, int vocab,
+                                    ihip_stream stream);
 /* 1 when ihip_lm_head_argmax_dev with these arguments fuses the argmax into
  * the GEMV (logits may then be NULL), else 0. */
 int ihip_lm_head_fused(int ggml_type, const void *w, const float *x, int hidden, int vocab);

@@ -9,6 +9,7 @@
 #include "inferno_hip.h"
 #include "kq_common.h"
 #include "kq_launch.h"
+#include "kq_sdig_plan.h"
 
 #include <cstdarg>
 #include <cstdio>
@@ -111,6 +112,35 @@ Ctx &ctx()
     return c;
 }
 
+// Scratch of the allocation-free lm_head entry point: the argmax partials
+// (one 16-byte partial per workgroup, at most kArgMaxParts of them).  Every
+// device the library runs on holds its own copy for the life of the process;
+// the kernels write every partial they read, so nothing needs clearing.  In
+// host code `scratch` only names the symbol: kernels get the device address
+// resolved by hipGetSymbolAddress, kept per device in scratch_dev.
+static __device__ __align__(256) uint8_t scratch[IHIP_ARGMAX_WS_BYTES];
+constexpr int kMaxDevices = 64;
+void *scratch_dev[kMaxDevices]; // device address of `scratch`, per device (nullptr: not resolved yet)
+
+// The current device's copy of `scratch` (resolved on the first call on that
+// device, with it current; the library mutex is held).
+int scratch_for_current_device(void **p)
+{
+    int dev = -1;
+    HIPCHK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(IHIP_ERR_INVALID, "device %d is beyond the %d the library tracks", dev, kMaxDevices);
+    if (!scratch_dev[dev]) {
+        void *q = nullptr;
+        HIPCHK(hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)));
+        if (!q)
+            return fail(IHIP_ERR_HIP, "no device address for the scratch array");
+        scratch_dev[dev] = q;
+    }
+    *p = scratch_dev[dev];
+    return IHIP_OK;
+}
+
 bool disabled()
 {
     const char *e = getenv("IHIP_DISABLE");
@@ -176,6 +206,8 @@ int init_locked(int device)
         return fail(IHIP_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
                     device, prop.gcnArchName);
     HIPCHK(hipSetDevice(device));
+    void *sp = nullptr;
+    RET_IF(scratch_for_current_device(&sp)); // set-up of the allocation-free entry point
     HIPCHK(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
     HIPCHK(hipMalloc(&c.argmax_ws, IHIP_ARGMAX_WS_BYTES + 64));
     HIPCHK(hipMemset(c.argmax_ws, 0, IHIP_ARGMAX_WS_BYTES + 64));
@@ -340,6 +372,11 @@ int gate_up_dev_locked(int gt, const void *wg, int ut, const void *wu, const flo
 bool lm_head_fused(int type, const void *w, const float *x, int hidden, int vocab)
 {
     return (type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden) && lm_head_fusable(vocab);
+}
+
+int lm_head_parts(int type, const void *w, const float *x, int hidden, int vocab)
+{
+    return lm_head_argmax_parts(type, hidden, vocab, lm_head_fused(type, w, x, hidden, vocab));
 }
 
 int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, int32_t *token,
@@ -882,6 +919,24 @@ int ihip_lm_head_argmax_dev(int ggml_type, const void *w, const float *x, float 
     if (disabled())
         return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
     return lm_head_dev_locked(ggml_type, w, x, logits, token, flags, hidden, vocab, workspace,
+                              (hipStream_t)stream);
+}
+
+int ihip_lm_head_argmax_noalloc_dev(int ggml_type, const void *w, const float *x, float *logits,
+                                    int32_t *token, uint32_t *flags, int hidden, int vocab,
+                                    ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(ggml_type, hidden, vocab));
+    const int nparts = lm_head_parts(ggml_type, w, x, hidden, vocab);
+    if (nparts > kArgMaxParts)
+        return fail(IHIP_ERR_INVALID, "this lm_head needs %d argmax partials; the scratch holds %d",
+                    nparts, kArgMaxParts);
+    void *ws = nullptr;
+    RET_IF(scratch_for_current_device(&ws));
+    return lm_head_dev_locked(ggml_type, w, x, logits, token, flags, hidden, vocab, ws,
                               (hipStream_t)stream);
 }
 

@@ -28,6 +28,8 @@
 //     one-workgroup kernel reduces the partials, so no two workgroups touch
 //     the same address.
 #include "inferno_hip.h"
+
+#include <algorithm>
 #include "kq_common.h"
 #include "kq_launch.h"
 #include "kq_sdig_plan.h"
@@ -1822,6 +1824,15 @@ static void launch_argmax_finalize(const void *ws, int nparts, int32_t *token, u
     }
 }
 
+int lm_head_argmax_parts(int type, int hidden, int vocab, bool fused)
+{
+    if (!fused) // the GEMV, then the standalone argmax over the logits
+        return (int)std::min<int64_t>(std::max<int64_t>(1, ((int64_t)vocab + 255) / 256), kArgMaxParts);
+    const int nblk = hidden / block_elems(type);
+    return sdig_usable(type, nblk) ? sdig_plan(type, nblk, vocab, true, sdig_knobs(), device_cus()).grid
+                                   : stream_grid(vocab, stream_rows(vocab, true));
+}
+
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s)
@@ -1836,11 +1847,7 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
     }
     if (e != hipSuccess)
         return e;
-    const int nblk = hidden / block_elems(type);
-    const int nparts = sdig_usable(type, nblk)
-                           ? sdig_plan(type, nblk, vocab, true, sdig_knobs(), device_cus()).grid
-                           : stream_grid(vocab, stream_rows(vocab, true));
-    launch_argmax_finalize(ws, nparts, token, flags, s);
+    launch_argmax_finalize(ws, lm_head_argmax_parts(type, hidden, vocab, true), token, flags, s);
     return hipGetLastError();
 }
 

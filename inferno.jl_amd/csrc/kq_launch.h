@@ -18,6 +18,9 @@ hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const
                                  const float *norm_w = nullptr, float eps = 0.0f);
 // The fused lm_head argmax handles vocab <= 16384 chunks of at most 64 rows.
 bool lm_head_fusable(int vocab);
+// Argmax partials (16 bytes each) one lm_head call writes: fused into the
+// streamed GEMV, or the standalone argmax after the GEMV.
+int lm_head_argmax_parts(int type, int hidden, int vocab, bool fused);
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s);

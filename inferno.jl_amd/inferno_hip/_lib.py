@@ -96,6 +96,7 @@ SIGNATURES = {
     "ihip_gate_up_swiglu_dev": ([_i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_ffn_swiglu_dev": ([_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_lm_head_argmax_dev": ([_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp], _i),
+    "ihip_lm_head_argmax_noalloc_dev": ([_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_lm_head_fused": ([_i, _vp, _vp, _i, _i], _i),
     "ihip_ffn_block_scratch_floats": ([_i, _i, _i, _i], _sz),
     "ihip_argmax_dev": ([_vp, _i64, _vp, _vp, _vp, _vp], _i),
