@@ -72,6 +72,8 @@ def parse():
     ap.add_argument("--only", default="", help="gemv: the headline GEMV only")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the short program the rocprofv3 --pmc runs profile")
+    ap.add_argument("--floors", action="store_true",
+                    help="sweep the empty-launch and read floors over launch shapes")
     return ap.parse_args()
 
 
@@ -94,7 +96,7 @@ def floors_lib():
         return None
     L = C.CDLL(str(p))
     L.ifl_empty.argtypes = [C.c_int, C.c_int, C.c_void_p]
-    L.ifl_read.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_int, C.c_void_p]
+    L.ifl_read.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
     L.ifl_empty.restype = L.ifl_read.restype = C.c_int
     return L
 
@@ -215,7 +217,7 @@ def q4k_gemv(torch, stream, synth, D, oracle, steps, warmup):
 
         def read(i):
             assert F.ifl_read(ws[i % NCOPY].data.data_ptr(), w.size, 0x9E3779B9, out.data_ptr(),
-                              grid, torch.cuda.current_stream().cuda_stream) == 0
+                              grid, 512, torch.cuda.current_stream().cuda_stream) == 0
         n = 10
         res["floor_empty_us"] = time_sweeps(torch, stream, empty, NCOPY, n, 2) * 1e3 / (n * NCOPY)
         res["floor_read_us"] = time_sweeps(torch, stream, read, NCOPY, n, 2) * 1e3 / (n * NCOPY)
@@ -434,6 +436,33 @@ def pmc_workload(torch, synth, D):
           "12 lm_heads, 10 prefills", flush=True)
 
 
+def floors_sweep(torch, stream):
+    """Per-launch cost of an empty launch and of a fully coalesced read of
+    9437184 bytes (and of twice that: the difference is the transfer time of
+    the bytes alone) over launch shapes, 64 rotated buffers, HIP graph."""
+    F = floors_lib()
+    if F is None:
+        raise SystemExit("inferno.jl_amd/lib/libinferno_floors.so is not built")
+    nb = 9437184
+    big = torch.empty(NCOPY, 2 * nb, dtype=torch.uint8, device="cuda").random_(0, 255)
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cs = lambda: torch.cuda.current_stream().cuda_stream
+
+    def per_launch(fn, sweeps=10):
+        return time_sweeps(torch, stream, fn, NCOPY, sweeps, 2) * 1e3 / (sweeps * NCOPY)
+    print("| launch | grid x block | us per launch |\n|---|---|---|", flush=True)
+    for g, b in ((1, 64), (256, 64), (256, 512), (1024, 256), (2048, 256), (4096, 256)):
+        us = per_launch(lambda i: F.ifl_empty(g, b, cs()))
+        print(f"| empty | {g} x {b} | {us:.3f} |", flush=True)
+    print("\n| read | grid x block | 9437184 B us | 2 x 9437184 B us | marginal us | marginal GB/s |\n"
+          "|---|---|---|---|---|---|", flush=True)
+    for g, b in ((128, 1024), (256, 512), (512, 512), (1024, 256), (2048, 256)):
+        r = [per_launch(lambda i: F.ifl_read(big[i].data_ptr(), n, 0x9E3779B9, out.data_ptr(), g, b, cs()))
+             for n in (nb, 2 * nb)]
+        print(f"| read | {g} x {b} | {r[0]:.3f} | {r[1]:.3f} | {r[1] - r[0]:.3f} | "
+              f"{nb / (r[1] - r[0]) / 1e3:.0f} |", flush=True)
+
+
 # --------------------------------------------------------------- CPU baseline --
 
 def _host_info():
@@ -566,6 +595,9 @@ def main():
         pmc_workload(torch, synth, D)
         return
     stream = torch.cuda.Stream()
+    if args.floors:
+        floors_sweep(torch, stream)
+        return
     steps, warmup = max(1, args.steps), max(0, args.warmup)
 
     log(f"Q4_K GEMV 4096x4096: warmup {warmup} sweeps, {steps} timed sweeps of {NCOPY} launches")

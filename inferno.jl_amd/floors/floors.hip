@@ -22,8 +22,8 @@ __global__ void k_floor_empty() {}
 // consecutive bytes) and folds them; the store is taken only when the fold
 // equals `key` (never, for the keys bench.py passes), so the loads are live.
 template <int LPT>
-__global__ __launch_bounds__(512) void k_floor_read(const uint4 *__restrict__ w, uint64_t n16,
-                                                    uint32_t key, uint32_t *out)
+__global__ __launch_bounds__(1024) void k_floor_read(const uint4 *__restrict__ w, uint64_t n16,
+                                                     uint32_t key, uint32_t *out)
 {
     const uint64_t per_wg = (n16 + gridDim.x - 1) / gridDim.x;
     const uint64_t base = (uint64_t)blockIdx.x * per_wg;
@@ -51,21 +51,22 @@ int ifl_empty(int grid, int block, void *stream)
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// n: bytes to read (a multiple of 16); the grid's workgroups of 512 threads
-// split them into contiguous slices of at most 16 loads per thread.
-int ifl_read(const void *w, uint64_t n, uint32_t key, uint32_t *out, int grid, void *stream)
+// n: bytes to read (a multiple of 16); the grid's workgroups of `block`
+// threads (64..1024) split them into contiguous slices of at most 32 loads
+// per thread.
+int ifl_read(const void *w, uint64_t n, uint32_t key, uint32_t *out, int grid, int block, void *stream)
 {
-    if (n % 16 || grid < 1)
+    if (n % 16 || grid < 1 || block < 64 || block > 1024 || block % 64)
         return -1;
     const uint64_t n16 = n / 16;
-    const uint64_t per_thread = (n16 + (uint64_t)grid * 512 - 1) / ((uint64_t)grid * 512);
+    const uint64_t per_thread = (n16 + (uint64_t)grid * block - 1) / ((uint64_t)grid * block);
     const hipStream_t s = (hipStream_t)stream;
 #define IFL_R(L)                                                                                   \
     if (per_thread <= L) {                                                                         \
-        hipLaunchKernelGGL(k_floor_read<L>, dim3(grid), dim3(512), 0, s, (const uint4 *)w, n16, key, out); \
+        hipLaunchKernelGGL(k_floor_read<L>, dim3(grid), dim3(block), 0, s, (const uint4 *)w, n16, key, out); \
         return hipGetLastError() == hipSuccess ? 0 : -1;                                           \
     }
-    IFL_R(1) IFL_R(2) IFL_R(4) IFL_R(5) IFL_R(8) IFL_R(16)
+    IFL_R(1) IFL_R(2) IFL_R(4) IFL_R(5) IFL_R(8) IFL_R(9) IFL_R(16) IFL_R(32)
 #undef IFL_R
     return -1;
 }
