@@ -68,6 +68,9 @@ struct XWide {
 };
 
 constexpr int kXPadFloats = 4096 + 4096 / 64 * 4;
+// float4s of a 4096-element pass per thread of an NT-thread workgroup (768
+// threads: two, the second only for threads below 256)
+__host__ __device__ constexpr int xnv(int nt) { return (1024 + nt - 1) / nt; }
 __device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
 
 // Stage x[col0, col0 + 4096) (zeros past `inner`) and its 128 sub-block sums.
@@ -76,6 +79,7 @@ __device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
 template <int NT>
 __device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&xv)[1024 / NT])
 {
+    static_assert(1024 % NT == 0, "fp32 staging: NT divides 1024");
     const int tid = threadIdx.x;
 #pragma unroll
     for (int k = 0; k < 1024 / NT; ++k) {
@@ -93,13 +97,14 @@ __device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&x
 
 template <int NT>
 __device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col0, int inner,
-                                            float4 (&xv)[1024 / NT])
+                                            float4 (&xv)[xnv(NT)])
 {
 #pragma unroll
-    for (int k = 0; k < 1024 / NT; ++k) {
-        const int col = col0 + 4 * (threadIdx.x + NT * k);
-        xv[k] = col < inner ? *reinterpret_cast<const float4 *>(x + col)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < xnv(NT); ++k) {
+        const int f = threadIdx.x + NT * k; // float4 of the pass
+        const int col = col0 + 4 * f;
+        xv[k] = (f < 1024 && col < inner) ? *reinterpret_cast<const float4 *>(x + col)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
@@ -271,11 +276,14 @@ __device__ __forceinline__ uint32_t abs_bits_max(float4 v)
 // steps.
 template <int NT>
 __device__ __forceinline__ void x_stage_dig(uint32_t *pl, float *xsum, int *xexp,
-                                            const float4 (&xv)[1024 / NT])
+                                            const float4 (&xv)[xnv(NT)])
 {
+    static_assert(NT % 64 == 0, "whole waves");
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < 1024 / NT; ++k) {
+    for (int k = 0; k < xnv(NT); ++k) {
+        if (tid + NT * k >= 1024)
+            continue; // past the pass; wave-uniform (NT and 1024 are multiples of 64)
         const float4 v = xv[k];
         float t = (v.x + v.y) + (v.z + v.w);
         uint32_t m = abs_bits_max(v);
@@ -393,7 +401,8 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
     using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
     constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
-    constexpr int NT = NWV * 64, NXV = 1024 / NT;
+    constexpr int NT = NWV * 64, NXV = xnv(NT);
+    static_assert(DIG || 1024 % NT == 0, "fp32 staging: NT divides 1024");
     // fp32 x (kXPadFloats) or its three digit planes (3 * kDigPlaneDw dwords)
     __shared__ __attribute__((aligned(16))) uint32_t xbuf[DIG ? 3 * kDigPlaneDw : kXPadFloats];
     __shared__ __attribute__((aligned(16))) float xsum[128];
@@ -523,21 +532,19 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
 // load is a microsecond or more, several group reductions).  A group is R
 // rows (GATEUP: R gate rows and the same R up rows).  Same outputs as
 // k_gemv_kwide<FMT, R, GATEUP, true, EXT, NWV>.
+// The walk itself, shared with the fused FFN kernel (phase A): the LDS it
+// stages x in is the caller's (xbuf: 3 * kDigPlaneDw dwords, xsum / xexp: 128
+// each, ssw: NWV floats).
 template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB>
-__global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restrict__ W,
-                                                         const uint8_t *__restrict__ W2,
-                                                         const float *__restrict__ x,
-                                                         float *y, int outer, int nblk,
-                                                         const float *__restrict__ nw, float eps,
-                                                         const float *resid, int epi)
+__device__ __forceinline__ void kpers_run(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
+                                          const float *__restrict__ x, float *y, int outer, int nblk,
+                                          const float *__restrict__ nw, float eps, const float *resid,
+                                          int epi, uint32_t *xbuf, float *xsum, int *xexp, float *ssw)
 {
     using F = KFmt<FMT>;
     constexpr int NM = GATEUP ? 2 : 1;
     constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
-    constexpr int NT = NWV * 64, NXV = 1024 / NT;
-    __shared__ __attribute__((aligned(16))) uint32_t xbuf[3 * kDigPlaneDw];
-    __shared__ __attribute__((aligned(16))) float xsum[128];
-    __shared__ __attribute__((aligned(8))) int xexp[128];
+    constexpr int NT = NWV * 64, NXV = xnv(NT);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -589,7 +596,6 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
     x_stage_dig<NT>(xbuf, xsum, xexp, xv);
     float scale = 1.0f;
     if constexpr (NORM) {
-        __shared__ float ssw[NWV];
         const float t = wave_sum(ssq);
         if (lane == 0)
             ssw[wave] = t;
@@ -648,6 +654,22 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
     for (int q = 0; q < NB; ++q)
         if (gi + (q + NB) * stride < ngroups)
             reduce(B[q], RV[q], gi + (q + NB) * stride);
+}
+
+template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restrict__ W,
+                                                         const uint8_t *__restrict__ W2,
+                                                         const float *__restrict__ x,
+                                                         float *y, int outer, int nblk,
+                                                         const float *__restrict__ nw, float eps,
+                                                         const float *resid, int epi)
+{
+    __shared__ __attribute__((aligned(16))) uint32_t xbuf[3 * kDigPlaneDw];
+    __shared__ __attribute__((aligned(16))) float xsum[128];
+    __shared__ __attribute__((aligned(8))) int xexp[128];
+    __shared__ float ssw[NWV];
+    kpers_run<FMT, R, GATEUP, EXT, NWV, NB>(W, W2, x, y, outer, nblk, nw, eps, resid, epi, xbuf, xsum,
+                                            xexp, ssw);
 }
 
 // ------------------------------------------------------------------------
@@ -1415,11 +1437,18 @@ __device__ __forceinline__ void sxd_load(SXD &X, const uint32_t (*d)[64][4], int
     }
 }
 
-template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
-__global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
-                                                       const float *x, float *y, int outer, int nblk,
-                                                       int rpc, ArgPart *__restrict__ parts,
-                                                       const float *resid, int epi)
+// The walk itself, shared with the fused FFN kernel (phase B).  LDS is the
+// caller's (ring: NW * D * sdig_slot bytes, 16-byte aligned; digs: the staged
+// digits of sdig_share_cap(NW) segments unless ARGMAX; part: kSdigMaxRows x 8;
+// wkey / wflag: NW each).  PRE: every wave issues its first D rows' copies
+// (which do not depend on x), then calls before_x() -- where the fused kernel
+// waits for x to be complete -- and only then loads x.
+template <int FMT, int NW, int D, bool ARGMAX, bool RESID, bool PRE, typename BeforeX>
+__device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const float *x, float *y,
+                                         int outer, int nblk, int rpc, ArgPart *__restrict__ parts,
+                                         const float *resid, int epi, uint8_t *ring,
+                                         uint32_t (*digs)[kDigQuads][64][4], float (*part)[8],
+                                         unsigned long long *wkey, uint32_t *wflag, BeforeX &&before_x)
 {
     using F = SFmt<FMT>;
     // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
@@ -1435,11 +1464,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     // segments whose digits can be staged in LDS (none for the lm_head: its 32 KB
     // workgroups run four to a CU, which the staging area would halve)
     constexpr int SHC = ARGMAX ? 0 : sdig_share_cap(NW);
-    __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * SLOT];
-    __shared__ __attribute__((aligned(16))) uint32_t digs[SHC > 0 ? SHC : 1][kDigQuads][64][4];
-    __shared__ float part[kSdigMaxRows][8];
-    __shared__ unsigned long long wkey[NW];
-    __shared__ uint32_t wflag[NW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1459,18 +1483,27 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     };
 
     // x first, then the first D rows' copies, all in flight together; the
-    // digits wait only for x (vmcnt counts completions in issue order)
+    // digits wait only for x (vmcnt counts completions in issue order).  PRE:
+    // the copies first, x after before_x(), and the wait is for everything.
     float4 xv[8];
     bool xact = false;
+    if constexpr (PRE) {
+#pragma unroll
+        for (int k = 0; k < D; ++k)
+            issue(k);
+        before_x();
+    }
     if (producer) // wave-uniform
         xact = staged_dig_issue<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!PRE) {
 #pragma unroll
-    for (int k = 0; k < D; ++k)
-        issue(k);
+        for (int k = 0; k < D; ++k)
+            issue(k);
+    }
     SXD X;
     if (producer) {
-        wait_vmcnt(D * IPR);
+        wait_vmcnt(PRE ? 0 : D * IPR);
         staged_dig_pin(xv);
         __builtin_amdgcn_sched_barrier(0);
         staged_dig_x<FMT>(xv, xact, X);
@@ -1577,6 +1610,22 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
         }
     }
     __builtin_amdgcn_s_waitcnt(0); // every copy has landed before the workgroup ends
+}
+
+template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
+__global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
+                                                       const float *x, float *y, int outer, int nblk,
+                                                       int rpc, ArgPart *__restrict__ parts,
+                                                       const float *resid, int epi)
+{
+    constexpr int SHC = ARGMAX ? 0 : sdig_share_cap(NW);
+    __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * sdig_slot(FMT)];
+    __shared__ __attribute__((aligned(16))) uint32_t digs[SHC > 0 ? SHC : 1][kDigQuads][64][4];
+    __shared__ float part[kSdigMaxRows][8];
+    __shared__ unsigned long long wkey[NW];
+    __shared__ uint32_t wflag[NW];
+    sdig_run<FMT, NW, D, ARGMAX, RESID, false>(W, x, y, outer, nblk, rpc, parts, resid, epi, ring, digs,
+                                               part, wkey, wflag, [] {});
 }
 
 // ------------------------------------------------------------------------
