@@ -532,9 +532,8 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
 // load is a microsecond or more, several group reductions).  A group is R
 // rows (GATEUP: R gate rows and the same R up rows).  Same outputs as
 // k_gemv_kwide<FMT, R, GATEUP, true, EXT, NWV>.
-// The walk itself, shared with the fused FFN kernel (phase A): the LDS it
-// stages x in is the caller's (xbuf: 3 * kDigPlaneDw dwords, xsum / xexp: 128
-// each, ssw: NWV floats).
+// The walk itself over LDS the caller declares (xbuf: 3 * kDigPlaneDw
+// dwords, xsum / xexp: 128 each, ssw: NWV floats).
 template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB>
 __device__ __forceinline__ void kpers_run(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
                                           const float *__restrict__ x, float *y, int outer, int nblk,
@@ -1437,18 +1436,15 @@ __device__ __forceinline__ void sxd_load(SXD &X, const uint32_t (*d)[64][4], int
     }
 }
 
-// The walk itself, shared with the fused FFN kernel (phase B).  LDS is the
-// caller's (ring: NW * D * sdig_slot bytes, 16-byte aligned; digs: the staged
-// digits of sdig_share_cap(NW) segments unless ARGMAX; part: kSdigMaxRows x 8;
-// wkey / wflag: NW each).  PRE: every wave issues its first D rows' copies
-// (which do not depend on x), then calls before_x() -- where the fused kernel
-// waits for x to be complete -- and only then loads x.
-template <int FMT, int NW, int D, bool ARGMAX, bool RESID, bool PRE, typename BeforeX>
+// The walk itself over LDS the caller declares (ring: NW * D * sdig_slot
+// bytes, 16-byte aligned; digs: the staged digits of sdig_share_cap(NW)
+// segments unless ARGMAX; part: kSdigMaxRows x 8; wkey / wflag: NW each).
+template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
 __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const float *x, float *y,
                                          int outer, int nblk, int rpc, ArgPart *__restrict__ parts,
                                          const float *resid, int epi, uint8_t *ring,
                                          uint32_t (*digs)[kDigQuads][64][4], float (*part)[8],
-                                         unsigned long long *wkey, uint32_t *wflag, BeforeX &&before_x)
+                                         unsigned long long *wkey, uint32_t *wflag)
 {
     using F = SFmt<FMT>;
     // every copy instruction moves 64 x 16 bytes with all lanes on (lanes past the
@@ -1483,27 +1479,18 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
     };
 
     // x first, then the first D rows' copies, all in flight together; the
-    // digits wait only for x (vmcnt counts completions in issue order).  PRE:
-    // the copies first, x after before_x(), and the wait is for everything.
+    // digits wait only for x (vmcnt counts completions in issue order).
     float4 xv[8];
     bool xact = false;
-    if constexpr (PRE) {
-#pragma unroll
-        for (int k = 0; k < D; ++k)
-            issue(k);
-        before_x();
-    }
     if (producer) // wave-uniform
         xact = staged_dig_issue<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!PRE) {
 #pragma unroll
-        for (int k = 0; k < D; ++k)
-            issue(k);
-    }
+    for (int k = 0; k < D; ++k)
+        issue(k);
     SXD X;
     if (producer) {
-        wait_vmcnt(PRE ? 0 : D * IPR);
+        wait_vmcnt(D * IPR);
         staged_dig_pin(xv);
         __builtin_amdgcn_sched_barrier(0);
         staged_dig_x<FMT>(xv, xact, X);
@@ -1624,8 +1611,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     __shared__ float part[kSdigMaxRows][8];
     __shared__ unsigned long long wkey[NW];
     __shared__ uint32_t wflag[NW];
-    sdig_run<FMT, NW, D, ARGMAX, RESID, false>(W, x, y, outer, nblk, rpc, parts, resid, epi, ring, digs,
-                                               part, wkey, wflag, [] {});
+    sdig_run<FMT, NW, D, ARGMAX, RESID>(W, x, y, outer, nblk, rpc, parts, resid, epi, ring, digs, part,
+                                        wkey, wflag);
 }
 
 // ------------------------------------------------------------------------

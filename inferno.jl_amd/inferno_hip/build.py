@@ -45,17 +45,38 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    LIBDIR.mkdir(exist_ok=True)
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(tmp),
-           *[str(s) for s in sources()]]
+OBJDIR = PKG / "_build"
+
+
+def _run(cmd, verbose: bool):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError(f"hipcc failed ({r.returncode})")
+
+
+def build(verbose: bool = False) -> Path:
+    """Every source compiled to an object in parallel (no relocatable device
+    code: each file's kernels are self-contained), then linked."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    LIBDIR.mkdir(exist_ok=True)
+    OBJDIR.mkdir(exist_ok=True)
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    objs = []
+    cmds = []
+    for src in sources():
+        obj = OBJDIR / (src.stem + ".o")
+        objs.append(obj)
+        cmds.append([HIPCC, *compile_flags, "-c", f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(obj), str(src)])
+    workers = max(1, min(len(cmds), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *FLAGS, "-o", str(tmp), *[str(o) for o in objs]], verbose)
     os.replace(tmp, LIB)
     return LIB
 
