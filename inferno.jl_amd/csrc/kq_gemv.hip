@@ -330,9 +330,11 @@ __device__ __forceinline__ void x_from_lds_dig(const uint32_t *pl, const float *
 }
 
 // Exact digit sums S0, S1 (unsigned planes) and S2 (signed) of one sub-block
-// -> 65536 * S2 + 256 * S1 + S0 in fp32.  |S2| <= 32 * 63 * 64 and
-// S0, S1 <= 32 * 63 * 255 for 6-bit weights, so 256 * S2 + S1 is an exact
-// fp32 integer (< 2^24) and the combine rounds once.
+// of the 4- or 5-bit weights of Q4_K / Q5_K -> 65536 * S2 + 256 * S1 + S0 in
+// fp32.  |S2| <= 32 * 31 * 64 and S0, S1 <= 32 * 31 * 255, so 256 * S2 + S1
+// (< 2^24) is an exact fp32 integer and the combine rounds once.  (Not for
+// 6-bit weights: there 256 * S2 can reach 2^25.  The Q6_K dot applies its
+// scales to each plane's integer sums and folds the planes in fp32 instead.)
 __device__ __forceinline__ float dig_combine(uint32_t s0, uint32_t s1, int s2)
 {
     return fmaf((float)(int)(((uint32_t)s2 << 8) + s1), 256.0f, (float)s0);
