@@ -18,6 +18,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 using namespace ihip;
 
@@ -90,6 +91,18 @@ uint64_t fingerprint(const void *p, size_t n)
 struct DevBuf {
     void *p = nullptr;
     size_t cap = 0;
+    void *hp = nullptr; // pinned host staging of the same buffer (hipHostMalloc, mapped)
+    void *hdp = nullptr; // the staging's device-side address (hipHostGetDevicePointer)
+    size_t hcap = 0;
+};
+
+// Host copies that wait for the library stream: y, h, logits ... come back
+// through a buffer's pinned staging and are copied to the caller's memory
+// once the stream has drained (finish_locked).
+struct PendingOut {
+    void *dst;
+    const void *src;
+    size_t bytes;
 };
 
 struct Ctx {
@@ -101,6 +114,7 @@ struct Ctx {
     std::unordered_map<const void *, uint64_t> by_host;
     uint64_t next_handle = 1;
     DevBuf x, y, h, t, src, nrm; // staging and scratch, grown on demand
+    std::vector<PendingOut> pending; // host copies after the next stream drain
     void *argmax_ws = nullptr; // IHIP_ARGMAX_WS_BYTES, left zeroed by the kernels
     int32_t *d_token = nullptr;
     uint32_t *d_flags = nullptr;
@@ -221,6 +235,7 @@ int init_locked(int device)
 int ready_locked()
 {
     Ctx &c = ctx();
+    c.pending.clear(); // a host call that failed half-way leaves no copies behind
     if (disabled())
         return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
     if (!c.ready)
@@ -402,10 +417,81 @@ int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, i
     return IHIP_OK;
 }
 
+// Transfers up to this size go through a buffer's pinned host staging (a
+// host memcpy plus a DMA copy: a pageable copy of a few KB costs several
+// times more); larger ones are copied from the caller's memory directly.
+constexpr size_t kStageMax = 1u << 20;
+
+int finish_locked();
+
+int ensure_pinned(DevBuf &b, size_t need)
+{
+    if (b.hcap >= need)
+        return IHIP_OK;
+    if (b.hp) {
+        // outputs already staged (possibly in this buffer) are delivered first
+        RET_IF(finish_locked());
+        HIPCHK(hipHostFree(b.hp));
+        b.hp = nullptr;
+        b.hcap = 0;
+    }
+    size_t cap = 4096;
+    while (cap < need)
+        cap *= 2;
+    HIPCHK(hipHostMalloc(&b.hp, cap, hipHostMallocMapped));
+    b.hcap = cap;
+    b.hdp = nullptr;
+    void *d = nullptr;
+    if (hipHostGetDevicePointer(&d, b.hp, 0) == hipSuccess)
+        b.hdp = d; // else: outputs come back through a DMA copy
+    else
+        (void)hipGetLastError();
+    return IHIP_OK;
+}
+
 int copy_in(DevBuf &b, const void *host, size_t bytes)
 {
     RET_IF(ensure(b, bytes));
-    HIPCHK(hipMemcpyAsync(b.p, host, bytes, hipMemcpyHostToDevice, ctx().stream));
+    if (bytes <= kStageMax) {
+        // the staging is reused: an earlier copy from it has completed, because
+        // every host entry point drains the stream before it returns
+        RET_IF(ensure_pinned(b, bytes));
+        memcpy(b.hp, host, bytes);
+        HIPCHK(hipMemcpyAsync(b.p, b.hp, bytes, hipMemcpyHostToDevice, ctx().stream));
+    } else {
+        HIPCHK(hipMemcpyAsync(b.p, host, bytes, hipMemcpyHostToDevice, ctx().stream));
+    }
+    return IHIP_OK;
+}
+
+// bytes of b (device) -> host, complete after finish_locked().  `off` is a
+// byte offset into b.
+int copy_out(DevBuf &b, void *host, size_t bytes, size_t off = 0)
+{
+    const uint8_t *dev = (const uint8_t *)b.p + off;
+    if (bytes <= kStageMax) {
+        RET_IF(ensure_pinned(b, off + bytes));
+        uint8_t *stage = (uint8_t *)b.hp + off;
+        HIPCHK(hipMemcpyAsync(stage, dev, bytes, hipMemcpyDeviceToHost, ctx().stream));
+        ctx().pending.push_back({host, stage, bytes});
+    } else {
+        HIPCHK(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, ctx().stream));
+    }
+    return IHIP_OK;
+}
+
+// Drain the library stream, then deliver the staged outputs.
+int finish_locked()
+{
+    Ctx &c = ctx();
+    const hipError_t e = hipStreamSynchronize(c.stream);
+    if (e != hipSuccess) {
+        c.pending.clear();
+        return fail(IHIP_ERR_HIP, "%s", hipGetErrorString(e));
+    }
+    for (const PendingOut &o : c.pending)
+        memcpy(o.dst, o.src, o.bytes);
+    c.pending.clear();
     return IHIP_OK;
 }
 
@@ -420,11 +506,22 @@ int host_gemv(int type, const uint8_t *w, const float *x, float *out, int inner,
     const void *dw = nullptr;
     RET_IF(resolve_locked(w, type, inner, outer, &dw));
     RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)inner));
-    RET_IF(ensure(c.y, sizeof(float) * (size_t)outer));
+    const size_t ybytes = sizeof(float) * (size_t)outer;
+    if (ybytes <= kStageMax) {
+        // the kernel stores y straight into the mapped pinned staging: no
+        // device-to-host copy behind it
+        RET_IF(ensure_pinned(c.y, ybytes));
+        if (c.y.hdp) {
+            RET_IF(gemv_dev_locked(type, dw, (const float *)c.x.p, (float *)c.y.hdp, inner, outer,
+                                   c.stream));
+            c.pending.push_back({out, c.y.hp, ybytes});
+            return finish_locked();
+        }
+    }
+    RET_IF(ensure(c.y, ybytes));
     RET_IF(gemv_dev_locked(type, dw, (const float *)c.x.p, (float *)c.y.p, inner, outer, c.stream));
-    HIPCHK(hipMemcpyAsync(out, c.y.p, sizeof(float) * (size_t)outer, hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+    RET_IF(copy_out(c.y, out, ybytes));
+    return finish_locked();
 }
 
 bool q8k_type(int t) { return t == kQ4_K || t == kQ5_K || t == kQ6_K; }
@@ -452,12 +549,10 @@ int host_gemv_q8k(int type, const uint8_t *w, const float *x, float *out, void *
         e = launch_gemv_q8k(type, dw, c.t.p, (float *)c.y.p, inner, outer, c.stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
-    HIPCHK(hipMemcpyAsync(out, c.y.p, sizeof(float) * (size_t)outer, hipMemcpyDeviceToHost,
-                          c.stream));
+    RET_IF(copy_out(c.y, out, sizeof(float) * (size_t)outer));
     if (q8_buf)
-        HIPCHK(hipMemcpyAsync(q8_buf, c.t.p, q8k_bytes(inner), hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+        RET_IF(copy_out(c.t, q8_buf, q8k_bytes(inner)));
+    return finish_locked();
 }
 
 int host_vec_dot_q8k(int type, const void *x, const void *y, int nb, float *s)
@@ -476,9 +571,8 @@ int host_vec_dot_q8k(int type, const void *x, const void *y, int nb, float *s)
     hipError_t e = launch_gemv_q8k(type, c.src.p, c.t.p, (float *)c.y.p, nb * 256, 1, c.stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "q8k dot launch failed: %s", hipGetErrorString(e));
-    HIPCHK(hipMemcpyAsync(s, c.y.p, sizeof(float), hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+    RET_IF(copy_out(c.y, s, sizeof(float)));
+    return finish_locked();
 }
 
 } // namespace
@@ -540,9 +634,15 @@ int ihip_shutdown(void)
     for (DevBuf *b : {&c.x, &c.y, &c.h, &c.t, &c.src, &c.nrm}) {
         if (b->p)
             (void)hipFree(b->p);
+        if (b->hp)
+            (void)hipHostFree(b->hp);
         b->p = nullptr;
         b->cap = 0;
+        b->hp = nullptr;
+        b->hdp = nullptr;
+        b->hcap = 0;
     }
+    c.pending.clear();
     (void)hipFree(c.argmax_ws);
     c.argmax_ws = nullptr;
     (void)hipStreamDestroy(c.stream);
@@ -674,9 +774,8 @@ int ihip_quantize_row_q8_k(const float *x, void *y, int64_t k)
     hipError_t e = launch_quantize_q8k((const float *)c.x.p, c.t.p, k, c.stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "quantize launch failed: %s", hipGetErrorString(e));
-    HIPCHK(hipMemcpyAsync(y, c.t.p, q8k_bytes(k), hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+    RET_IF(copy_out(c.t, y, q8k_bytes(k)));
+    return finish_locked();
 }
 
 int ihip_vec_dot_q4_k_q8_k(const void *x, const void *y, int nb, float *s)
@@ -732,9 +831,8 @@ int ihip_dequantize(int ggml_type, const uint8_t *src, float *dst, int64_t n)
     hipError_t e = launch_dequant(ggml_type, c.src.p, (float *)c.y.p, n, true, c.stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "dequant launch failed: %s", hipGetErrorString(e));
-    HIPCHK(hipMemcpyAsync(dst, c.y.p, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+    RET_IF(copy_out(c.y, dst, sizeof(float) * (size_t)n));
+    return finish_locked();
 }
 
 int ihip_ffn_swiglu(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
@@ -761,10 +859,9 @@ int ihip_ffn_swiglu(int gate_type, const uint8_t *wg, int up_type, const uint8_t
     RET_IF(gemv_dev_locked(down_type, dd, (const float *)c.h.p, (float *)c.y.p, inter, hidden,
                            c.stream));
     if (h)
-        HIPCHK(hipMemcpyAsync(h, c.h.p, sizeof(float) * (size_t)inter, hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipMemcpyAsync(y, c.y.p, sizeof(float) * (size_t)hidden, hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+        RET_IF(copy_out(c.h, h, sizeof(float) * (size_t)inter));
+    RET_IF(copy_out(c.y, y, sizeof(float) * (size_t)hidden));
+    return finish_locked();
 }
 
 int ihip_ffn_block(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
@@ -792,9 +889,8 @@ int ihip_ffn_block(int gate_type, const uint8_t *wg, int up_type, const uint8_t 
                               (float *)c.nrm.p));
     RET_IF(gemv_dev_locked(down_type, dd, (const float *)c.h.p, (float *)c.x.p, inter, hidden,
                            c.stream, (const float *)c.x.p));
-    HIPCHK(hipMemcpyAsync(x, c.x.p, sizeof(float) * (size_t)hidden, hipMemcpyDeviceToHost, c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+    RET_IF(copy_out(c.x, x, sizeof(float) * (size_t)hidden));
+    return finish_locked();
 }
 
 int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *logits,
@@ -820,10 +916,14 @@ int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *
     uint32_t fl = 0;
     HIPCHK(hipMemcpyAsync(&tok, c.d_token, 4, hipMemcpyDeviceToHost, c.stream));
     HIPCHK(hipMemcpyAsync(&fl, c.d_flags, 4, hipMemcpyDeviceToHost, c.stream));
-    if (logits)
-        HIPCHK(hipMemcpyAsync(logits, dlog, sizeof(float) * (size_t)vocab, hipMemcpyDeviceToHost,
-                              c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
+    if (logits) {
+        if (dlog == (float *)c.y.p)
+            RET_IF(copy_out(c.y, logits, sizeof(float) * (size_t)vocab));
+        else
+            HIPCHK(hipMemcpyAsync(logits, dlog, sizeof(float) * (size_t)vocab, hipMemcpyDeviceToHost,
+                                  c.stream));
+    }
+    RET_IF(finish_locked());
     if (fl & IHIP_FLAG_NAN)
         return fail(IHIP_ERR_NONFINITE, "logits must not contain NaN");
     if (fl & IHIP_FLAG_POSINF)
@@ -851,10 +951,8 @@ int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inn
                                       outer, c.stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
-    HIPCHK(hipMemcpyAsync(Y, c.y.p, sizeof(float) * (size_t)T * outer, hipMemcpyDeviceToHost,
-                          c.stream));
-    HIPCHK(hipStreamSynchronize(c.stream));
-    return IHIP_OK;
+    RET_IF(copy_out(c.y, Y, sizeof(float) * (size_t)T * outer));
+    return finish_locked();
 }
 
 // ---- device-pointer entry points ----------------------------------------
