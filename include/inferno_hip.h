@@ -88,17 +88,6 @@ int ihip_available(void);
 int ihip_init(int device);
 /* Free every cached weight and buffer. */
 int ihip_shutdown(void);
-/* Performance knobs; every setting stays within the parity bound, 0 restores
- * the measured default.  Q4_K/Q5_K: "rows_wide" / "rows_gateup" (rows per
- * wave, 1, 2, 4), "wide_waves" (4 or 8 waves per workgroup), "wide_persist"
- * (1 always / -1 never use the persistent kernel), "pers_bufs" (its register
- * buffers, 2..4), "wide_fp32" (1: fp32 activations instead of the default
- * integer digits).  Q6_K/Q8_0/IQ4_NL: "sdig_rows" (rows per chunk, 1..64),
- * "sdig_depth" (LDS ring slots per wave, 2, 4 or 6), "sdig_wg_per_cu", "sdig_waves" (6, 8,
- * 12, 16), "sdig_off" (1: the fp32-activation streamed kernel, whose
- * "stream_rows" and "stream_wg_per_cu" then apply).  Argmax: "argmax_threads"
- * (64, 256 or 1024 threads in the kernel that reduces the partials). */
-int ihip_set_tuning(const char *name, int value);
 
 /* ---- weight registry (host entry points use it implicitly) ------------ */
 /* Upload `bytes` of GGML blocks once; *handle names the device copy. */

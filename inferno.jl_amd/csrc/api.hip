@@ -386,7 +386,7 @@ int gate_up_dev_locked(int gt, const void *wg, int ut, const void *wu, const flo
 // buffer needed).
 bool lm_head_fused(int type, const void *w, const float *x, int hidden, int vocab)
 {
-    return (type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden) && lm_head_fusable(vocab);
+    return (type == kQ6_K || type == kQ8_0) && fast_ok(type, w, x, hidden) && lm_head_fusable(type, hidden);
 }
 
 int lm_head_parts(int type, const void *w, const float *x, int hidden, int vocab)
@@ -649,16 +649,6 @@ int ihip_shutdown(void)
     c.stream = nullptr;
     c.ready = false;
     c.device = -1;
-    return IHIP_OK;
-}
-
-int ihip_set_tuning(const char *name, int value)
-{
-    if (!name)
-        return fail(IHIP_ERR_INVALID, "null name");
-    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
-    set_tuning(name, value);
-    set_prefill_tuning(name, value);
     return IHIP_OK;
 }
 

@@ -1,29 +1,31 @@
-// kq_gemv.hip -- gfx950 dequant-fused GEMV kernels for GGML K-quant/Q8_0
-// weights and fp32 activations: y[r] = sum_c W[r,c] x[c].
+// kq_gemv.hip -- gfx950 dequant-fused GEMV kernels for GGML K-quant, Q8_0
+// and IQ4_NL weights and fp32 activations: y[r] = sum_c W[r,c] x[c].
 //
 // Semantics: the fp32-activation path of Inferno.jl's mul_quant_mat_vec
-// (src/ModelCPU.jl:285-379) with the weights of src/Dequant.jl:304-601.
-// Activations stay fp32 (the reference C path's int8 re-quantization of x,
-// src/kernels/quant_kernels.c:166-194, is not used: it breaks the
-// 1e-4*||w_row||*||x|| bound).
+// (src/ModelCPU.jl:285-379) with the weights of src/Dequant.jl:304-601, to
+// the 1e-4 * ||w_row|| * ||x|| row bound.  (The reference C path's int8
+// re-quantization of x, src/kernels/quant_kernels.c:166-194, is the separate
+// bit-exact variant in kq_q8k.hip.)
 //
 // A decode GEMV is a single pass over the weight bytes, so every kernel here
-// is built to put all of a wave's weight loads in flight before it waits on
-// any of them, to reuse each lane's x registers over several rows, and to
-// keep the per-weight ALU work at one byte convert plus one FMA (the
-// `dmin*m` term of Q4_K/Q5_K and the -32 offset of Q6_K are folded into
-// per-sub-block sums of x, which all rows share).
+// puts all of a wave's weight loads in flight before it waits on any of them
+// and reuses each lane's activations over many rows.  x enters as 22-bit
+// fixed-point integers per 32 values, split into three byte digits, so the
+// weight products run on the integer dot units (v_dot4, exact sums; the
+// representation and its error bound are described at XDig below), and the
+// `dmin*m` term of Q4_K/Q5_K and the weight offsets of Q6_K / Q8_0 / IQ4_NL
+// are taken off through per-sub-block sums of x that all rows share.
 //
-//   * Q4_K / Q5_K ("wide" kernels): blocks are 16-byte multiples, so lanes
-//     load straight from HBM with 128-bit loads.  A wave covers 16 blocks
-//     (4096 columns) of R rows per pass: lane = (block, sub-block pair), 64
-//     weights per lane per row.
-//   * Q6_K (210 B) and Q8_0 (34 B) blocks are not 16-byte aligned, but 8 of
-//     them are (1680 B / 272 B).  Each wave copies its own rows into a
-//     private LDS region with gfx950's direct-to-LDS 128-bit loads (no
-//     registers, no workgroup barrier), every segment of the row in flight
-//     at once, then re-slices blocks from LDS ("staged" kernels).
-//   * Greedy argmax (lm_head) is fused into the staged kernel's epilogue:
+//   * Q4_K / Q5_K ("wide" kernels, k_gemv_kwide / k_gemv_kpers): blocks are
+//     16-byte multiples, so lanes load straight from HBM with 128-bit loads.
+//     A wave covers 16 blocks (4096 columns) of R rows per pass: lane =
+//     (block, sub-block pair), 64 weights per lane per row.
+//   * Q6_K (210 B), Q8_0 (34 B) and IQ4_NL (18 B) blocks are not 16-byte
+//     aligned, but 8 of them are.  k_gemv_sdig streams each wave's rows
+//     through a private LDS ring filled by gfx950's direct-to-LDS 128-bit
+//     copies (no registers, no workgroup barrier), then re-slices blocks
+//     from LDS.
+//   * Greedy argmax (lm_head) is fused into the streamed kernel's epilogue:
 //     each workgroup writes one (value, index) partial to its own slot and a
 //     one-workgroup kernel reduces the partials, so no two workgroups touch
 //     the same address.
@@ -56,45 +58,15 @@ struct KFmt<kQ5_K> {
 // 64j + 32 + l (sub-block 2j+1), l = 0..31 (src/Dequant.jl:364-371).
 //
 // The weight bytes go straight to registers (three 128-bit loads per row and
-// lane).  x is read once per workgroup with contiguous loads and kept in LDS
-// in a padded layout (4 floats of padding after every 64) under which a
-// lane's 16-byte reads hit distinct banks across the wave; the workgroup also
-// leaves the sum of every 32-element sub-block of x there.  Loads are issued
-// x first, then every row's weights, so x can be staged while the weights are
-// still in flight, and each row is reduced as soon as its own bytes land.
-struct XWide {
-    float a[32], b[32];
-    float sa, sb;
-};
+// lane).  x is read once per workgroup with contiguous loads and staged in LDS
+// as integer digits (below), with the sum of every 32-element sub-block of x.
+// Loads are issued x first, then every row's weights, so x can be staged while
+// the weights are still in flight, and each row is reduced as soon as its own
+// bytes land.
 
-constexpr int kXPadFloats = 4096 + 4096 / 64 * 4;
 // float4s of a 4096-element pass per thread of an NT-thread workgroup (768
 // threads: two, the second only for threads below 256)
 __host__ __device__ constexpr int xnv(int nt) { return (1024 + nt - 1) / nt; }
-__device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
-
-// Stage x[col0, col0 + 4096) (zeros past `inner`) and its 128 sub-block sums.
-// `xv` holds this thread's float4s of x (NT threads: 1024 / NT each), loaded
-// by the caller.
-template <int NT>
-__device__ __forceinline__ void x_stage(float *xs, float *xsum, const float4 (&xv)[1024 / NT])
-{
-    static_assert(1024 % NT == 0, "fp32 staging: NT divides 1024");
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < 1024 / NT; ++k) {
-        const int i = 4 * (tid + NT * k);
-        *reinterpret_cast<float4 *>(xs + xpad(i)) = xv[k];
-        // 8 consecutive threads hold one 32-element sub-block
-        float t = (xv[k].x + xv[k].y) + (xv[k].z + xv[k].w);
-        t = dpp_add<0xb1, 0xf>(t);  // pairs
-        t = dpp_add<0x4e, 0xf>(t);  // quads
-        t = dpp_add<0x141, 0xf>(t); // 8 lanes (row_half_mirror)
-        if ((tid & 7) == 0)
-            xsum[(tid + NT * k) >> 3] = t;
-    }
-}
-
 template <int NT>
 __device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col0, int inner,
                                             float4 (&xv)[xnv(NT)])
@@ -106,22 +78,6 @@ __device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col
         xv[k] = (f < 1024 && col < inner) ? *reinterpret_cast<const float4 *>(x + col)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-}
-
-__device__ __forceinline__ void x_from_lds(const float *xs, const float *xsum, int b, int j,
-                                           XWide &X)
-{
-    const int base = 256 * b + 64 * j;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const float4 va = *reinterpret_cast<const float4 *>(xs + xpad(base + 4 * t));
-        const float4 vb = *reinterpret_cast<const float4 *>(xs + xpad(base + 32 + 4 * t));
-        X.a[4 * t + 0] = va.x; X.a[4 * t + 1] = va.y; X.a[4 * t + 2] = va.z; X.a[4 * t + 3] = va.w;
-        X.b[4 * t + 0] = vb.x; X.b[4 * t + 1] = vb.y; X.b[4 * t + 2] = vb.z; X.b[4 * t + 3] = vb.w;
-    }
-    const float2 s2 = *reinterpret_cast<const float2 *>(xsum + 8 * b + 2 * j);
-    X.sa = s2.x;
-    X.sb = s2.y;
 }
 
 // The block bytes one lane needs for one row: header (d, dmin, scales), its
@@ -141,73 +97,6 @@ __device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int
         B.e0 = *reinterpret_cast<const uint4 *>(blk + 16);
         B.e1 = *reinterpret_cast<const uint4 *>(blk + 32);
     }
-}
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// One lane's contribution to one row.
-//
-// Q4_K converts nibbles with v_cvt_pk_f32_fp8, two per instruction: a byte
-// 0000qqqq is the OCP e4m3 encoding of q * 2^-9 exactly (q3 becomes the
-// exponent's low bit, q2..q0 the mantissa; 0..7 are e4m3 subnormals, which
-// gfx950 converts exactly), so the sums are formed in units of 2^-9 and the
-// exact power-of-two factor 512 is applied once per sub-block.  Q5_K's 5-bit
-// values are not linear in e4m3 and use v_cvt_f32_ubyte.
-template <int FMT>
-__device__ __forceinline__ float kwide_dot(const KBytes &B, int j, const XWide &X)
-{
-    const uint32_t qw[8] = {B.q0.x, B.q0.y, B.q0.z, B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w};
-    float sa0 = 0.0f, sa1 = 0.0f, sb0 = 0.0f, sb1 = 0.0f;
-    if constexpr (FMT == kQ4_K) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t lo = qw[t] & 0x0f0f0f0fu;
-            const uint32_t hi = (qw[t] >> 4) & 0x0f0f0f0fu;
-            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-            const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-            const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-            sa0 = fmaf(l01[0], X.a[4 * t + 0], sa0);
-            sa1 = fmaf(l01[1], X.a[4 * t + 1], sa1);
-            sa0 = fmaf(l23[0], X.a[4 * t + 2], sa0);
-            sa1 = fmaf(l23[1], X.a[4 * t + 3], sa1);
-            sb0 = fmaf(h01[0], X.b[4 * t + 0], sb0);
-            sb1 = fmaf(h01[1], X.b[4 * t + 1], sb1);
-            sb0 = fmaf(h23[0], X.b[4 * t + 2], sb0);
-            sb1 = fmaf(h23[1], X.b[4 * t + 3], sb1);
-        }
-        sa0 = (sa0 + sa1) * 512.0f;
-        sb0 = (sb0 + sb1) * 512.0f;
-    } else {
-        // qh[l] bit 2j lifts element 64j + l, bit 2j+1 element 64j + 32 + l;
-        // shift both bits down to bit positions 0 and 1 of each byte once
-        const uint32_t sh = 2 * j;
-        const uint32_t ew[8] = {B.e0.x >> sh, B.e0.y >> sh, B.e0.z >> sh, B.e0.w >> sh,
-                                B.e1.x >> sh, B.e1.y >> sh, B.e1.z >> sh, B.e1.w >> sh};
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            uint32_t lo = (qw[t] & 0x0f0f0f0fu) | ((ew[t] & 0x01010101u) << 4);
-            uint32_t hi = ((qw[t] >> 4) & 0x0f0f0f0fu) | ((ew[t] & 0x02020202u) << 3);
-            lo = opaque(lo);
-            hi = opaque(hi);
-            sa0 = fmaf(ubyte_f(lo, 0), X.a[4 * t + 0], sa0);
-            sa1 = fmaf(ubyte_f(lo, 1), X.a[4 * t + 1], sa1);
-            sa0 = fmaf(ubyte_f(lo, 2), X.a[4 * t + 2], sa0);
-            sa1 = fmaf(ubyte_f(lo, 3), X.a[4 * t + 3], sa1);
-            sb0 = fmaf(ubyte_f(hi, 0), X.b[4 * t + 0], sb0);
-            sb1 = fmaf(ubyte_f(hi, 1), X.b[4 * t + 1], sb1);
-            sb0 = fmaf(ubyte_f(hi, 2), X.b[4 * t + 2], sb0);
-            sb1 = fmaf(ubyte_f(hi, 3), X.b[4 * t + 3], sb1);
-        }
-        sa0 += sa1;
-        sb0 += sb1;
-    }
-    const float d = h2f(B.h.x & 0xffffu), dmin = h2f(B.h.x >> 16);
-    float scA, mA, scB, mB;
-    k_scale_min_pair(B.h.y, B.h.z, B.h.w, j, scA, mA, scB, mB);
-    const float pos = fmaf(scA, sa0, scB * sb0);
-    const float neg = fmaf(mA, X.sa, mB * X.sb);
-    return fmaf(d, pos, -(dmin * neg));
 }
 
 // ---- integer-digit activations -------------------------------------------
@@ -340,8 +229,10 @@ __device__ __forceinline__ float dig_combine(uint32_t s0, uint32_t s1, int s2)
     return fmaf((float)(int)(((uint32_t)s2 << 8) + s1), 256.0f, (float)s0);
 }
 
-// One lane's contribution to one row with digit activations: the same sum as
-// kwide_dot.
+// One lane's contribution to one row: its two sub-blocks (2j, 2j + 1) of
+// block b, d * (sc_A * sum_A + sc_B * sum_B) - dmin * (m_A * xsum_A + m_B *
+// xsum_B) (src/Dequant.jl:364-371), the weight sums formed exactly on the
+// integer dot units.
 template <int FMT>
 __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
 {
@@ -392,7 +283,7 @@ __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
 //     1/sqrt(mean(x^2) + eps) at the end, so the norm costs no extra pass.
 //   plain: y[r] = resid[r] + (W x)[r], the residual add of
 //     src/ModelCPU.jl:913-920 (resid may be y itself).
-template <int FMT, int R, bool GATEUP, bool DIG, bool EXT, int NWV>
+template <int FMT, int R, bool GATEUP, bool EXT, int NWV>
 __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restrict__ W,
                                                     const uint8_t *__restrict__ W2,
                                                     const float *__restrict__ x,
@@ -404,12 +295,10 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
     constexpr int NW = GATEUP ? 2 : 1;
     constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
     constexpr int NT = NWV * 64, NXV = xnv(NT);
-    static_assert(DIG || 1024 % NT == 0, "fp32 staging: NT divides 1024");
-    // fp32 x (kXPadFloats) or its three digit planes (3 * kDigPlaneDw dwords)
-    __shared__ __attribute__((aligned(16))) uint32_t xbuf[DIG ? 3 * kDigPlaneDw : kXPadFloats];
+    // x's three digit planes, its sub-block sums and exponents
+    __shared__ __attribute__((aligned(16))) uint32_t xbuf[3 * kDigPlaneDw];
     __shared__ __attribute__((aligned(16))) float xsum[128];
-    __shared__ __attribute__((aligned(8))) int xexp[DIG ? 128 : 1];
-    float *xs = reinterpret_cast<float *>(xbuf);
+    __shared__ __attribute__((aligned(8))) int xexp[128];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
@@ -467,34 +356,20 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
         __builtin_amdgcn_sched_barrier(0);
         if (pass > 0)
             __syncthreads(); // the previous pass is done with xs / xsum
-        if constexpr (DIG) {
-            x_stage_dig<NT>(xbuf, xsum, xexp, xv);
-            __syncthreads();
-            XDig X;
-            x_from_lds_dig(xbuf, xsum, xexp, b, j, X);
-            // rows one after the other, in load order: row r is reduced as soon as
-            // its own bytes have landed instead of after every row's
+        x_stage_dig<NT>(xbuf, xsum, xexp, xv);
+        __syncthreads();
+        XDig X;
+        x_from_lds_dig(xbuf, xsum, xexp, b, j, X);
+        // rows one after the other, in load order: row r is reduced as soon as
+        // its own bytes have landed instead of after every row's
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int m = 0; m < NW; ++m) {
-                    const float c = kdig_dot<FMT>(B[m][r], j, X);
-                    acc[m][r] += active ? c : 0.0f;
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-        } else {
-            x_stage<NT>(xs, xsum, xv);
-            __syncthreads();
-            XWide X;
-            x_from_lds(xs, xsum, b, j, X);
-#pragma unroll
-            for (int m = 0; m < NW; ++m)
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float c = kwide_dot<FMT>(B[m][r], j, X);
-                    acc[m][r] += active ? c : 0.0f;
-                }
-        }
+            for (int m = 0; m < NW; ++m) {
+                const float c = kdig_dot<FMT>(B[m][r], j, X);
+                acc[m][r] += active ? c : 0.0f;
+                __builtin_amdgcn_sched_barrier(0);
+            }
     }
     float scale = 1.0f;
     if constexpr (NORM) { // every wave takes part in the barrier
@@ -533,7 +408,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
 // NB - 1 groups are in flight while a group is reduced (HBM latency under
 // load is a microsecond or more, several group reductions).  A group is R
 // rows (GATEUP: R gate rows and the same R up rows).  Same outputs as
-// k_gemv_kwide<FMT, R, GATEUP, true, EXT, NWV>.
+// k_gemv_kwide<FMT, R, GATEUP, EXT, NWV>.
 // The walk itself over LDS the caller declares (xbuf: 3 * kDigPlaneDw
 // dwords, xsum / xexp: 128 each, ssw: NWV floats).
 template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB>
@@ -674,11 +549,11 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
 }
 
 // ------------------------------------------------------------------------
-// Staged kernels (Q6_K, Q8_0)
+// Streamed kernels (Q6_K, Q8_0, IQ4_NL)
 // ------------------------------------------------------------------------
-// A segment is 8 Q6_K blocks (2048 columns, 1680 B) or 64 Q8_0 blocks (2048
-// columns, 2176 B); rows of a whole number of 8-block groups are 16-byte
-// aligned, which the host checks before choosing these kernels.
+// A segment is 8 Q6_K blocks (2048 columns, 1680 B), 64 Q8_0 blocks (2176 B)
+// or 64 IQ4_NL blocks (1152 B); rows of a whole number of 8-block groups are
+// 16-byte aligned, which the host checks before choosing these kernels.
 template <int FMT>
 struct SFmt;
 template <>
@@ -693,154 +568,16 @@ template <>
 struct SFmt<kIQ4_NL> {
     static constexpr int SEG_BLOCKS = 64, SEG_BYTES = 64 * 18;
 };
-__host__ __device__ constexpr int SFmtSegBlocks(int fmt)
-{
-    return fmt == kQ6_K ? SFmt<kQ6_K>::SEG_BLOCKS : fmt == kQ8_0 ? SFmt<kQ8_0>::SEG_BLOCKS
-         : SFmt<kIQ4_NL>::SEG_BLOCKS;
-}
 static_assert(SFmt<kQ6_K>::SEG_BYTES % 16 == 0, "Q6_K segment must be 16-byte aligned");
 static_assert(SFmt<kQ8_0>::SEG_BYTES % 16 == 0, "Q8_0 segment must be 16-byte aligned");
 static_assert(SFmt<kIQ4_NL>::SEG_BYTES % 16 == 0, "IQ4_NL segment must be 16-byte aligned");
 
-// Q6_K lane geometry: block bs = lane>>3; unit u = lane&7: half n = u>>2,
-// positions l0 = 8*(u&3) .. +7.  Group g (0..3) of the unit holds the
-// elements 128n + 32g + l0 + i (src/Dequant.jl:584-597): g=0 low nibble of
-// ql[64n+l0+i], g=1 low nibble of ql[64n+32+l0+i], g=2/3 the high nibbles,
-// with qh[32n+l0+i] bits 2g..2g+1 on top and scale sc[8n + 2g + (l0>>4)].
-// Q8_0 and IQ4_NL lane geometry: lane = block of the 64-block segment, 32
-// weights (IQ4_NL also keeps the sum of its 32 x values).
-template <int FMT>
-struct SX;
-template <>
-struct SX<kQ6_K> {
-    float x[4][8];
-    float s[4];
-};
-template <>
-struct SX<kQ8_0> {
-    float x[32];
-};
-template <>
-struct SX<kIQ4_NL> {
-    float x[32];
-    float s;
-};
-
-// All loads first, then the selects and sums, so that the loads are in
-// flight together.
-template <int FMT>
-__device__ __forceinline__ void staged_load_x(const float *__restrict__ xseg, int lane,
-                                              int seg_blocks, SX<FMT> &X)
-{
-    float4 v[8];
-    bool active;
-    if constexpr (FMT == kQ6_K) {
-        const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-        active = bs < seg_blocks;
-        const float *base = xseg + (active ? 256 * bs + 128 * n + l0 : 0);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4 *p = reinterpret_cast<const float4 *>(base + 32 * g);
-            v[2 * g] = p[0];
-            v[2 * g + 1] = p[1];
-        }
-    } else {
-        active = lane < seg_blocks;
-        const float4 *p = reinterpret_cast<const float4 *>(xseg + (active ? 32 * lane : 0));
-#pragma unroll
-        for (int t = 0; t < 8; ++t) v[t] = p[t];
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-        if (!active) v[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (FMT == kQ6_K) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4 a = v[2 * g], b = v[2 * g + 1];
-            X.x[g][0] = a.x; X.x[g][1] = a.y; X.x[g][2] = a.z; X.x[g][3] = a.w;
-            X.x[g][4] = b.x; X.x[g][5] = b.y; X.x[g][6] = b.z; X.x[g][7] = b.w;
-            X.s[g] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-        }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            X.x[4 * t] = v[t].x; X.x[4 * t + 1] = v[t].y;
-            X.x[4 * t + 2] = v[t].z; X.x[4 * t + 3] = v[t].w;
-        }
-        if constexpr (FMT == kIQ4_NL) {
-            float a = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-                a += (v[t].x + v[t].y) + (v[t].z + v[t].w);
-            X.s = a;
-        }
-    }
-}
-
-// `tile` is the 16-byte-aligned LDS array, `bo` the block's byte offset in it.
-__device__ __forceinline__ float q6_dot(const uint8_t *tile, uint32_t bo, int n, int l0,
-                                        const SX<kQ6_K> &X)
-{
-    uint32_t A[2], B[2], H[2], S[2];
-    lds_read8_even(tile, bo + 64 * n + l0, A[0], A[1]);
-    lds_read8_even(tile, bo + 64 * n + 32 + l0, B[0], B[1]);
-    lds_read8_even(tile, bo + 128 + 32 * n + l0, H[0], H[1]);
-    lds_read8_even(tile, bo + 192 + 8 * n, S[0], S[1]);
-    const float d = h2f(lds_read_u16(tile, bo + 208));
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const uint32_t v[4] = {
-            (A[t] & 0x0f0f0f0fu) | ((H[t] & 0x03030303u) << 4),
-            (B[t] & 0x0f0f0f0fu) | ((H[t] & 0x0c0c0c0cu) << 2),
-            ((A[t] >> 4) & 0x0f0f0f0fu) | (H[t] & 0x30303030u),
-            ((B[t] >> 4) & 0x0f0f0f0fu) | ((H[t] >> 2) & 0x30303030u),
-        };
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                acc[g] = fmaf(ubyte_f(v[g], b), X.x[g][4 * t + b], acc[g]);
-    }
-    const int c = l0 >> 4;
-    float r = 0.0f;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int si = 2 * g + c; // byte of the 8 scales sc[8n..8n+7]
-        const float ds = d * sbyte_f(S[si >> 2], si & 3);
-        r = fmaf(ds, fmaf(-32.0f, X.s[g], acc[g]), r);
-    }
-    return r;
-}
-
-// Q8_0 block at byte `off` of the 16-byte-aligned LDS row `row_lds`.
-__device__ __forceinline__ float q80_dot(const uint8_t *row_lds, uint32_t off, const float *xr)
-{
-    const float d = h2f(lds_read_u16(row_lds, off));
-    const uint32_t o = off + 2;
-    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
-    const uint32_t sh = o & 3u;
-    uint32_t w[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) w[i] = p[i];
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh);
-        a0 = fmaf(sbyte_f(q, 0), xr[4 * t + 0], a0);
-        a1 = fmaf(sbyte_f(q, 1), xr[4 * t + 1], a1);
-        a0 = fmaf(sbyte_f(q, 2), xr[4 * t + 2], a0);
-        a1 = fmaf(sbyte_f(q, 3), xr[4 * t + 3], a1);
-    }
-    return d * (a0 + a1);
-}
-
-// IQ4_NL block at byte `off` of the 16-byte-aligned LDS row `row_lds`
-// (src/Dequant.jl:683-693: element j = low nibble of qs[j], element j + 16 =
-// high nibble; weight = d * grid[nibble], grid src/QuantsData.jl:384).  The
-// grid, biased by +128 to unsigned bytes, is looked up four nibbles at a time
-// with byte permutes (grid[0..7] and grid[8..15], then a choice by the
-// nibble's bit 3); the bias comes back off through the lane's x sum.
+// IQ4_NL weights (src/Dequant.jl:683-693: element j = low nibble of qs[j],
+// element j + 16 = high nibble; weight = d * grid[nibble], grid
+// src/QuantsData.jl:384).  The grid, biased by +128 to unsigned bytes, is
+// looked up four nibbles at a time with byte permutes (grid[0..7] and
+// grid[8..15], then a choice by the nibble's bit 3); the bias comes back off
+// exactly in the integer sums (iq4nl_dot_dig).
 constexpr uint32_t kIQ4G0 = 0x3F2D1801u; // grid + 128: 1, 24, 45, 63
 constexpr uint32_t kIQ4G1 = 0x766A5D4Fu; // 79, 93, 106, 118
 constexpr uint32_t kIQ4G2 = 0xA6998D81u; // 129, 141, 153, 166
@@ -853,34 +590,6 @@ __device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t nib) // four nibbles i
     const uint32_t hi = __builtin_amdgcn_perm(kIQ4G3, kIQ4G2, n7);
     const uint32_t pick = 0x03020100u + ((nib & 0x08080808u) >> 1); // byte i of lo or of hi
     return __builtin_amdgcn_perm(hi, lo, pick);
-}
-
-__device__ __forceinline__ float iq4nl_dot(const uint8_t *row_lds, uint32_t off,
-                                           const SX<kIQ4_NL> &X)
-{
-    const float d = h2f(lds_read_u16(row_lds, off));
-    const uint32_t o = off + 2;
-    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
-    const uint32_t sh = o & 3u;
-    uint32_t w[5];
-#pragma unroll
-    for (int i = 0; i < 5; ++i) w[i] = p[i];
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh); // qs[4t..4t+3]
-        const uint32_t vl = opaque(iq4nl_lookup(q & 0x0f0f0f0fu));         // elements 4t + b
-        const uint32_t vh = opaque(iq4nl_lookup((q >> 4) & 0x0f0f0f0fu));  // elements 16 + 4t + b
-        a0 = fmaf(ubyte_f(vl, 0), X.x[4 * t + 0], a0);
-        a1 = fmaf(ubyte_f(vl, 1), X.x[4 * t + 1], a1);
-        a0 = fmaf(ubyte_f(vl, 2), X.x[4 * t + 2], a0);
-        a1 = fmaf(ubyte_f(vl, 3), X.x[4 * t + 3], a1);
-        a0 = fmaf(ubyte_f(vh, 0), X.x[16 + 4 * t + 0], a0);
-        a1 = fmaf(ubyte_f(vh, 1), X.x[16 + 4 * t + 1], a1);
-        a0 = fmaf(ubyte_f(vh, 2), X.x[16 + 4 * t + 2], a0);
-        a1 = fmaf(ubyte_f(vh, 3), X.x[16 + 4 * t + 3], a1);
-    }
-    return d * fmaf(-128.0f, X.s, a0 + a1);
 }
 
 // ---- greedy argmax partials ----------------------------------------------
@@ -959,16 +668,14 @@ __device__ __forceinline__ void argmax_store_partial(unsigned long long key, uin
     }
 }
 
-// Reduce `nparts` partials with NT threads, U 16-byte partials in flight per
-// thread; writes the 0-based token and the IHIP_FLAG_* bits.  With NT = 64
-// there is no LDS exchange and no barrier; NT = 256 (four partials per thread
-// for the lm_head's ~1000) is the default.
-template <int NT>
-__global__ __launch_bounds__(NT) void k_argmax_finalize(const ArgPart *__restrict__ parts,
-                                                        int nparts, int32_t *token,
-                                                        uint32_t *flags_out)
+// Reduce `nparts` partials with 256 threads, up to 16 16-byte partials in
+// flight per thread (the lm_head leaves three per thread); writes the 0-based
+// token and the IHIP_FLAG_* bits.
+__global__ __launch_bounds__(256) void k_argmax_finalize(const ArgPart *__restrict__ parts,
+                                                         int nparts, int32_t *token,
+                                                         uint32_t *flags_out)
 {
-    constexpr int NWV = NT / 64, U = NT >= 1024 ? 4 : 16;
+    constexpr int NT = 256, NWV = NT / 64, U = 16;
     unsigned long long key = 0;
     uint32_t fl = 0;
     for (int i0 = threadIdx.x; i0 < nparts; i0 += U * NT) {
@@ -986,20 +693,18 @@ __global__ __launch_bounds__(NT) void k_argmax_finalize(const ArgPart *__restric
         }
     }
     argmax_wave_reduce(key, fl);
-    if constexpr (NWV > 1) {
-        __shared__ unsigned long long wkey[NWV];
-        __shared__ uint32_t wflag[NWV];
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        if (lane == 0) {
-            wkey[wave] = key;
-            wflag[wave] = fl;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            for (int w = 1; w < NWV; ++w) {
-                key = wkey[w] > key ? wkey[w] : key;
-                fl |= wflag[w];
-            }
+    __shared__ unsigned long long wkey[NWV];
+    __shared__ uint32_t wflag[NWV];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        wkey[wave] = key;
+        wflag[wave] = fl;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < NWV; ++w) {
+            key = wkey[w] > key ? wkey[w] : key;
+            fl |= wflag[w];
         }
     }
     if (threadIdx.x == 0) {
@@ -1024,141 +729,6 @@ __global__ __launch_bounds__(256) void k_argmax_partials(const float *__restrict
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
         argmax_fold(v[i], (uint32_t)i, key, fl);
     argmax_store_partial(key, fl, parts + blockIdx.x);
-}
-
-// ---- the streamed staged GEMV --------------------------------------------
-// Workgroup = NW waves; wave w owns K segments w, w + NW, ... so the x slice
-// of its segment stays in registers while it streams the workgroup's rows
-// through a D-slot LDS ring filled by direct-to-LDS 128-bit loads: the copy
-// of row i + D is issued as soon as row i has been reduced, so D rows per
-// wave are always in flight.  Per-row partial sums meet in LDS and the
-// workgroup's threads finish the rows (and, ARGMAX, fold them into one
-// partial per workgroup).  Workgroups walk chunks of `rpc` rows grid-stride.
-
-constexpr int kStreamMaxRows = 64; // rows per chunk (one partial slot per row and wave)
-static_assert(kStreamMaxRows <= 64, "the epilogue gives every row its own thread");
-
-template <int FMT, int NW, int D, bool ARGMAX>
-__global__ __launch_bounds__(NW * 64) void k_gemv_stream(const uint8_t *__restrict__ W,
-                                                         const float *__restrict__ x,
-                                                         float *y, int outer,
-                                                         int nblk, int rpc,
-                                                         ArgPart *__restrict__ parts,
-                                                         const float *resid, int epi)
-{
-    using F = SFmt<FMT>;
-    constexpr int SLOT = F::SEG_BYTES + 16; // Q8_0 reads one dword past a segment
-    __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * SLOT];
-    __shared__ float part[kStreamMaxRows][NW];
-    __shared__ unsigned long long wkey[NW];
-    __shared__ uint32_t wflag[NW];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
-    const int bb = block_bytes(FMT);
-    const size_t row_bytes = (size_t)nblk * bb;
-    const int nseg = (nblk + F::SEG_BLOCKS - 1) / F::SEG_BLOCKS;
-    const int nchunks = (outer + rpc - 1) / rpc;
-    const uint32_t my_ring = (uint32_t)(w * D * SLOT);
-
-    unsigned long long key = 0;
-    uint32_t fl = 0;
-    SX<FMT> X;
-    int x_seg = -1; // segment whose x slice X holds
-
-    for (int chunk = blockIdx.x; chunk < nchunks; chunk += gridDim.x) {
-        const int row0 = chunk * rpc;
-        const int nrows = min(rpc, outer - row0);
-        // the residual of this thread's row (the epilogue below has one row
-        // per thread) is loaded now, under the weight stream; the segment
-        // loop's first s_waitcnt(0) completes it before the copy waits start
-        const float rv = (resid && tid < nrows) ? resid[row0 + tid] : 0.0f;
-        for (int i = tid; i < kStreamMaxRows * NW; i += NW * 64)
-            (&part[0][0])[i] = 0.0f;
-        __syncthreads();
-        for (int sg = w; sg < nseg; sg += NW) { // wave-uniform
-            const int seg_blocks = min(F::SEG_BLOCKS, nblk - sg * F::SEG_BLOCKS);
-            // whole 8-block groups (checked on the host): a multiple of 16 bytes
-            const int chunks16 = seg_blocks * bb / 16;
-            const int ipr = (chunks16 + 63) >> 6; // copy instructions per row
-            const uint8_t *src0 = W + (size_t)row0 * row_bytes + (size_t)sg * F::SEG_BYTES;
-            auto issue = [&](int i) {
-                const uint8_t *src = src0 + (size_t)i * row_bytes;
-                uint8_t *dst = ring + my_ring + (i % D) * SLOT;
-                for (int c0 = 0; c0 < chunks16; c0 += 64) {
-                    const int c = c0 + lane;
-                    if (c < chunks16)
-                        __builtin_amdgcn_global_load_lds(
-                            (const void *)(src + 16 * (size_t)c),
-                            (__attribute__((address_space(3))) void *)(dst + 16 * c0), 16, 0, 0);
-                }
-            };
-            const int pre = min(D, nrows);
-            for (int i = 0; i < pre; ++i)
-                issue(i);
-            if (x_seg != sg) {
-                staged_load_x<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, X);
-                x_seg = sg;
-            }
-            // x (and the prologue rows) complete here, so that inside the row loop
-            // only ring copies are outstanding and the explicit waits below are
-            // the only ones
-            __builtin_amdgcn_s_waitcnt(0);
-            for (int i = 0; i < nrows; ++i) {
-                wait_vmcnt(ipr * min(D - 1, nrows - 1 - i)); // row i has landed
-                const uint32_t slot = my_ring + (uint32_t)((i % D) * SLOT);
-                float v = 0.0f;
-                if constexpr (FMT == kQ6_K) {
-                    const int bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
-                    if (bs < seg_blocks)
-                        v = q6_dot(ring, slot + (uint32_t)(210 * bs), n, l0, X);
-                } else if constexpr (FMT == kIQ4_NL) {
-                    if (lane < seg_blocks)
-                        v = iq4nl_dot(ring + slot, 18u * lane, X);
-                } else {
-                    if (lane < seg_blocks)
-                        v = q80_dot(ring + slot, 34u * lane, X.x);
-                }
-                v = wave_sum(v);
-                if (lane == 0)
-                    part[i][w] += v;
-                if (i + D < nrows)
-                    issue(i + D); // slot i % D has been read
-            }
-        }
-        __syncthreads();
-        for (int i = tid; i < nrows; i += NW * 64) {
-            float v = 0.0f;
-#pragma unroll
-            for (int k = 0; k < NW; ++k)
-                v += part[i][k];
-            if (y)
-                y[row0 + i] = resid ? epi_apply(rv, v, epi) : v; // i == tid; resid may be y
-            if constexpr (ARGMAX)
-                argmax_fold(v, (uint32_t)(row0 + i), key, fl);
-        }
-        __syncthreads(); // part is cleared for the next chunk
-    }
-    if constexpr (ARGMAX) {
-        argmax_wave_reduce(key, fl);
-        if (lane == 0) {
-            wkey[w] = key;
-            wflag[w] = fl;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            unsigned long long k = wkey[0];
-            uint32_t f = wflag[0];
-#pragma unroll
-            for (int i = 1; i < NW; ++i) {
-                k = wkey[i] > k ? wkey[i] : k;
-                f |= wflag[i];
-            }
-            parts[blockIdx.x].key = k;
-            parts[blockIdx.x].flags = f;
-            parts[blockIdx.x].pad = 0;
-        }
-    }
 }
 
 // ---- persistent streamed kernel with integer-digit activations -----------
@@ -1440,12 +1010,12 @@ __device__ __forceinline__ void sxd_load(SXD &X, const uint32_t (*d)[64][4], int
 
 // The walk itself over LDS the caller declares (ring: NW * D * sdig_slot
 // bytes, 16-byte aligned; digs: the staged digits of sdig_share_cap(NW)
-// segments unless ARGMAX; part: kSdigMaxRows x 8; wkey / wflag: NW each).
+// segments unless ARGMAX; part: kSdigMaxRows x NW; wkey / wflag: NW each).
 template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
 __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const float *x, float *y,
                                          int outer, int nblk, int rpc, ArgPart *__restrict__ parts,
                                          const float *resid, int epi, uint8_t *ring,
-                                         uint32_t (*digs)[kDigQuads][64][4], float (*part)[8],
+                                         uint32_t (*digs)[kDigQuads][64][4], float (*part)[NW],
                                          unsigned long long *wkey, uint32_t *wflag)
 {
     using F = SFmt<FMT>;
@@ -1610,7 +1180,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     constexpr int SHC = ARGMAX ? 0 : sdig_share_cap(NW);
     __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * sdig_slot(FMT)];
     __shared__ __attribute__((aligned(16))) uint32_t digs[SHC > 0 ? SHC : 1][kDigQuads][64][4];
-    __shared__ float part[kSdigMaxRows][8];
+    __shared__ float part[kSdigMaxRows][NW]; // one column per segment (nseg <= NW)
     __shared__ unsigned long long wkey[NW];
     __shared__ uint32_t wflag[NW];
     sdig_run<FMT, NW, D, ARGMAX, RESID>(W, x, y, outer, nblk, rpc, parts, resid, epi, ring, digs, part,
@@ -1620,144 +1190,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
 // ------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------
-// Rows per wave of the wide kernels and rows per chunk of the streamed
-// kernels; 0 = the measured default.
-static int g_rows_wide = 0;   // Q4_K/Q5_K GEMV (default 2)
-static int g_rows_gateup = 0; // fused gate/up (default 1)
-static int g_stream_rows = 0; // Q6_K/Q8_0 rows per chunk (default: see stream_rows())
-static int g_wide_fp32 = 0;   // Q4_K/Q5_K: 1 = fp32 activations instead of integer digits
-static int g_wide_waves = 0;  // Q4_K/Q5_K waves per workgroup (4 or 8; default 8)
-static int g_wide_persist = 0; // Q4_K/Q5_K persistent kernel: 1 = always, -1 = never, 0 = by size
-static int g_pers_wg_per_cu = 1; // workgroups per CU of the persistent kernel
-static int g_pers_bufs = 0;      // register buffers per wave of the persistent kernel (2..4)
-static int g_stream_wg_per_cu = 0; // streamed kernel: cap on workgroups per CU (0 = one per chunk)
-// persistent digit streamed kernel: rows per chunk, ring depth (0 = default), 1 = not used
-static int g_sdig_rows = 0, g_sdig_depth = 0, g_sdig_off = 0, g_sdig_wg_per_cu = 0, g_sdig_waves = 0;
-static int g_argmax_threads = 0; // argmax finalize: 64, 256 or 1024 threads (0 = 256)
-
-void set_tuning(const char *name, int value)
-{
-    if (!__builtin_strcmp(name, "rows_wide")) g_rows_wide = value;
-    if (!__builtin_strcmp(name, "rows_gateup")) g_rows_gateup = value;
-    if (!__builtin_strcmp(name, "stream_rows")) g_stream_rows = value;
-    if (!__builtin_strcmp(name, "wide_fp32")) g_wide_fp32 = value;
-    if (!__builtin_strcmp(name, "wide_waves")) g_wide_waves = value;
-    if (!__builtin_strcmp(name, "wide_persist")) g_wide_persist = value;
-    if (!__builtin_strcmp(name, "pers_wg_per_cu")) g_pers_wg_per_cu = value > 0 ? value : 1;
-    if (!__builtin_strcmp(name, "pers_bufs")) g_pers_bufs = value;
-    if (!__builtin_strcmp(name, "stream_wg_per_cu")) g_stream_wg_per_cu = value;
-    if (!__builtin_strcmp(name, "sdig_rows")) g_sdig_rows = value;
-    if (!__builtin_strcmp(name, "sdig_depth")) g_sdig_depth = value;
-    if (!__builtin_strcmp(name, "sdig_off")) g_sdig_off = value;
-    if (!__builtin_strcmp(name, "sdig_wg_per_cu")) g_sdig_wg_per_cu = value;
-    if (!__builtin_strcmp(name, "sdig_waves")) g_sdig_waves = value;
-    if (!__builtin_strcmp(name, "argmax_threads")) g_argmax_threads = value;
-}
-
-template <int FMT, bool GATEUP>
-static hipError_t launch_kwide(const void *w, const void *w2, const float *x, float *y,
-                               int inner, int outer, hipStream_t s, const float *nw = nullptr,
-                               float eps = 0.0f, const float *resid = nullptr, int epi = kEpiAdd)
-{
-    const int nblk = inner / 256;
-    int R = GATEUP ? g_rows_gateup : g_rows_wide;
-    if (R <= 0) // measured on MI355X: 4096 x 4096 GEMV and 2 x 12288 x 4096 gate/up
-        R = GATEUP ? 1 : 2;
-    if (FMT == kQ5_K && GATEUP && R > 2)
-        R = 2; // register budget
-    const bool dig = g_wide_fp32 <= 0;
-    const bool ext = GATEUP ? nw != nullptr : resid != nullptr;
-    const int nwv = g_wide_waves == 4 ? 4 : 8;
-#define IHIP_KW(RR, DG, EX, NV)                                                              \
-    hipLaunchKernelGGL((k_gemv_kwide<FMT, RR, GATEUP, DG, EX, NV>),                          \
-                       dim3((outer + NV * RR - 1) / (NV * RR)), dim3(NV * 64), 0, s,          \
-                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid, epi)
-#define IHIP_KW_R(DG, EX)                                                                    \
-    do {                                                                                     \
-        if (nwv == 8) {                                                                      \
-            if (R == 1) IHIP_KW(1, DG, EX, 8); else if (R == 4) IHIP_KW(4, DG, EX, 8); else IHIP_KW(2, DG, EX, 8); \
-        } else {                                                                             \
-            if (R == 1) IHIP_KW(1, DG, EX, 4); else if (R == 4) IHIP_KW(4, DG, EX, 4); else IHIP_KW(2, DG, EX, 4); \
-        }                                                                                    \
-    } while (0)
-    // the persistent kernel once every wave has at least four rows (measured on
-    // MI355X: 2 x 12288 x 4096 gate/up 12.7 us against 13.9 us; at 4096 x 4096
-    // one row group per wave is all there is and the plain kernel is faster)
-    const bool pers = dig && nblk <= 16 && (g_wide_persist > 0 || (g_wide_persist == 0 && outer >= 4 * nwv * 256));
-    if (pers) {
-        int dev = 0, ncu = 256;
-        if (hipGetDevice(&dev) == hipSuccess)
-            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-        const int nbuf = g_pers_bufs >= 2 && g_pers_bufs <= 4 ? g_pers_bufs : 2;
-        const int grid = max(1, min(ncu * g_pers_wg_per_cu, (outer + nwv - 1) / nwv));
-#define IHIP_KP(RR, EX, NV, NBB)                                                             \
-    hipLaunchKernelGGL((k_gemv_kpers<FMT, RR, GATEUP, EX, NV, NBB>), dim3(grid), dim3(NV * 64), 0, s, \
-                       (const uint8_t *)w, (const uint8_t *)w2, x, y, outer, nblk, nw, eps, resid, epi)
-#define IHIP_KP_R(EX)                                                                        \
-    do {                                                                                     \
-        if (nwv == 8) {                                                                      \
-            if (nbuf == 2) IHIP_KP(1, EX, 8, 2); else if (nbuf == 3) IHIP_KP(1, EX, 8, 3); else IHIP_KP(1, EX, 8, 4); \
-        } else {                                                                             \
-            if (nbuf == 2) IHIP_KP(1, EX, 4, 2); else if (nbuf == 3) IHIP_KP(1, EX, 4, 3); else IHIP_KP(1, EX, 4, 4); \
-        }                                                                                    \
-    } while (0)
-        if (ext) IHIP_KP_R(true); else IHIP_KP_R(false);
-#undef IHIP_KP_R
-#undef IHIP_KP
-    } else if (dig) {
-        if (ext) IHIP_KW_R(true, true); else IHIP_KW_R(true, false);
-    } else {
-        if (ext) IHIP_KW_R(false, true); else IHIP_KW_R(false, false);
-    }
-#undef IHIP_KW_R
-#undef IHIP_KW
-    return hipGetLastError();
-}
-
-// Waves per workgroup of the streamed kernel: one per K segment, at most 8.
-static int stream_waves(int nseg) { return nseg >= 8 ? 8 : nseg >= 6 ? 6 : nseg >= 4 ? 4 : nseg; }
-
-// Rows per chunk: outer / 1024 within 4..16 (at least four workgroups per
-// CU; measured on MI355X at 4096 x 4096 Q8_0, 4096 x 12288 Q6_K and
-// 151936 x 2048 Q6_K).  With the fused argmax every chunk leaves one partial,
-// so the chunk count is kept within kArgMaxParts.
-static int stream_rows(int outer, bool argmax)
-{
-    int r;
-    if (g_stream_rows > 0) {
-        r = min(g_stream_rows, kStreamMaxRows);
-    } else {
-        r = outer / 1024;
-        r = r < 4 ? 4 : r > 16 ? 16 : r;
-    }
-    if (argmax)
-        r = max(r, (outer + kArgMaxParts - 1) / kArgMaxParts);
-    return r;
-}
-
-// One workgroup per chunk, or at most g_stream_wg_per_cu workgroups per CU that
-// walk the chunks grid-stride (each keeps its x slice across its chunks).
-static int stream_grid(int outer, int rpc)
-{
-    const int nchunks = (outer + rpc - 1) / rpc;
-    if (g_stream_wg_per_cu <= 0)
-        return nchunks;
-    int dev = 0, ncu = 256;
-    if (hipGetDevice(&dev) == hipSuccess)
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    return max(1, min(nchunks, g_stream_wg_per_cu * ncu));
-}
-
-static SdigKnobs sdig_knobs()
-{
-    SdigKnobs k;
-    k.rows = g_sdig_rows;
-    k.depth = g_sdig_depth;
-    k.wg_per_cu = g_sdig_wg_per_cu;
-    k.waves = g_sdig_waves;
-    return k;
-}
-
 static int device_cus()
 {
     int dev = 0, ncu = 256;
@@ -1766,64 +1198,73 @@ static int device_cus()
     return ncu;
 }
 
-static bool sdig_usable(int fmt, int nblk) { return g_sdig_off <= 0 && sdig_rows_ok(fmt, nblk); }
-
-template <int FMT, bool ARGMAX, int NWV, int DD>
-static void launch_sdig_nd(const void *w, const float *x, float *y, int nblk, int outer,
-                           const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
+// Q4_K / Q5_K: 8-wave workgroups; two rows per wave for the GEMV, one gate and
+// one up row per wave for the fused gate/up (measured on MI355X at 4096 x 4096
+// and 2 x 12288 x 4096).  Rows of at most 4096 columns with at least four row
+// groups per wave over one workgroup per CU take the persistent kernel (2 x
+// 12288 x 4096 gate/up 12.7 us against 13.9 us; at 4096 x 4096 one row group
+// per wave is all there is and the plain kernel is faster).
+template <int FMT, bool GATEUP>
+static hipError_t launch_kwide(const void *w, const void *w2, const float *x, float *y,
+                               int inner, int outer, hipStream_t s, const float *nw = nullptr,
+                               float eps = 0.0f, const float *resid = nullptr, int epi = kEpiAdd)
 {
-    if (resid)
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, true>), dim3(p.grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
-    else
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, DD, ARGMAX, false>), dim3(p.grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
-}
-
-// The instantiation sdig_plan chose (ring depths that do not fit the LDS are
-// never instantiated; the plan never picks them).
-template <int FMT, bool ARGMAX>
-static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner, int outer,
-                              void *parts, hipStream_t s, const float *resid, int epi)
-{
-    const int nblk = inner / block_elems(FMT);
-    const SdigPlan p = sdig_plan(FMT, nblk, outer, ARGMAX, sdig_knobs(), device_cus());
-    switch (p.nw * 16 + p.d) {
-    case 12 * 16 + 6:
-        if constexpr (sdig_fits(FMT, 12, 6))
-            launch_sdig_nd<FMT, ARGMAX, 12, 6>(w, x, y, nblk, outer, p, parts, s, resid, epi);
-        break;
-    case 12 * 16 + 4:
-        if constexpr (sdig_fits(FMT, 12, 4))
-            launch_sdig_nd<FMT, ARGMAX, 12, 4>(w, x, y, nblk, outer, p, parts, s, resid, epi);
-        break;
-    case 12 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 12, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
-    case 16 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 16, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
-    case 6 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 6, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
-    case 6 * 16 + 4: launch_sdig_nd<FMT, ARGMAX, 6, 4>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
-    case 8 * 16 + 2: launch_sdig_nd<FMT, ARGMAX, 8, 2>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
-    case 8 * 16 + 4: launch_sdig_nd<FMT, ARGMAX, 8, 4>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
-    default: return hipErrorInvalidValue;
+    constexpr int NWV = 8, R = GATEUP ? 1 : 2, NB = 2;
+    const int nblk = inner / 256;
+    const bool ext = GATEUP ? nw != nullptr : resid != nullptr;
+    const uint8_t *W = (const uint8_t *)w, *W2 = (const uint8_t *)w2;
+    if (nblk <= 16 && outer >= 4 * NWV * 256) {
+        const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
+        if (ext)
+            hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, true, NWV, NB>), dim3(grid), dim3(NWV * 64),
+                               0, s, W, W2, x, y, outer, nblk, nw, eps, resid, epi);
+        else
+            hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, false, NWV, NB>), dim3(grid), dim3(NWV * 64),
+                               0, s, W, W2, x, y, outer, nblk, nw, eps, resid, epi);
+    } else {
+        const dim3 grid((outer + NWV * R - 1) / (NWV * R));
+        if (ext)
+            hipLaunchKernelGGL((k_gemv_kwide<FMT, R, GATEUP, true, NWV>), grid, dim3(NWV * 64), 0, s, W,
+                               W2, x, y, outer, nblk, nw, eps, resid, epi);
+        else
+            hipLaunchKernelGGL((k_gemv_kwide<FMT, R, GATEUP, false, NWV>), grid, dim3(NWV * 64), 0, s, W,
+                               W2, x, y, outer, nblk, nw, eps, resid, epi);
     }
     return hipGetLastError();
 }
 
-template <int FMT, bool ARGMAX>
-static hipError_t launch_stream(const void *w, const float *x, float *y, int inner, int outer,
-                                void *parts, hipStream_t s, const float *resid = nullptr,
-                                int epi = kEpiAdd)
+template <int FMT, bool ARGMAX, int NWV>
+static void launch_sdig_nw(const void *w, const float *x, float *y, int nblk, int outer,
+                           const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
 {
-    if (sdig_usable(FMT, inner / block_elems(FMT)))
-        return launch_sdig<FMT, ARGMAX>(w, x, y, inner, outer, parts, s, resid, epi);
+    if (resid)
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, true>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+    else
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, false>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+}
+
+// Q6_K / Q8_0 / IQ4_NL rows of 1..16 segments through the streamed digit
+// kernel, with the waves and grid sdig_plan chooses; wider rows through the
+// byte-granular kernel (no argmax fusion for them: the caller checks
+// lm_head_fusable).
+template <int FMT, bool ARGMAX>
+static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner, int outer,
+                              void *parts, hipStream_t s, const float *resid = nullptr,
+                              int epi = kEpiAdd)
+{
     const int nblk = inner / block_elems(FMT);
-    const int nseg = (nblk + SFmt<FMT>::SEG_BLOCKS - 1) / SFmt<FMT>::SEG_BLOCKS;
-    const int nw = stream_waves(nseg);
-    const int rpc = stream_rows(outer, ARGMAX);
-    const int grid = stream_grid(outer, rpc);
-#define IHIP_ST(NWV, DD)                                                                         if (nw == NWV) {                                                                                 hipLaunchKernelGGL((k_gemv_stream<FMT, NWV, DD, ARGMAX>), dim3(grid), dim3(NWV * 64),                            0, s, (const uint8_t *)w, x, y, outer, nblk, rpc, (ArgPart *)parts, resid, epi);         return hipGetLastError();                                                                }
-    IHIP_ST(1, 2) IHIP_ST(2, 2) IHIP_ST(3, 2) IHIP_ST(4, 2) IHIP_ST(6, 2) IHIP_ST(8, 2)
-#undef IHIP_ST
-    return hipErrorInvalidValue;
+    if (!sdig_rows_ok(FMT, nblk))
+        return ARGMAX ? hipErrorInvalidValue : launch_gemv_generic(FMT, w, x, y, inner, outer, s, resid, epi);
+    const SdigPlan p = sdig_plan(FMT, nblk, outer, ARGMAX, device_cus());
+    switch (p.nw) {
+    case 8: launch_sdig_nw<FMT, ARGMAX, 8>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 12: launch_sdig_nw<FMT, ARGMAX, 12>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    case 16: launch_sdig_nw<FMT, ARGMAX, 16>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
@@ -1832,9 +1273,9 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     switch (type) {
     case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
     case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
-    case kQ6_K: return launch_stream<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
-    case kQ8_0: return launch_stream<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
-    case kIQ4_NL: return launch_stream<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kQ6_K: return launch_sdig<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kQ8_0: return launch_sdig<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kIQ4_NL: return launch_sdig<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     default: return hipErrorInvalidValue;
     }
 }
@@ -1855,48 +1296,38 @@ hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const
     }
 }
 
-bool lm_head_fusable(int vocab) { return stream_rows(vocab, true) <= kStreamMaxRows; }
+bool lm_head_fusable(int type, int hidden)
+{
+    return (type == kQ6_K || type == kQ8_0) && sdig_rows_ok(type, hidden / block_elems(type));
+}
 
+// 256 threads, four 16-byte partials in flight per thread (measured on MI355X
+// for the lm_head's 768 partials: 0.9 us per call less than 1024 threads; a
+// single wave gains nothing)
 static void launch_argmax_finalize(const void *ws, int nparts, int32_t *token, uint32_t *flags,
                                    hipStream_t s)
 {
-    // 256 measured fastest for the lm_head's 1024 partials (against 1024 threads:
-    // -0.9 us per call; a single wave gains nothing)
-    int nt = g_argmax_threads;
-    if (nt != 64 && nt != 256 && nt != 1024)
-        nt = 256;
-    const ArgPart *parts = (const ArgPart *)ws;
-    switch (nt) {
-    case 64:
-        hipLaunchKernelGGL(k_argmax_finalize<64>, dim3(1), dim3(64), 0, s, parts, nparts, token, flags);
-        break;
-    case 256:
-        hipLaunchKernelGGL(k_argmax_finalize<256>, dim3(1), dim3(256), 0, s, parts, nparts, token, flags);
-        break;
-    default:
-        hipLaunchKernelGGL(k_argmax_finalize<1024>, dim3(1), dim3(1024), 0, s, parts, nparts, token, flags);
-    }
+    hipLaunchKernelGGL(k_argmax_finalize, dim3(1), dim3(256), 0, s, (const ArgPart *)ws, nparts,
+                       token, flags);
 }
 
 int lm_head_argmax_parts(int type, int hidden, int vocab, bool fused)
 {
     if (!fused) // the GEMV, then the standalone argmax over the logits
         return (int)std::min<int64_t>(std::max<int64_t>(1, ((int64_t)vocab + 255) / 256), kArgMaxParts);
-    const int nblk = hidden / block_elems(type);
-    return sdig_usable(type, nblk) ? sdig_plan(type, nblk, vocab, true, sdig_knobs(), device_cus()).grid
-                                   : stream_grid(vocab, stream_rows(vocab, true));
+    return sdig_plan(type, hidden / block_elems(type), vocab, true, device_cus()).grid;
 }
 
 hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float *logits,
                                  int32_t *token, uint32_t *flags, int hidden, int vocab,
                                  void *ws, hipStream_t s)
 {
-    if (!lm_head_fusable(vocab))
+    if (!lm_head_fusable(type, hidden))
         return hipErrorInvalidValue;
     hipError_t e;
     switch (type) {
-    case kQ6_K: e = launch_stream<kQ6_K, true>(w, x, logits, hidden, vocab, ws, s); break;
-    case kQ8_0: e = launch_stream<kQ8_0, true>(w, x, logits, hidden, vocab, ws, s); break;
+    case kQ6_K: e = launch_sdig<kQ6_K, true>(w, x, logits, hidden, vocab, ws, s); break;
+    case kQ8_0: e = launch_sdig<kQ8_0, true>(w, x, logits, hidden, vocab, ws, s); break;
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess)

@@ -16,8 +16,10 @@ bool gate_up_fusable(int gate_type, int up_type);
 hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,
                                  float *h, int hidden, int inter, hipStream_t s,
                                  const float *norm_w = nullptr, float eps = 0.0f);
-// The fused lm_head argmax handles vocab <= 16384 chunks of at most 64 rows.
-bool lm_head_fusable(int vocab);
+// Whether the argmax can be fused into the lm_head GEMV: Q6_K / Q8_0 rows of
+// at most 16 segments of 2048 columns (any vocabulary: the grid is capped at
+// kArgMaxParts workgroups, one partial each).
+bool lm_head_fusable(int type, int hidden);
 // Argmax partials (16 bytes each) one lm_head call writes: fused into the
 // streamed GEMV, or the standalone argmax after the GEMV.
 int lm_head_argmax_parts(int type, int hidden, int vocab, bool fused);
@@ -26,7 +28,6 @@ hipError_t launch_lm_head_argmax(int type, const void *w, const float *x, float 
                                  void *ws, hipStream_t s);
 hipError_t launch_argmax(const float *v, int64_t n, int32_t *token, uint32_t *flags, void *ws,
                          hipStream_t s);
-void set_tuning(const char *name, int value);
 
 // kq_dequant.hip
 hipError_t launch_gemv_generic(int type, const void *w, const float *x, float *y, int inner,
@@ -43,7 +44,6 @@ hipError_t launch_silu_gate_mul(float *out, const float *x, const float *gate, i
 // kq_prefill.hip
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s);
-void set_prefill_tuning(const char *name, int value);
 
 // kq_q8k.hip
 hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t s);

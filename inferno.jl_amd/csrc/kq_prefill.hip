@@ -362,8 +362,6 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     }
 }
 
-void set_prefill_tuning(const char *, int) {}
-
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s)
 {

@@ -25,6 +25,7 @@
 namespace ihip {
 
 constexpr int kSdigMaxRows = 64;    // rows per chunk (part[] in LDS holds one chunk)
+constexpr int kSdigMaxSeg = 16;     // segments per row: one wave each in a 16-wave workgroup
 constexpr int kArgMaxParts = 16384; // argmax partials: IHIP_ARGMAX_WS_BYTES / 16
 constexpr int kDigQuads = 10;       // staged digits per lane: 10 x 16 bytes
 
@@ -44,10 +45,11 @@ __host__ __device__ constexpr int sdig_slot(int fmt) { return sdig_ipr(fmt) * 10
 __host__ __device__ constexpr int sdig_share_cap(int nw) { return nw == 12 ? 6 : nw == 8 ? 2 : 0; }
 
 // Whether NW waves with D ring slots fit the 160 KB of LDS: the ring, the
-// staged digits, the chunk partial sums and 2 KB for the rest.
+// staged digits, the chunk partial sums (one column per wave) and 2 KB for
+// the rest.
 __host__ __device__ constexpr bool sdig_fits(int fmt, int nw, int d)
 {
-    return nw * d * sdig_slot(fmt) + sdig_share_cap(nw) * kDigQuads * 1024 + kSdigMaxRows * 8 * 4 +
+    return nw * d * sdig_slot(fmt) + sdig_share_cap(nw) * kDigQuads * 1024 + kSdigMaxRows * nw * 4 +
                2048 <= 160 * 1024;
 }
 
@@ -209,70 +211,62 @@ __host__ __device__ inline SdigChunk sdig_chunk(const SdigWave &g, int ci, int b
 __host__ __device__ inline int sdig_chunk_row(const SdigWave &g, int rr) { return g.rl + rr * g.wps; }
 
 // ---- host: the launch plan ------------------------------------------------
-// Process-wide knobs (0 = the measured default).
-struct SdigKnobs {
-    int rows = 0;      // rows per chunk (1..64)
-    int depth = 0;     // ring slots per wave (2, 4 or 6)
-    int wg_per_cu = 0; // workgroups per CU
-    int waves = 0;     // waves per workgroup (6, 8, 12, 16)
-};
-
 struct SdigPlan {
     int nseg, nw, d, rpc, grid;
 };
 
-// Rows per chunk (measured on MI355X: 151936 x 2048 Q6_K lm_head, 4096 x 4096
-// Q8_0, 4096 x 12288 Q6_K): rows of one segment finish inside their wave and
-// take long chunks; rows of several segments meet in LDS once per chunk and
-// take short ones, which spread a small matrix over more workgroups.
-inline int sdig_rows(int nseg, const SdigKnobs &kn)
+// Waves per workgroup, rows per chunk and workgroups per CU by segment count,
+// measured on MI355X (us per GEMV in sweeps of HBM-resident copies; the
+// previous plan in parentheses where it differed):
+//   1 segment     8 waves, 32 rows, 3 per CU: the 151936 x 2048 Q6_K lm_head
+//                 (54-55 us; 57 with 4 per CU).  Rows finish inside their wave.
+//   2..6          12 waves, 16 rows, 4 per CU: 4096 x 4096 Q8_0 6.47, Q6_K 6.48,
+//                 IQ4_NL 6.23 (8 waves: 6.95+); 4096 x 6144 Q6_K 8.17;
+//                 4096 x 8192 Q8_0 9.67 (16.0); 4096 x 10240 Q8_0 12.70
+//                 (18.7); 4096 x 12288 Q6_K 12.3-12.4 (6 waves: 14.3).
+//                 Two or more waves per segment share its staged digits.
+//   7..8          16 waves, 16 rows, 2 per CU: 4096 x 14336 Q6_K 15.1-15.5
+//                 (18.2), IQ4_NL 16.1-16.3 (19.8); 4096 x 16384 Q6_K 15.7
+//                 (18.9).  Q8_0, whose 16-wave workgroup takes 104 KB of
+//                 LDS: 8 waves, 16 rows, 4 per CU (4096 x 16384 17.0; 21.8).
+//   9..12         12 waves, 16 rows, 1 per CU: 4096 x 24576 Q6_K 20.6 (16
+//                 waves 21.3), 4096 x 20480 Q8_0 21.9 (23.0).
+//   13..16        16 waves, 16 rows, 1 per CU: 8192 x 28672 Q6_K 42.6 (2 per
+//                 CU 46.5), 4096 x 32768 Q8_0 30.7.
+// Rows of several segments meet in LDS once per chunk; the sweeps' best
+// chunk was 16 rows throughout (4 and 8 lost 0.5-7 us, 32 up to 10 us).
+inline int sdig_waves(int fmt, int nseg)
 {
-    const int r = kn.rows > 0 ? kn.rows : nseg == 1 ? 32 : nseg == 2 ? 16 : (nseg == 3 || nseg == 6) ? 16 : 4;
-    return sd_min(r, kSdigMaxRows);
+    return nseg == 1 ? 8 : nseg <= 6 ? 12 : nseg <= 8 ? (fmt == kQ8_0 ? 8 : 16) : nseg <= 12 ? 12 : 16;
+}
+inline int sdig_rows(int nseg) { return nseg == 1 ? 32 : 16; }
+inline int sdig_wg_per_cu(int fmt, int nseg)
+{
+    return nseg == 1 ? 3 : nseg <= 6 ? 4 : nseg <= 8 ? (fmt == kQ8_0 ? 4 : 2) : 1;
 }
 
-// Waves per workgroup: a multiple of nseg where possible (measured on MI355X:
-// 4096 x 12288 Q6_K 12 waves 12.8 us, 6 waves 14.3 us; 4096 x 4096, two
-// segments, 12 against 8 waves: Q8_0 5.98 / 6.26 us, Q6_K 6.04 / 6.45 us,
-// IQ4_NL 5.79 / 5.99 us).
-inline int sdig_waves(int nseg, const SdigKnobs &kn)
-{
-    if ((kn.waves == 6 || kn.waves == 8 || kn.waves == 12 || kn.waves == 16) && kn.waves >= nseg)
-        return kn.waves;
-    return (nseg == 2 || nseg == 3 || nseg == 6) ? 12 : 8;
-}
-
-// Whether the streamed kernel takes rows of nblk blocks: 1..8 segments.
+// Whether the streamed kernel takes rows of nblk blocks: 1..16 segments.
 inline bool sdig_rows_ok(int fmt, int nblk)
 {
     const int nseg = (nblk + sdig_seg_blocks(fmt) - 1) / sdig_seg_blocks(fmt);
-    return nblk > 0 && nseg >= 1 && nseg <= 8;
+    return nblk > 0 && nseg >= 1 && nseg <= kSdigMaxSeg;
 }
 
-// The launch: waves, ring depth, rows per chunk and grid.  With the fused
-// argmax every workgroup leaves one partial, so the grid stays within
-// kArgMaxParts whatever the knobs or the device's CU count.
-inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, const SdigKnobs &kn, int ncu)
+// The launch: waves, ring depth (two slots per wave), rows per chunk and grid.
+// With the fused argmax every workgroup leaves one partial, so the grid stays
+// within kArgMaxParts whatever the device's CU count.
+inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, int ncu)
 {
     SdigPlan p;
     p.nseg = (nblk + sdig_seg_blocks(fmt) - 1) / sdig_seg_blocks(fmt);
-    p.rpc = sdig_rows(p.nseg, kn);
+    p.rpc = sd_min(sdig_rows(p.nseg), kSdigMaxRows);
     const int nchunks = (outer + p.rpc - 1) / p.rpc;
-    // one-segment rows (the 2048-wide lm_head): 3 workgroups per CU measured
-    // 54-55 us against 57 us with 4 (151936 rows, 32 per chunk, interleaved)
-    const int per_cu = kn.wg_per_cu > 0 ? kn.wg_per_cu : p.nseg == 1 ? 3 : 4;
-    int grid = sd_max(1, sd_min(nchunks, sd_max(1, ncu) * sd_min(per_cu, 64)));
+    int grid = sd_max(1, sd_min(nchunks, sd_max(1, ncu) * sdig_wg_per_cu(fmt, p.nseg)));
     if (argmax)
         grid = sd_min(grid, kArgMaxParts);
     p.grid = grid;
-    p.nw = sdig_waves(p.nseg, kn);
-    const int dd = kn.depth >= 6 ? 6 : kn.depth >= 4 ? 4 : 2;
-    if (p.nw == 12)
-        p.d = (dd == 6 && sdig_fits(fmt, 12, 6)) ? 6 : (dd == 4 && sdig_fits(fmt, 12, 4)) ? 4 : 2;
-    else if (p.nw == 16)
-        p.d = 2;
-    else
-        p.d = dd == 2 ? 2 : 4;
+    p.nw = sdig_waves(fmt, p.nseg);
+    p.d = 2;
     return p;
 }
 

@@ -17,4 +17,4 @@ FusedKernels and Dequant modules over that library:
 There is no CPU fallback: without the built library the calls raise.
 """
 from ._lib import (IHIPArgumentError, IHIPError, LibraryNotBuilt, Q4_K, Q5_K, Q6_K, Q8_0,  # noqa: F401
-                   available, lib, set_tuning)
+                   available, lib)

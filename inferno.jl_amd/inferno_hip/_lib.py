@@ -56,7 +56,6 @@ SIGNATURES = {
     "ihip_available": ([], _i),
     "ihip_init": ([_i], _i),
     "ihip_shutdown": ([], _i),
-    "ihip_set_tuning": ([C.c_char_p, _i], _i),
     "ihip_weight_register": ([_vp, _sz, _i, _i, _i, C.POINTER(_u64)], _i),
     "ihip_weight_release": ([_u64], _i),
     "ihip_weight_forget": ([_vp], _i),
@@ -141,5 +140,3 @@ def available() -> bool:
         return False
 
 
-def set_tuning(name: str, value: int) -> None:
-    check(lib().ihip_set_tuning(name.encode(), int(value)))

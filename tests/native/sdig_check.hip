@@ -51,9 +51,8 @@ struct Report {
 // Returns the number of violations (0: the launch is clean); msg receives the
 // first.  stats[0..7]: grid, waves, ring depth, rows per chunk, segments,
 // copies checked, rows produced, highest W byte read + 1.
-extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int k_rows, int k_depth,
-                                int k_wg_per_cu, int k_waves, int ncu, char *msg, int cap,
-                                long long *stats)
+extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int ncu, char *msg,
+                                int cap, long long *stats)
 {
     Report R{msg, cap};
     if (msg && cap > 0)
@@ -71,24 +70,18 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int k
         R.fail("the host does not take %d blocks to this kernel", nblk);
         return R.errors;
     }
-    SdigKnobs kn;
-    kn.rows = k_rows;
-    kn.depth = k_depth;
-    kn.wg_per_cu = k_wg_per_cu;
-    kn.waves = k_waves;
-    const SdigPlan p = sdig_plan(fmt, nblk, outer, argmax != 0, kn, ncu);
+    const SdigPlan p = sdig_plan(fmt, nblk, outer, argmax != 0, ncu);
     const int NW = p.nw, D = p.d, rpc = p.rpc, grid = p.grid;
     const int IPR = sdig_ipr(fmt), SLOT = sdig_slot(fmt), bb = block_bytes(fmt);
     const int SHC = argmax ? 0 : sdig_share_cap(NW);
     const size_t row_bytes = (size_t)nblk * bb, w_bytes = (size_t)outer * row_bytes;
     const int ring_bytes = NW * D * SLOT;
 
-    // the instantiations the launcher can dispatch
-    const bool inst = (NW == 12 && (D == 2 || (D == 4 && sdig_fits(fmt, 12, 4)) ||
-                                    (D == 6 && sdig_fits(fmt, 12, 6)))) ||
-                      (NW == 16 && D == 2) || ((NW == 6 || NW == 8) && (D == 2 || D == 4));
-    if (!inst)
+    // the instantiations the launcher can dispatch, and their LDS
+    if (!((NW == 8 || NW == 12 || NW == 16) && D == 2))
         R.fail("plan picked %d waves x depth %d, which is not instantiated", NW, D);
+    if (!sdig_fits(fmt, NW, D))
+        R.fail("%d waves x depth %d do not fit the LDS", NW, D);
     if (p.nseg > NW)
         R.fail("%d segments > %d waves", p.nseg, NW);
     if (rpc < 1 || rpc > kSdigMaxRows)
@@ -210,8 +203,8 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int k
                         if (row >= 0 && row < outer)
                             seen_row[(size_t)row]++;
                     } else {
-                        if (lr >= kSdigMaxRows || g.sg >= 8)
-                            R.fail("part[%d][%d] outside [%d][8]", lr, g.sg, kSdigMaxRows);
+                        if (lr >= kSdigMaxRows || g.sg >= NW)
+                            R.fail("part[%d][%d] outside [%d][%d]", lr, g.sg, kSdigMaxRows, NW);
                         if (row >= 0 && row < outer)
                             seen_seg[(size_t)row * p.nseg + g.sg]++;
                     }

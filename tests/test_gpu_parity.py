@@ -195,124 +195,94 @@ def test_gemv_host_mirror_and_weight_cache(t):
                   oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), "after forget")
 
 
-STREAM_SHAPES = ((synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144), (synth.Q6_K, 300, 24576),
-                 (synth.Q6_K, 33, 10240), (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304),
-                 (synth.Q8_0, 19, 256), (synth.IQ4_NL, 517, 4608))
-
-TUNING_CASES = [
-    ({"rows_wide": r}, t, outer, inner)
-    for r in (1, 2, 4) for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608))
-] + [
-    # Q4_K/Q5_K: fp32 activations instead of integer digits; four waves per workgroup
-    ({knob: 1 if knob == "wide_fp32" else 4}, t, outer, inner)
-    for knob in ("wide_fp32", "wide_waves")
-    for t, outer, inner in ((synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608), (synth.Q4_K, 9, 8448))
-] + [
-    # Q4_K/Q5_K persistent digit kernel (register-buffered row groups), forced on
-    ({"wide_persist": 1, "pers_bufs": nb, "wide_waves": nw}, t, outer, inner)
-    for nb, nw in ((2, 8), (3, 4), (4, 8))
-    for t, outer, inner in ((synth.Q4_K, 4099, 4096), (synth.Q5_K, 2051, 2560), (synth.Q4_K, 7, 256))
-] + [
-    # fp32 streamed Q6_K / Q8_0 / IQ4_NL kernel: rows per chunk x (waves per workgroup =
-    # segments, up to 8; 12 and 5 segments give waves that own two segments)
-    ({"sdig_off": 1, "stream_rows": r}, t, outer, inner)
-    for r in (4, 17, 64) for t, outer, inner in STREAM_SHAPES
-] + [
-    # persistent digit streamed kernel: ring depth, rows per chunk (1 and 7: chunks that
-    # split unevenly over the waves of a segment), workgroups per CU (1: many chunks each)
-    ({"sdig_depth": dd, "sdig_rows": r, "sdig_wg_per_cu": wg, "sdig_waves": nw}, t, outer, inner)
-    for dd, r, wg, nw in ((2, 0, 0, 0), (4, 1, 1, 8), (8, 7, 2, 16), (2, 64, 1, 12), (4, 33, 3, 6),
-                          (2, 5, 2, 16), (6, 16, 2, 12))
-    for t, outer, inner in STREAM_SHAPES
+# Shapes that reach every launch the host makes (one instantiation each):
+#   Q4_K / Q5_K wide kernel, two rows per wave: ragged row counts, 1..3 passes
+#     of 4096 columns, the last one partial;
+#   the persistent wide kernel: >= 8192 rows of at most 4096 columns;
+#   the streamed digit kernel: 8 waves for one segment of 2048 columns and
+#     for 7..8 Q8_0 segments, 12 waves for 2..6 (staged digits shared by two
+#     or more waves of a segment) and 9..12, 16 waves for 7..8 Q6_K / IQ4_NL
+#     segments and 13..16 (waves past the segments idle), partial last
+#     segments, chunks that end inside a workgroup's last round;
+#   rows past 16 segments: the byte-granular kernel.
+LAUNCH_SHAPES = [
+    (synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608), (synth.Q4_K, 9, 8448),
+    (synth.Q4_K, 8195, 4096), (synth.Q5_K, 8199, 2560), (synth.Q4_K, 8192, 256),
+    (synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144), (synth.Q6_K, 33, 10240),
+    (synth.Q6_K, 65, 16384), (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304),
+    (synth.Q8_0, 19, 256), (synth.IQ4_NL, 517, 4608), (synth.Q8_0, 300, 14336),
+    (synth.Q6_K, 300, 24576), (synth.Q8_0, 129, 18688), (synth.Q6_K, 40, 32768),
+    (synth.IQ4_NL, 70, 30720), (synth.Q6_K, 1031, 20480),
+    (synth.Q6_K, 1029, 14336), (synth.IQ4_NL, 260, 16384),
+    (synth.Q8_0, 5, 34816),
 ]
 
 
-def _tuned(knobs, fn):
-    from inferno_hip import _lib
-    for k, v in knobs.items():
-        _lib.set_tuning(k, v)
-    try:
-        return fn()
-    finally:
-        for k in knobs:
-            _lib.set_tuning(k, 0)
-
-
-@pytest.mark.parametrize("knobs,t,outer,inner", TUNING_CASES)
-def test_gemv_every_kernel_variant(knobs, t, outer, inner):
+@pytest.mark.parametrize("t,outer,inner", LAUNCH_SHAPES)
+def test_gemv_every_launch(t, outer, inner):
     from inferno_hip import device as D
-    say(f"gemv {knobs} type={t} {outer}x{inner}")
-    rng = synth.rng_for(sum(knobs.values()) * 131 + t + inner + outer)
+    say(f"gemv type={t} {outer}x{inner}")
+    rng = synth.rng_for(131 + t + inner + outer)
     w = synth.weight(rng, t, outer, inner)
     x = synth.activations(rng, inner)
-    y = _tuned(knobs, lambda: D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy())
+    y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
     ref = oracle.gemv_f64(t, w, x, inner, outer)
     tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
-    assert_within(y, ref, tol, f"{knobs} type {t} {outer}x{inner}")
+    assert_within(y, ref, tol, f"type {t} {outer}x{inner}")
 
 
-@pytest.mark.parametrize("knobs", [{"rows_gateup": 1}, {"rows_gateup": 2}, {"rows_gateup": 4},
-                                   {"wide_fp32": 1}, {"wide_persist": 1},
-                                   {"wide_persist": 1, "pers_bufs": 2, "wide_waves": 4},
-                                   {"wide_persist": -1}])
+@pytest.mark.parametrize("hidden,inter", [
+    (4096, 1030),   # wide kernel, one gate and one up row per wave
+    (8448, 515),    # three passes, the last partial
+    (4096, 8195),   # persistent kernel
+    (2560, 8200),   # persistent kernel, partial pass
+])
 @pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K])
-def test_gate_up_every_kernel_variant(knobs, t):
+def test_gate_up_every_launch(t, hidden, inter):
     from inferno_hip import device as D
-    hidden, inter = 4096, 1030
-    say(f"gate/up {knobs} type={t}")
-    rng = synth.rng_for(sum(knobs.values()) + 17 * t)
+    say(f"gate/up type={t} {hidden}->{inter}")
+    rng = synth.rng_for(inter + 17 * t + hidden)
     wg = synth.weight(rng, t, inter, hidden)
     wu = synth.weight(rng, t, inter, hidden)
     x = synth.activations(rng, hidden)
-    h = _tuned(knobs, lambda: D.gate_up_swiglu(dweight(wg, t, hidden, inter), dweight(wu, t, hidden, inter),
-                                               dev(x)).cpu().numpy())
+    h = D.gate_up_swiglu(dweight(wg, t, hidden, inter), dweight(wu, t, hidden, inter), dev(x)).cpu().numpy()
     g = oracle.gemv_f64(t, wg, x, hidden, inter)
     u = oracle.gemv_f64(t, wu, x, hidden, inter)
     hb = _h_bound(g, u, oracle.row_norms(t, wg, hidden, inter), oracle.row_norms(t, wu, hidden, inter), x)
     assert_within(h, g / (1 + np.exp(-g)) * u, hb, "h")
 
 
-@pytest.mark.parametrize("fp32", [0, 1])
 @pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0])
-def test_gemv_activation_dynamic_range(t, fp32):
+def test_gemv_activation_dynamic_range(t):
     """Sub-blocks of x spread over 10^-30 .. 10^30 (fp32 subnormals included):
     the integer-digit activations scale every 32-element sub-block on its own,
     so small sub-blocks next to huge ones keep their precision."""
-    from inferno_hip import _lib, device as D
-    rng = synth.rng_for(777 + t + 5 * fp32)
+    from inferno_hip import device as D
+    rng = synth.rng_for(777 + t)
     outer, inner = 96, 4096
     w = synth.weight(rng, t, outer, inner)
     x = synth.activations(rng, inner).astype(np.float64)
     x *= np.repeat(10.0 ** rng.uniform(-30, 30, inner // 32), 32)
     x[:32] *= 1e-10  # a subnormal sub-block
     x = x.astype(np.float32)
-    say(f"dynamic range type={t} fp32={fp32}")
-    _lib.set_tuning("wide_fp32", fp32)
-    try:
-        y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
-    finally:
-        _lib.set_tuning("wide_fp32", 0)
+    say(f"dynamic range type={t}")
+    y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
     ref = oracle.gemv_f64(t, w, x, inner, outer)
     tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
     assert_within(y, ref, tol, f"type {t} dynamic range")
     # the small sub-blocks alone (the large ones zeroed) are not lost either
     xs = np.where(np.abs(x) < 1e-20, x, 0).astype(np.float32)
-    _lib.set_tuning("wide_fp32", fp32)
-    try:
-        ys = D.gemv(dweight(w, t, inner, outer), dev(xs)).cpu().numpy()
-    finally:
-        _lib.set_tuning("wide_fp32", 0)
+    ys = D.gemv(dweight(w, t, inner, outer), dev(xs)).cpu().numpy()
     refs = oracle.gemv_f64(t, w, xs, inner, outer)
     tols = oracle.tolerance(oracle.row_norms(t, w, inner, outer), xs)
     assert_within(ys, refs, tols, f"type {t} small sub-blocks only")
 
 
-@pytest.mark.parametrize("fp32", [0, 1])
-def test_gemv_nonfinite_activations(fp32):
+def test_gemv_nonfinite_activations():
     """A NaN or an infinity in x makes every output non-finite (the fp32 sum
     of the reference gives +-Inf or NaN per row; the integer-digit path gives
     NaN for all of them)."""
-    from inferno_hip import _lib, device as D
+    from inferno_hip import device as D
     rng = synth.rng_for(4343)
     outer, inner = 64, 4096
     for t in (synth.Q4_K, synth.Q5_K):
@@ -321,12 +291,8 @@ def test_gemv_nonfinite_activations(fp32):
         for bad in (np.nan, np.inf, -np.inf):
             x = synth.activations(rng, inner)
             x[1234] = bad
-            say(f"nonfinite type={t} fp32={fp32} x[1234]={bad}")
-            _lib.set_tuning("wide_fp32", fp32)
-            try:
-                y = D.gemv(dw, dev(x)).cpu().numpy()
-            finally:
-                _lib.set_tuning("wide_fp32", 0)
+            say(f"nonfinite type={t} x[1234]={bad}")
+            y = D.gemv(dw, dev(x)).cpu().numpy()
             assert not np.any(np.isfinite(y)), (t, bad)
 
 
@@ -391,26 +357,25 @@ def test_ffn_block(hidden, inter, gt, dt):
     assert_within(y, y_ref, 1e-4 * nd * np.linalg.norm(h_ref) + nd * dh, "ffn y")
 
 
-@pytest.mark.parametrize("gt,ut,hidden,inter,knobs", [
-    (synth.Q8_0, synth.Q8_0, 2048, 1030, {}),           # streamed digit kernel, SwiGLU epilogue
-    (synth.Q6_K, synth.Q6_K, 4096, 515, {}),
-    (synth.IQ4_NL, synth.IQ4_NL, 1024, 777, {}),
-    (synth.Q4_K, synth.Q5_K, 1024, 1030, {}),           # mixed pair: wide kernel, SwiGLU epilogue
-    (synth.Q4_K, synth.Q5_K, 4096, 8200, {}),           # mixed pair: persistent kernel (>= 8192 rows)
-    (synth.Q8_0, synth.Q8_0, 2048, 1030, {"sdig_off": 1}),  # fp32 streamed kernel
-    (synth.Q6_K, synth.Q6_K, 768, 301, {}),             # 3-block rows: byte-granular kernel
+@pytest.mark.parametrize("gt,ut,hidden,inter", [
+    (synth.Q8_0, synth.Q8_0, 2048, 1030),           # streamed digit kernel, SwiGLU epilogue
+    (synth.Q6_K, synth.Q6_K, 4096, 515),
+    (synth.IQ4_NL, synth.IQ4_NL, 1024, 777),
+    (synth.Q4_K, synth.Q5_K, 1024, 1030),           # mixed pair: wide kernel, SwiGLU epilogue
+    (synth.Q4_K, synth.Q5_K, 4096, 8200),           # mixed pair: persistent kernel (>= 8192 rows)
+    (synth.Q8_0, synth.Q8_0, 18432, 300),           # 9 segments: 16-wave streamed kernel
+    (synth.Q6_K, synth.Q6_K, 768, 301),             # 3-block rows: byte-granular kernel
 ])
-def test_gate_up_unfused_pairs(gt, ut, hidden, inter, knobs):
+def test_gate_up_unfused_pairs(gt, ut, hidden, inter):
     """Pairs that are not a matching Q4_K/Q5_K pair: the gate GEMV writes g into
     h, and the up GEMV's epilogue makes h = silu(g) * u in place (no scratch)."""
     from inferno_hip import device as D
-    say(f"unfused gate/up gate={gt} up={ut} {hidden}->{inter} {knobs}")
+    say(f"unfused gate/up gate={gt} up={ut} {hidden}->{inter}")
     rng = synth.rng_for(0x6A7E + gt + 3 * ut + inter)
     wg = synth.weight(rng, gt, inter, hidden)
     wu = synth.weight(rng, ut, inter, hidden)
     x = synth.activations(rng, hidden)
-    h = _tuned(knobs, lambda: D.gate_up_swiglu(dweight(wg, gt, hidden, inter),
-                                               dweight(wu, ut, hidden, inter), dev(x)).cpu().numpy())
+    h = D.gate_up_swiglu(dweight(wg, gt, hidden, inter), dweight(wu, ut, hidden, inter), dev(x)).cpu().numpy()
     g = oracle.gemv_f64(gt, wg, x, hidden, inter)
     u = oracle.gemv_f64(ut, wu, x, hidden, inter)
     hb = _h_bound(g, u, oracle.row_norms(gt, wg, hidden, inter), oracle.row_norms(ut, wu, hidden, inter), x)
@@ -474,23 +439,13 @@ def test_fused_elementwise_kernels():
     (synth.Q6_K, 151936, 2048, 0xC2 + 1),
     (synth.Q6_K, 1000, 2048, 5),
     (synth.Q8_0, 32000, 2048, 6),
+    (synth.Q6_K, 4099, 8192, 8),       # four segments: rows meet in LDS per chunk
+    (synth.Q8_0, 3001, 20480, 9),      # ten segments: 16-wave streamed kernel
+    (synth.Q8_0, 777, 34816, 11),      # 17 segments: GEMV + standalone argmax
     (synth.Q4_K, 5003, 1024, 7),       # GEMV + standalone argmax path
 ])
-@pytest.mark.parametrize("knobs", [{}, {"sdig_off": 1}, {"sdig_wg_per_cu": 1, "sdig_rows": 7},
-                                   {"argmax_threads": 64}, {"argmax_threads": 256}])
-def test_lm_head_argmax(t, vocab, hidden, seed, knobs):
-    from inferno_hip import _lib
-    for k, v in knobs.items():
-        _lib.set_tuning(k, v)
-    try:
-        _lm_head_case(t, vocab, hidden, seed, knobs)
-    finally:
-        for k in knobs:
-            _lib.set_tuning(k, 0)
-
-
-def _lm_head_case(t, vocab, hidden, seed, knobs):
-    say(f"lm_head type={t} vocab={vocab} hidden={hidden} seed={seed} {knobs}")
+def test_lm_head_argmax(t, vocab, hidden, seed):
+    say(f"lm_head type={t} vocab={vocab} hidden={hidden} seed={seed}")
     rng = synth.rng_for(seed)
     w = synth.weight(rng, t, vocab, hidden)
     x = synth.activations(rng, hidden)
@@ -605,17 +560,8 @@ def test_argmax_reference_cases(name):
     assert oracle.argmax(v)[0] == want
 
 
-@pytest.mark.parametrize("threads", [0, 64, 256, 1024])
-def test_argmax_errors_and_large_ties(threads):
+def test_argmax_errors_and_large_ties():
     from inferno_hip import FusedKernels as FK, _lib
-    _lib.set_tuning("argmax_threads", threads)
-    try:
-        _argmax_errors_and_large_ties(FK, _lib)
-    finally:
-        _lib.set_tuning("argmax_threads", 0)
-
-
-def _argmax_errors_and_large_ties(FK, _lib):
     for bad in ([1, np.inf], [1, np.nan], [np.nan, np.nan]):
         say(f"argmax error case {bad}")
         with pytest.raises(_lib.IHIPArgumentError):

@@ -9,9 +9,9 @@ x, y and the argmax partials, copies land in the wave's own LDS ring, ring
 reads stay inside a slot, each vmcnt wait covers the item it guards, every
 wave meets the same barriers and every row is produced exactly once.
 
-The launches checked are the ones the GPU tests and the benchmark make (with
-every tuning-knob combination they set), the 151936 x 2048 plain Q6_K GEMV,
-and knob values and CU counts that push the grid to its limits.
+The launches checked are the ones the GPU tests and the benchmark make, the
+151936 x 2048 plain Q6_K GEMV, rows of every segment count the kernel takes
+(1..16), and CU counts that push the grid to its limits.
 """
 import ctypes as C
 from pathlib import Path
@@ -30,32 +30,29 @@ def chk():
         from inferno_hip import build
         build.build_checks()
     L = C.CDLL(str(LIB))
-    L.sdig_check.argtypes = [C.c_int] * 9 + [C.c_char_p, C.c_int, C.POINTER(C.c_longlong)]
+    L.sdig_check.argtypes = [C.c_int] * 5 + [C.c_char_p, C.c_int, C.POINTER(C.c_longlong)]
     L.sdig_check.restype = C.c_longlong
 
-    def run(t, inner, outer, argmax=False, rows=0, depth=0, wg=0, waves=0, ncu=256):
+    def run(t, inner, outer, argmax=False, ncu=256):
         msg = C.create_string_buffer(512)
         st = (C.c_longlong * 8)()
-        n = L.sdig_check(t, inner, outer, int(argmax), rows, depth, wg, waves, ncu, msg, 512, st)
+        n = L.sdig_check(t, inner, outer, int(argmax), ncu, msg, 512, st)
         return n, msg.value.decode(), list(st)
     return run
 
 
 # (type, outer, inner) the GPU tests run through the streamed kernel
 STREAM_SHAPES = ((Q6_K, 1029, 12288), (Q6_K, 77, 6144), (Q6_K, 300, 24576), (Q6_K, 33, 10240),
-                 (Q8_0, 1031, 4096), (Q8_0, 45, 2304), (Q8_0, 19, 256), (IQ4_NL, 517, 4608))
+                 (Q6_K, 65, 16384), (Q8_0, 1031, 4096), (Q8_0, 45, 2304), (Q8_0, 19, 256),
+                 (IQ4_NL, 517, 4608), (Q8_0, 300, 14336), (Q8_0, 129, 18688), (Q6_K, 40, 32768),
+                 (IQ4_NL, 70, 30720), (Q6_K, 1031, 20480), (Q8_0, 300, 18432), (Q6_K, 515, 4096),
+                 (Q8_0, 1030, 2048), (IQ4_NL, 777, 1024), (Q6_K, 1029, 14336), (IQ4_NL, 260, 16384))
 DEFAULT_SHAPES = ((Q6_K, 4096, 12288), (Q6_K, 300, 2048), (Q8_0, 4096, 4096), (Q8_0, 11, 2304),
                   (IQ4_NL, 2048, 1024), (IQ4_NL, 1000, 4096), (IQ4_NL, 13, 2304),
                   (Q6_K, 4096, 4096), (IQ4_NL, 4096, 4096), (Q6_K, 512, 2048), (Q8_0, 256, 4096),
                   (Q6_K, 1, 2048), (Q8_0, 1, 256), (Q6_K, 65, 16384), (Q8_0, 8191, 14336))
-# sdig knob sets of the GPU tests: (depth, rows, workgroups per CU, waves)
-KNOBS = ((2, 0, 0, 0), (4, 1, 1, 8), (8, 7, 2, 16), (2, 64, 1, 12), (4, 33, 3, 6), (2, 5, 2, 16),
-         (6, 16, 2, 12))
-
-
-def _streamed(t, inner):
-    """Rows the host gives this kernel: 1..8 segments of 2048 columns."""
-    return -(-inner // 2048) <= 8
+# lm_head shapes of the GPU tests (vocab, hidden) with the fused argmax
+ARGMAX_SHAPES = ((Q6_K, 1000, 2048), (Q8_0, 32000, 2048), (Q6_K, 4099, 8192), (Q8_0, 3001, 20480))
 
 
 def _ok(res, what):
@@ -75,43 +72,56 @@ def test_lm_head_shape_151936x2048(chk, argmax):
     assert copies == 151936 * 2 * 64  # every wave has >= 2 rows: one pair of 64-lane copies per row
 
 
-def test_lm_head_knob_sets(chk):
-    for argmax in (False, True):
-        for t, vocab in ((Q6_K, 151936), (Q6_K, 1000), (Q8_0, 32000)):
-            for kn in ({}, {"wg": 1, "rows": 7}):
-                _ok(chk(t, 2048, vocab, argmax, **kn), f"type {t} vocab {vocab} {kn} argmax={argmax}")
-
-
 @pytest.mark.parametrize("t,outer,inner", DEFAULT_SHAPES)
 def test_default_launches(chk, t, outer, inner):
     for argmax in (False, True):
         _ok(chk(t, inner, outer, argmax), f"type {t} {outer}x{inner} argmax={argmax}")
 
 
-@pytest.mark.parametrize("knobs", KNOBS)
-def test_tuned_launches(chk, knobs):
-    depth, rows, wg, waves = knobs
-    for t, outer, inner in STREAM_SHAPES + DEFAULT_SHAPES[:4]:
-        if not _streamed(t, inner):
-            continue  # 12 segments: the fp32 streamed kernel takes these rows
-        for argmax in (False, True):
-            _ok(chk(t, inner, outer, argmax, rows=rows, depth=depth, wg=wg, waves=waves),
-                f"type {t} {outer}x{inner} knobs {knobs} argmax={argmax}")
+@pytest.mark.parametrize("t,outer,inner", STREAM_SHAPES)
+def test_gpu_test_launches(chk, t, outer, inner):
+    for argmax in (False, True):
+        _ok(chk(t, inner, outer, argmax), f"type {t} {outer}x{inner} argmax={argmax}")
+
+
+@pytest.mark.parametrize("t,vocab,hidden", ARGMAX_SHAPES)
+def test_fused_argmax_launches(chk, t, vocab, hidden):
+    _ok(chk(t, hidden, vocab, True), f"type {t} vocab {vocab} hidden {hidden}")
+
+
+@pytest.mark.parametrize("t", [Q6_K, Q8_0, IQ4_NL])
+def test_every_segment_count(chk, t):
+    """Rows of 1..16 segments (full and partial last segments): 8 waves for
+    one segment, 12 for 2..6 and 9..12, 16 for 7..8 (Q8_0: 8) and 13..16; two
+    ring slots; 32 rows per chunk for one segment, else 16."""
+    unit = 2048 if t == Q6_K else 256  # the host's row-alignment unit
+    for nseg in range(1, 17):
+        for inner in {2048 * nseg, 2048 * nseg - (2048 - unit)}:
+            st = _ok(chk(t, inner, 1037, False), f"type {t} inner {inner}")
+            want = (8 if nseg == 1 else 12 if nseg <= 6 else (8 if t == Q8_0 else 16) if nseg <= 8
+                    else 12 if nseg <= 12 else 16)
+            assert (st[1], st[2], st[4]) == (want, 2, nseg), (inner, st)
+            assert st[3] == (32 if nseg == 1 else 16), (inner, st)
+    n, msg, _ = chk(t, 2048 * 16 + unit, 7)
+    assert n > 0 and "does not take" in msg  # 17 segments: the byte-granular kernel's
 
 
 def test_argmax_grid_stays_within_the_partials(chk):
-    """One partial per workgroup: whatever the knobs and the CU count, the
-    fused-argmax grid is at most 16384 workgroups (the 256 KiB workspace)."""
-    for ncu in (256, 304, 1024):
-        st = _ok(chk(Q6_K, 2048, 1_000_003, True, rows=1, wg=64, ncu=ncu), f"ncu {ncu}")
-        assert st[0] == 16384
-        st = _ok(chk(Q8_0, 2048, 600_000, True, rows=1, wg=1000, ncu=ncu), f"ncu {ncu}")
-        assert st[0] <= 16384
+    """One partial per workgroup: whatever the CU count, the fused-argmax grid
+    is at most 16384 workgroups (the 256 KiB workspace)."""
+    for ncu in (256, 304, 1024, 4096, 5000):
+        st = _ok(chk(Q6_K, 2048, 1_000_003, True, ncu=ncu), f"ncu {ncu}")
+        assert st[0] == min(16384, 3 * ncu)
+        st = _ok(chk(Q8_0, 8192, 600_000, True, ncu=ncu), f"ncu {ncu}")
+        assert st[0] == min(16384, 4 * ncu)
+        st = _ok(chk(Q8_0, 20480, 600_000, True, ncu=ncu), f"ncu {ncu}")
+        assert st[0] == min(16384, ncu)
 
 
 def test_small_and_odd_devices(chk):
     for ncu in (1, 7, 80):
-        for t, outer, inner in ((Q6_K, 4096, 12288), (Q6_K, 151936, 2048), (Q8_0, 1031, 4096)):
+        for t, outer, inner in ((Q6_K, 4096, 12288), (Q6_K, 151936, 2048), (Q8_0, 1031, 4096),
+                                (Q8_0, 129, 18688)):
             _ok(chk(t, inner, outer, False, ncu=ncu), f"ncu {ncu} type {t} {outer}x{inner}")
 
 
@@ -122,5 +132,5 @@ def test_checker_flags_shapes_the_host_never_sends(chk):
     assert n > 0 and "16-byte" in msg
     n, msg, _ = chk(Q8_0, 480, 7)
     assert n > 0 and "16-byte" in msg
-    n, msg, _ = chk(Q6_K, 2048 * 9, 7)  # nine segments: more than the kernel takes
+    n, msg, _ = chk(Q6_K, 2048 * 17, 7)  # 17 segments: more than the kernel takes
     assert n > 0
