@@ -76,6 +76,8 @@ FFN_CASES = [
     (4096, 12288, synth.Q4_K, synth.Q6_K),   # decode FFN block, full size: fused norm + residual
     (2048, 5632, synth.Q5_K, synth.Q6_K),
     (1024, 2816, synth.Q4_K, synth.Q4_K),    # residual in the wide kernel's epilogue
+    (5120, 1280, synth.Q5_K, synth.Q5_K),    # norm folded into a two-pass gate/up
+    (1024, 8448, synth.Q4_K, synth.Q4_K),    # residual in a three-pass down; persistent gate/up
     (512, 768, synth.Q8_0, synth.Q8_0),      # unfused gate/up: norm kernel first
 ]
 

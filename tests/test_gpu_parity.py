@@ -196,8 +196,8 @@ def test_gemv_host_mirror_and_weight_cache(t):
 
 
 # Shapes that reach every launch the host makes (one instantiation each):
-#   Q4_K / Q5_K wide kernel, two rows per wave: ragged row counts, 1..3 passes
-#     of 4096 columns, the last one partial;
+#   Q4_K / Q5_K wide kernel, two rows per wave: ragged row counts, 1..9
+#     passes of 4096 columns, the last one partial;
 #   the persistent wide kernel: >= 8192 rows of at most 4096 columns;
 #   the streamed digit kernel: 8 waves for one segment of 2048 columns and
 #     for 7..8 Q8_0 segments, 12 waves for 2..6 (staged digits shared by two
@@ -208,6 +208,8 @@ def test_gemv_host_mirror_and_weight_cache(t):
 LAUNCH_SHAPES = [
     (synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608), (synth.Q4_K, 9, 8448),
     (synth.Q4_K, 8195, 4096), (synth.Q5_K, 8199, 2560), (synth.Q4_K, 8192, 256),
+    (synth.Q5_K, 1030, 14336), (synth.Q4_K, 3, 20480), (synth.Q4_K, 1031, 32768),
+    (synth.Q4_K, 4100, 11008), (synth.Q4_K, 33, 36864),
     (synth.Q6_K, 1029, 12288), (synth.Q6_K, 77, 6144), (synth.Q6_K, 33, 10240),
     (synth.Q6_K, 65, 16384), (synth.Q8_0, 1031, 4096), (synth.Q8_0, 45, 2304),
     (synth.Q8_0, 19, 256), (synth.IQ4_NL, 517, 4608), (synth.Q8_0, 300, 14336),
@@ -234,6 +236,7 @@ def test_gemv_every_launch(t, outer, inner):
 @pytest.mark.parametrize("hidden,inter", [
     (4096, 1030),   # wide kernel, one gate and one up row per wave
     (8448, 515),    # three passes, the last partial
+    (14336, 300),   # four passes
     (4096, 8195),   # persistent kernel
     (2560, 8200),   # persistent kernel, partial pass
 ])
