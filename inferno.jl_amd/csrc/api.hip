@@ -313,19 +313,13 @@ int resolve_locked(const void *host, int type, int inner, int outer, const void 
     return IHIP_OK;
 }
 
-// Fast kernels need 16-byte aligned weights and x, and (staged formats)
-// 16-byte aligned rows: Q6_K, Q8_0 and IQ4_NL rows of a multiple of 8 blocks.
-bool fast_ok(int type, const void *w, const float *x, int inner)
+// Fast kernels need 16-byte aligned weights and x.  Rows of any whole number
+// of blocks qualify: the streamed Q6_K / Q8_0 / IQ4_NL kernel copies rows
+// that are not 16-byte multiples from the unit below each segment (which may
+// read up to 14 bytes past the weight's last byte, inside its 16-byte unit).
+bool fast_ok(int, const void *w, const float *x, int)
 {
-    if (!al16(w) || !al16(x))
-        return false;
-    if (type == kIQ4_NL) // 8-block groups of 144 bytes
-        return inner % 256 == 0;
-    if (type == kQ6_K)
-        return inner % 2048 == 0;
-    if (type == kQ8_0)
-        return inner % 256 == 0;
-    return true;
+    return al16(w) && al16(x);
 }
 
 // resid != nullptr: out = epi_apply(resid, W x, epi) row by row: the residual

@@ -552,8 +552,10 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
 // Streamed kernels (Q6_K, Q8_0, IQ4_NL)
 // ------------------------------------------------------------------------
 // A segment is 8 Q6_K blocks (2048 columns, 1680 B), 64 Q8_0 blocks (2176 B)
-// or 64 IQ4_NL blocks (1152 B); rows of a whole number of 8-block groups are
-// 16-byte aligned, which the host checks before choosing these kernels.
+// or 64 IQ4_NL blocks (1152 B), the last of a row possibly fewer.  Rows of
+// any whole number of blocks stream (16-byte aligned W and x); rows whose byte
+// length is not a multiple of 16 leave their segments at byte phases in the
+// ring slots (the PH instantiations).
 template <int FMT>
 struct SFmt;
 template <>
@@ -1011,7 +1013,9 @@ __device__ __forceinline__ void sxd_load(SXD &X, const uint32_t (*d)[64][4], int
 // The walk itself over LDS the caller declares (ring: NW * D * sdig_slot
 // bytes, 16-byte aligned; digs: the staged digits of sdig_share_cap(NW)
 // segments unless ARGMAX; part: kSdigMaxRows x NW; wkey / wflag: NW each).
-template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
+// PH: rows that are not 16-byte multiples (segments at a byte phase in their
+// slots); without it every phase is 0 and the lane offsets are fixed.
+template <int FMT, int NW, int D, bool ARGMAX, bool RESID, bool PH>
 __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const float *x, float *y,
                                          int outer, int nblk, int rpc, ArgPart *__restrict__ parts,
                                          const float *resid, int epi, uint8_t *ring,
@@ -1041,13 +1045,17 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
     const bool share = g.share, producer = g.producer;
     const int seg_blocks = g.seg_blocks, nitems = g.nitems;
 
-    // item k's row segment into slot k % D
+    // item k's row segment into slot k % D, from the 16-byte unit at or below
+    // its first byte
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
     auto issue = [&](int k) {
-        const uint8_t *src = W + sdig_copy_row(g, FMT, k, bid, grid, rpc, outer);
+        const size_t off = sdig_copy_row(g, FMT, k, bid, grid, rpc, outer);
+        const uint32_t ph = PH ? sdig_phase(off) : 0u;
+        const int units = sdig_units(g, ph);
+        const uint8_t *src = W + (off - ph);
 #pragma unroll
         for (int i = 0; i < IPR; ++i)
-            lds_copy16(src + sdig_copy_lane(g, i, lane), ring_lds + sdig_copy_dst(g, FMT, D, k, i));
+            lds_copy16(src + sdig_copy_lane(units, i, lane), ring_lds + sdig_copy_dst(g, FMT, D, k, i));
     };
 
     // x first, then the first D rows' copies, all in flight together; the
@@ -1055,7 +1063,7 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
     float4 xv[8];
     bool xact = false;
     if (producer) // wave-uniform
-        xact = staged_dig_issue<FMT>(x + (size_t)sg * 2048, lane, seg_blocks, xv);
+        xact = staged_dig_issue<FMT>(x + g.x0, lane, seg_blocks, xv);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < D; ++k)
@@ -1095,18 +1103,19 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
     for (int ci = 0; ci < g.my_chunks; ++ci) {
         const SdigChunk c = sdig_chunk(g, ci, bid, grid, rpc, outer);
         const int row0 = c.row0, nrows = c.nrows, mine = c.mine;
-        // the lane's share of the dot product of the row in ring slot `slot`
-        auto dot_at = [&](uint32_t slot) {
+        // the lane's share of the dot product of the row segment at byte phase
+        // ph of ring slot `slot`
+        auto dot_at = [&](uint32_t slot, uint32_t ph) {
             float v = 0.0f;
             if constexpr (FMT == kQ6_K) {
                 if ((lane >> 3) < seg_blocks)
-                    v = q6_dot_dig(ring + slot, q6l, X);
+                    v = q6_dot_dig(ring + slot, PH ? q6_dig_lane_at(q6l, ph) : q6l, X);
             } else if constexpr (FMT == kIQ4_NL) {
                 if (lane < seg_blocks)
-                    v = iq4nl_dot_dig(ring + slot, sdig_blk_off(FMT, lane), X);
+                    v = iq4nl_dot_dig(ring + slot, sdig_blk_off(FMT, lane) + ph, X);
             } else {
                 if (lane < seg_blocks)
-                    v = q80_dot_dig(ring + slot, sdig_blk_off(FMT, lane), X);
+                    v = q80_dot_dig(ring + slot, sdig_blk_off(FMT, lane) + ph, X);
             }
             return v;
         };
@@ -1124,8 +1133,9 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
             }
         };
         for (int rr = 0; rr < mine; ++rr, ++k) {
+            const uint32_t ph = PH ? sdig_phase(sdig_seg_off(g, FMT, row0 + sdig_chunk_row(g, rr))) : 0u;
             wait_vmcnt(IPR * sdig_wait_items(g, D, k));
-            finish(rr, wave_sum(dot_at(sdig_copy_dst(g, FMT, D, k, 0))));
+            finish(rr, wave_sum(dot_at(sdig_copy_dst(g, FMT, D, k, 0), ph)));
             if (k + D < nitems)
                 issue(k + D); // slot k % D has been read
         }
@@ -1171,7 +1181,7 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
     __builtin_amdgcn_s_waitcnt(0); // every copy has landed before the workgroup ends
 }
 
-template <int FMT, int NW, int D, bool ARGMAX, bool RESID>
+template <int FMT, int NW, int D, bool ARGMAX, bool RESID, bool PH>
 __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict__ W,
                                                        const float *x, float *y, int outer, int nblk,
                                                        int rpc, ArgPart *__restrict__ parts,
@@ -1183,8 +1193,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
     __shared__ float part[kSdigMaxRows][NW]; // one column per segment (nseg <= NW)
     __shared__ unsigned long long wkey[NW];
     __shared__ uint32_t wflag[NW];
-    sdig_run<FMT, NW, D, ARGMAX, RESID>(W, x, y, outer, nblk, rpc, parts, resid, epi, ring, digs, part,
-                                        wkey, wflag);
+    sdig_run<FMT, NW, D, ARGMAX, RESID, PH>(W, x, y, outer, nblk, rpc, parts, resid, epi, ring, digs,
+                                            part, wkey, wflag);
 }
 
 // ------------------------------------------------------------------------
@@ -1233,16 +1243,26 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
     return hipGetLastError();
 }
 
+template <int FMT, bool ARGMAX, int NWV, bool PH>
+static void launch_sdig_ph(const void *w, const float *x, float *y, int nblk, int outer,
+                           const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
+{
+    if (!ARGMAX && resid) // the lm_head has no residual
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, !ARGMAX, PH>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+    else
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, false, PH>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+}
+
 template <int FMT, bool ARGMAX, int NWV>
 static void launch_sdig_nw(const void *w, const float *x, float *y, int nblk, int outer,
                            const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
 {
-    if (resid)
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, true>), dim3(p.grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+    if (sdig_phased(FMT, nblk))
+        launch_sdig_ph<FMT, ARGMAX, NWV, true>(w, x, y, nblk, outer, p, parts, s, resid, epi);
     else
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, false>), dim3(p.grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+        launch_sdig_ph<FMT, ARGMAX, NWV, false>(w, x, y, nblk, outer, p, parts, s, resid, epi);
 }
 
 // Q6_K / Q8_0 / IQ4_NL rows of 1..16 segments through the streamed digit

@@ -9,12 +9,22 @@
 // arithmetic the kernel runs.
 //
 // Geometry.  K is cut into segments of 2048 columns (8 Q6_K blocks of 210 B,
-// 64 Q8_0 blocks of 34 B, 64 IQ4_NL blocks of 18 B: 16-byte multiples).  A
+// 64 Q8_0 blocks of 34 B, 64 IQ4_NL blocks of 18 B; the last may be shorter).
+// A wave's time per row segment is its instruction count whatever the number
+// of active lanes, so a short last segment is not worth evening out.  A
 // workgroup of NW waves walks chunks of `rpc` rows grid-stride.  Wave w owns
 // segment w % nseg and, when there are more waves than segments, every
 // (NW / nseg)-th row of a chunk; its rows of all its chunks are numbered
 // items k = 0, 1, ... and stream through a private D-slot LDS ring (slot
 // k % D) by direct-to-LDS copies of 64 lanes x 16 bytes.
+//
+// Rows need not be 16-byte multiples (Q6_K rows of any block count, Q8_0 and
+// IQ4_NL rows of any multiple of 32 columns): a row segment is copied from the
+// 16-byte unit at or below its first byte, so it sits in its slot at a byte
+// phase of 0..14 (even: every block size is even), which the dot adds to its
+// offsets.  The copies read whole aligned units: the matrix's last unit may
+// reach up to 14 bytes past W's last byte, inside the 16-byte unit (and so the
+// page) that holds that byte; those bytes are never used.
 #pragma once
 
 #include "kq_common.h"
@@ -44,13 +54,22 @@ __host__ __device__ constexpr int sdig_slot(int fmt) { return sdig_ipr(fmt) * 10
 // segments whose digits can be staged in LDS for the segment's other waves
 __host__ __device__ constexpr int sdig_share_cap(int nw) { return nw == 12 ? 6 : nw == 8 ? 2 : 0; }
 
-// Whether NW waves with D ring slots fit the 160 KB of LDS: the ring, the
-// staged digits, the chunk partial sums (one column per wave) and 2 KB for
-// the rest.
+// LDS of a workgroup of NW waves with D ring slots: the ring, the staged
+// digits (none with the argmax), the chunk partial sums (one column per wave)
+// and 2 KB for the rest; it must fit the 160 KB of a CU.
+__host__ __device__ constexpr int sdig_lds(int fmt, int nw, int d, bool argmax)
+{
+    return nw * d * sdig_slot(fmt) + (argmax ? 0 : sdig_share_cap(nw) * kDigQuads * 1024) +
+           kSdigMaxRows * nw * 4 + 2048;
+}
 __host__ __device__ constexpr bool sdig_fits(int fmt, int nw, int d)
 {
-    return nw * d * sdig_slot(fmt) + sdig_share_cap(nw) * kDigQuads * 1024 + kSdigMaxRows * nw * 4 +
-               2048 <= 160 * 1024;
+    return sdig_lds(fmt, nw, d, false) <= 160 * 1024;
+}
+
+__host__ __device__ inline int sdig_nseg(int fmt, int nblk)
+{
+    return (nblk + sdig_seg_blocks(fmt) - 1) / sdig_seg_blocks(fmt);
 }
 
 // One wave's share of a launch.
@@ -63,7 +82,8 @@ struct SdigWave {
     bool producer;   // this wave loads x and forms the digits
     int nchunks;     // chunks of the whole matrix
     int seg_blocks;  // blocks of this wave's segment
-    int chunks16;    // 16-byte units of the segment (whole 8-block groups: host-checked)
+    int seg_len;     // bytes of this wave's segment
+    int x0;          // first column (element of x) of this wave's segment
     uint32_t my_ring;// LDS byte offset of this wave's ring within the ring array
     int m;           // rows per full chunk
     int my_chunks;   // chunks of this workgroup
@@ -76,9 +96,9 @@ __host__ __device__ inline SdigWave sdig_wave(int fmt, int NW, int D, int SHC, i
                                               int rpc, int bid, int grid, int w)
 {
     SdigWave g;
-    const int sb = sdig_seg_blocks(fmt), bb = block_bytes(fmt);
+    const int bb = block_bytes(fmt);
     g.row_bytes = (size_t)nblk * bb;
-    g.nseg = (nblk + sb - 1) / sb;
+    g.nseg = sdig_nseg(fmt, nblk);
     g.wps = NW / g.nseg;
     g.sg = w % g.nseg;
     g.rl = w / g.nseg;
@@ -86,8 +106,9 @@ __host__ __device__ inline SdigWave sdig_wave(int fmt, int NW, int D, int SHC, i
     g.share = SHC > 0 && g.nseg <= SHC && g.wps >= 2;
     g.producer = !g.share || g.rl == 0;
     g.nchunks = (outer + rpc - 1) / rpc;
-    g.seg_blocks = sd_min(sb, nblk - g.sg * sb);
-    g.chunks16 = g.seg_blocks * bb / 16;
+    g.seg_blocks = sd_min(sdig_seg_blocks(fmt), nblk - g.sg * sdig_seg_blocks(fmt));
+    g.seg_len = g.seg_blocks * bb;
+    g.x0 = g.sg * sdig_seg_blocks(fmt) * block_elems(fmt);
     g.my_ring = (uint32_t)(w * D * sdig_slot(fmt));
     g.m = g.worker ? (rpc - g.rl + g.wps - 1) / g.wps : 0;
     g.my_chunks = bid < g.nchunks ? (g.nchunks - 1 - bid) / grid + 1 : 0;
@@ -109,21 +130,35 @@ __host__ __device__ inline int sdig_item_row(const SdigWave &g, int k, int bid, 
     return sd_min((bid + ci * grid) * rpc + g.rl + rr * g.wps, outer - 1);
 }
 
+// Byte offset in W of this wave's segment of `row`.
+__host__ __device__ inline size_t sdig_seg_off(const SdigWave &g, int fmt, int row)
+{
+    return (size_t)g.sg * (size_t)sdig_seg_bytes(fmt) + (size_t)row * g.row_bytes;
+}
 // Byte offset in W of the row segment copied for item k: items past the
 // wave's last re-copy its last item's row into a slot no remaining item uses.
 __host__ __device__ inline size_t sdig_copy_row(const SdigWave &g, int fmt, int k, int bid, int grid,
                                                 int rpc, int outer)
 {
     const int kk = sd_max(0, sd_min(k, g.nitems - 1));
-    return (size_t)g.sg * sdig_seg_bytes(fmt) + (size_t)sdig_item_row(g, kk, bid, grid, rpc, outer) * g.row_bytes;
+    return sdig_seg_off(g, fmt, sdig_item_row(g, kk, bid, grid, rpc, outer));
 }
-// Byte offset within the row segment of lane `lane`'s 16 bytes in copy i:
-// every copy runs with all 64 lanes on (lanes past the segment re-read its
-// last 16 bytes into the slot's tail), so the copies in flight are a
-// compile-time count.
-__host__ __device__ inline uint32_t sdig_copy_lane(const SdigWave &g, int i, int lane)
+// Whether rows of nblk blocks leave segments off 16-byte boundaries.
+__host__ __device__ constexpr bool sdig_phased(int fmt, int nblk) { return (nblk * block_bytes(fmt)) % 16 != 0; }
+// Where a segment at byte offset `off` of W lands in its slot (0..15; even),
+// and the 16-byte units its copies cover, from the unit at off - phase.
+__host__ __device__ inline uint32_t sdig_phase(size_t off) { return (uint32_t)(off & 15u); }
+__host__ __device__ inline int sdig_units(const SdigWave &g, uint32_t phase)
 {
-    return 16u * (uint32_t)sd_min(64 * i + lane, g.chunks16 - 1);
+    return ((int)phase + g.seg_len + 15) >> 4;
+}
+// Byte offset, from the segment's first unit, of lane `lane`'s 16 bytes in
+// copy i: every copy runs with all 64 lanes on (lanes past the segment
+// re-read its last unit into the slot's tail), so the copies in flight are a
+// compile-time count.
+__host__ __device__ inline uint32_t sdig_copy_lane(int units, int i, int lane)
+{
+    return 16u * (uint32_t)sd_min(64 * i + lane, units - 1);
 }
 // LDS byte offset (within the ring array) where copy i of item k lands; lane
 // l's 16 bytes go to this + 16 l.
@@ -171,6 +206,22 @@ struct Q6DigLane {
     uint32_t a, h, s, d, sh;
     int c; // which 16 of the lane's 32 elements' scale: l0 >> 4
 };
+
+// The same lane's offsets for a segment at byte phase ph (even, 0..14) of its
+// slot: the byte positions move by ph, so the dword-aligned offsets move by
+// ph rounded down to 4 (plus 4 when the 2-byte phases add up to 4) and the
+// byte phase of the reads becomes (sh + ph) mod 4.
+__host__ __device__ inline Q6DigLane q6_dig_lane_at(Q6DigLane L, uint32_t ph)
+{
+    const uint32_t t = L.sh + (ph & 3u);
+    const uint32_t o = (ph & ~3u) + (t & 4u);
+    L.a += o;
+    L.h += o;
+    L.s += o;
+    L.d += ph;
+    L.sh = t & 3u;
+    return L;
+}
 
 __host__ __device__ inline Q6DigLane q6_dig_lane(int lane)
 {
@@ -220,7 +271,9 @@ struct SdigPlan {
 // previous plan in parentheses where it differed):
 //   1 segment     8 waves, 32 rows, 3 per CU: the 151936 x 2048 Q6_K lm_head
 //                 (54-55 us; 57 with 4 per CU).  Rows finish inside their wave.
-//   2..6          12 waves, 16 rows, 4 per CU: 4096 x 4096 Q8_0 6.47, Q6_K 6.48,
+//   2..6          12 waves, 16 rows, 1 per CU (all of 113-137 KB of LDS a CU
+//                 holds; 4 per CU queued three more in rounds: 12288 x 4096
+//                 Q6_K 11.2 us against 15.6): 4096 x 4096 Q8_0 6.47, Q6_K 6.48,
 //                 IQ4_NL 6.23 (8 waves: 6.95+); 4096 x 6144 Q6_K 8.17;
 //                 4096 x 8192 Q8_0 9.67 (16.0); 4096 x 10240 Q8_0 12.70
 //                 (18.7); 4096 x 12288 Q6_K 12.3-12.4 (6 waves: 14.3).
@@ -233,8 +286,9 @@ struct SdigPlan {
 //                 waves 21.3), 4096 x 20480 Q8_0 21.9 (23.0).
 //   13..16        16 waves, 16 rows, 1 per CU: 8192 x 28672 Q6_K 42.6 (2 per
 //                 CU 46.5), 4096 x 32768 Q8_0 30.7.
-// Rows of several segments meet in LDS once per chunk; the sweeps' best
-// chunk was 16 rows throughout (4 and 8 lost 0.5-7 us, 32 up to 10 us).
+// Rows of several segments meet in LDS once per chunk; at 4096 rows the
+// sweeps' best chunk was 16 rows throughout (4 and 8 lost 0.5-7 us, 32 up to
+// 10 us).  Other row counts: sdig_plan.
 inline int sdig_waves(int fmt, int nseg)
 {
     return nseg == 1 ? 8 : nseg <= 6 ? 12 : nseg <= 8 ? (fmt == kQ8_0 ? 8 : 16) : nseg <= 12 ? 12 : 16;
@@ -242,7 +296,7 @@ inline int sdig_waves(int fmt, int nseg)
 inline int sdig_rows(int nseg) { return nseg == 1 ? 32 : 16; }
 inline int sdig_wg_per_cu(int fmt, int nseg)
 {
-    return nseg == 1 ? 3 : nseg <= 6 ? 4 : nseg <= 8 ? (fmt == kQ8_0 ? 4 : 2) : 1;
+    return nseg == 1 ? 3 : nseg <= 6 ? 1 : nseg <= 8 ? (fmt == kQ8_0 ? 4 : 2) : 1;
 }
 
 // Whether the streamed kernel takes rows of nblk blocks: 1..16 segments.
@@ -258,15 +312,32 @@ inline bool sdig_rows_ok(int fmt, int nblk)
 inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, int ncu)
 {
     SdigPlan p;
-    p.nseg = (nblk + sdig_seg_blocks(fmt) - 1) / sdig_seg_blocks(fmt);
+    p.nseg = sdig_nseg(fmt, nblk);
+    p.nw = sdig_waves(fmt, p.nseg);
+    p.d = 2;
     p.rpc = sd_min(sdig_rows(p.nseg), kSdigMaxRows);
-    const int nchunks = (outer + p.rpc - 1) / p.rpc;
-    int grid = sd_max(1, sd_min(nchunks, sd_max(1, ncu) * sdig_wg_per_cu(fmt, p.nseg)));
+    const int ncu1 = sd_max(1, ncu);
+    int per_cu = sdig_wg_per_cu(fmt, p.nseg);
+    // Two-segment rows of more chunks than one 12-wave workgroup per CU holds
+    // at once: 8-wave workgroups, two per CU, keep 16 waves working on a CU
+    // instead of 12 (12288 x 4096 Q6_K 10.75 us against 11.2; 9728 x 2560
+    // 10.96 against 11.6).
+    if (p.nseg == 2 && (outer + p.rpc - 1) / p.rpc > ncu1) {
+        p.nw = 8;
+        per_cu = 2;
+    }
+    const int resident = ncu1 * per_cu;
+    // rows of the busiest resident slot with r rows per chunk
+    auto busiest = [&](int r) { return ((outer + r - 1) / r + resident - 1) / resident * r; };
+    // 12 or 16 waves: 8-row chunks where 16-row chunks spill past one round
+    // of resident workgroups unevenly (5120 x 17408 Q6_K: 320 chunks of 16 on
+    // 256 workgroups, 29.0 us with 8-row chunks against 36.8)
+    if (p.nw >= 12 && p.nseg > 1 && (outer + 15) / 16 > resident && busiest(8) < busiest(16))
+        p.rpc = 8;
+    int grid = sd_max(1, sd_min((outer + p.rpc - 1) / p.rpc, ncu1 * per_cu));
     if (argmax)
         grid = sd_min(grid, kArgMaxParts);
     p.grid = grid;
-    p.nw = sdig_waves(fmt, p.nseg);
-    p.d = 2;
     return p;
 }
 

@@ -6,7 +6,11 @@
 // launch exactly as the kernel does -- every workgroup, wave, item, copy and
 // lane -- asserting that
 //   * every global byte read (x loads, row copies) and written (y, argmax
-//     partials) lies inside its buffer;
+//     partials) lies inside its buffer -- the row copies, which read whole
+//     aligned 16-byte units, inside W or the 16-byte unit holding W's last
+//     byte -- and every copy covers its row segment;
+//   * shapes the host sends to the unphased kernel have every segment on a
+//     16-byte boundary;
 //   * every direct-to-LDS copy lands inside the wave's own ring, and every
 //     ring read of the dot lies inside the slot;
 //   * the explicit vmcnt wait before reading item k never allows more copies
@@ -75,6 +79,7 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
     const int IPR = sdig_ipr(fmt), SLOT = sdig_slot(fmt), bb = block_bytes(fmt);
     const int SHC = argmax ? 0 : sdig_share_cap(NW);
     const size_t row_bytes = (size_t)nblk * bb, w_bytes = (size_t)outer * row_bytes;
+    const size_t w_units_end = (w_bytes + 15) & ~(size_t)15; // end of the unit holding W's last byte
     const int ring_bytes = NW * D * SLOT;
 
     // the instantiations the launcher can dispatch, and their LDS
@@ -92,11 +97,20 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
         R.fail("grid %d > %d argmax partials", grid, kArgMaxParts);
     if (SLOT < sdig_seg_bytes(fmt) + 16)
         R.fail("slot %d < segment %d + 16", SLOT, sdig_seg_bytes(fmt));
-    for (int s = 0; s < p.nseg; ++s) {
-        const int sb = sd_min(sdig_seg_blocks(fmt), nblk - s * sdig_seg_blocks(fmt));
-        if ((sb * bb) % 16)
-            R.fail("segment %d is %d bytes, not whole 16-byte units (the host routes such rows "
-                   "to the byte-granular kernel)", s, sb * bb);
+    const bool phased = sdig_phased(fmt, nblk);
+    // the segments tile the row: contiguous, non-empty, at most 2048 columns
+    {
+        int next = 0;
+        for (int s = 0; s < p.nseg; ++s) {
+            const SdigWave g = sdig_wave(fmt, NW, D, 0, outer, nblk, rpc, 0, grid, s);
+            if (g.sg != s || g.x0 != next * block_elems(fmt) || g.seg_blocks < 1 ||
+                g.seg_blocks > sdig_seg_blocks(fmt))
+                R.fail("segment %d: first block %d, %d blocks (expected first block %d)", s,
+                       g.x0 / block_elems(fmt), g.seg_blocks, next);
+            next += g.seg_blocks;
+        }
+        if (next != nblk)
+            R.fail("segments cover %d of %d blocks", next, nblk);
     }
     if (R.errors)
         return R.errors;
@@ -114,7 +128,7 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
             if (g.producer) {
                 for (int lane = 0; lane < 64; ++lane) {
                     bool act = false;
-                    const int base = g.sg * 2048 + sdig_x_lane(fmt, lane, g.seg_blocks, act);
+                    const int base = g.x0 + sdig_x_lane(fmt, lane, g.seg_blocks, act);
                     for (int t = 0; t < 8; ++t) {
                         const long long f0 = base + sdig_x_load_byte(fmt, t) / 4;
                         if (f0 < 0 || f0 + 4 > inner)
@@ -128,7 +142,17 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
             // copies: items [0, max(D, nitems)) are issued (the prologue issues D)
             const int nissue = sd_max(D, g.nitems);
             for (int k = 0; k < nissue; ++k) {
-                const size_t row = sdig_copy_row(g, fmt, k, bid, grid, rpc, outer);
+                const size_t off = sdig_copy_row(g, fmt, k, bid, grid, rpc, outer);
+                const uint32_t ph = sdig_phase(off);
+                const int units = sdig_units(g, ph);
+                if (!phased && ph)
+                    R.fail("wg %d wave %d item %d: segment at phase %u in the unphased kernel", bid, w, k, ph);
+                if (ph & 1)
+                    R.fail("odd phase %u", ph);
+                if (16 * units < (int)ph + g.seg_len || units > 64 * IPR)
+                    R.fail("wg %d wave %d item %d: %d units for a %d-byte segment at phase %u (%d copies)",
+                           bid, w, k, units, g.seg_len, ph, IPR);
+                const size_t row = off - ph; // the first unit
                 for (int i = 0; i < IPR; ++i) {
                     const uint32_t dst = sdig_copy_dst(g, fmt, D, k, i);
                     if (dst < g.my_ring || dst + 1024u > g.my_ring + (uint32_t)(D * SLOT) ||
@@ -137,44 +161,56 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
                                "[%u, %u)", bid, w, k, i, dst, dst + 1024u, g.my_ring,
                                g.my_ring + (uint32_t)(D * SLOT));
                     for (int lane = 0; lane < 64; ++lane) {
-                        const size_t src = row + sdig_copy_lane(g, i, lane);
+                        const size_t src = row + sdig_copy_lane(units, i, lane);
                         ++copies;
-                        if (src + 16 > w_bytes)
+                        if (src % 16 || src + 16 > w_units_end)
                             R.fail("wg %d wave %d item %d copy %d lane %d: W bytes [%zu, %zu) of %zu",
                                    bid, w, k, i, lane, src, src + 16, w_bytes);
-                        // inside this wave's segment of one row
-                        const size_t in_row = src % row_bytes;
-                        const size_t s0 = (size_t)g.sg * sdig_seg_bytes(fmt);
-                        if (in_row < s0 || in_row + 16 > s0 + (size_t)g.seg_blocks * bb)
-                            R.fail("wg %d wave %d item %d copy %d lane %d: bytes %zu..%zu of a row "
-                                   "are outside segment %d", bid, w, k, i, lane, in_row, in_row + 16, g.sg);
+                        // inside the units that hold this wave's segment of one row
+                        if (src < row || src + 16 > row + 16 * (size_t)units)
+                            R.fail("wg %d wave %d item %d copy %d lane %d: bytes [%zu, %zu) outside "
+                                   "the segment's units [%zu, %zu)", bid, w, k, i, lane, src, src + 16,
+                                   row, row + 16 * (size_t)units);
                         if (src + 16 > w_hi)
                             w_hi = src + 16;
                     }
                 }
             }
-            // ring reads of the dot (relative to a slot)
-            for (int lane = 0; lane < 64; ++lane) {
-                uint32_t hi = 0;
-                if (fmt == kQ6_K) {
-                    if ((lane >> 3) >= g.seg_blocks)
-                        continue;
-                    const Q6DigLane L = q6_dig_lane(lane);
-                    const uint32_t ends[] = {L.a + 12, L.a + 32 + 12, L.h + 12, L.s + 12, L.d + 2};
-                    for (uint32_t e : ends)
-                        hi = e > hi ? e : hi;
-                } else {
-                    if (lane >= g.seg_blocks)
-                        continue;
-                    const uint32_t o = sdig_blk_off(fmt, lane);
-                    hi = ((o + 2) & ~3u) + 4u * (uint32_t)sdig_blk_dwords(fmt);
-                    hi = o + 2 > hi ? o + 2 : hi;
+            // ring reads of the dot (relative to a slot), at every phase the
+            // kernel can meet: the bytes it uses lie inside the block at that
+            // phase, and every read stays inside the slot
+            for (uint32_t ph = 0; ph < (phased ? 16u : 1u); ph += 2) {
+                for (int lane = 0; lane < 64; ++lane) {
+                    uint32_t hi = 0;
+                    if (fmt == kQ6_K) {
+                        if ((lane >> 3) >= g.seg_blocks)
+                            continue;
+                        const Q6DigLane L0 = q6_dig_lane(lane);
+                        const Q6DigLane L = phased ? q6_dig_lane_at(L0, ph) : L0;
+                        const uint32_t bs = lane >> 3, n = (lane >> 2) & 1, l0 = 8 * (lane & 3);
+                        const uint32_t blk = ph + 210u * bs; // the block's first byte in the slot
+                        // the 8 bytes each read uses, and d
+                        if (L.a + L.sh != blk + 64 * n + l0 || L.h + L.sh != blk + 128 + 32 * n + l0 ||
+                            L.s + L.sh != blk + 192 + 8 * n || L.d != blk + 208 || L.sh > 2 || L.a % 4 ||
+                            L.h % 4 || L.s % 4)
+                            R.fail("phase %u lane %d: Q6_K offsets a %u h %u s %u d %u sh %u for block at %u",
+                                   ph, lane, L.a, L.h, L.s, L.d, L.sh, blk);
+                        const uint32_t ends[] = {L.a + 12, L.a + 32 + 12, L.h + 12, L.s + 12, L.d + 2};
+                        for (uint32_t e : ends)
+                            hi = e > hi ? e : hi;
+                    } else {
+                        if (lane >= g.seg_blocks)
+                            continue;
+                        const uint32_t o = sdig_blk_off(fmt, lane) + ph;
+                        hi = ((o + 2) & ~3u) + 4u * (uint32_t)sdig_blk_dwords(fmt);
+                        hi = o + 2 > hi ? o + 2 : hi;
+                    }
+                    if (hi > (uint32_t)SLOT)
+                        R.fail("wave %d lane %d phase %u: the dot reads up to byte %u of a %d-byte slot", w,
+                               lane, ph, hi, SLOT);
+                    if (hi > (uint32_t)(IPR * 1024))
+                        R.fail("lane %d reads past the copied bytes of a slot", lane);
                 }
-                if (hi > (uint32_t)SLOT)
-                    R.fail("wave %d lane %d: the dot reads up to byte %u of a %d-byte slot", w, lane,
-                           hi, SLOT);
-                if (hi > (uint32_t)(IPR * 1024))
-                    R.fail("lane %d reads past the copied bytes of a slot", lane);
             }
             // the item walk: waits, rows, partial sums
             int k = 0, barriers = g.share ? 1 : 0;
@@ -199,6 +235,10 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
                     if (sdig_item_row(g, k, bid, grid, rpc, outer) != row)
                         R.fail("wg %d wave %d item %d: read row %d, copied row %d", bid, w, k, row,
                                sdig_item_row(g, k, bid, grid, rpc, outer));
+                    // the phase the dot adds is the phase the copy left
+                    if (sdig_phase(sdig_seg_off(g, fmt, row)) !=
+                        sdig_phase(sdig_copy_row(g, fmt, k, bid, grid, rpc, outer)))
+                        R.fail("wg %d wave %d item %d: dot phase differs from the copy's", bid, w, k);
                     if (p.nseg == 1) {
                         if (row >= 0 && row < outer)
                             seen_row[(size_t)row]++;

@@ -78,6 +78,7 @@ FFN_CASES = [
     (1024, 2816, synth.Q4_K, synth.Q4_K),    # residual in the wide kernel's epilogue
     (5120, 1280, synth.Q5_K, synth.Q5_K),    # norm folded into a two-pass gate/up
     (1024, 8448, synth.Q4_K, synth.Q4_K),    # residual in a three-pass down; persistent gate/up
+    (2560, 9728, synth.Q4_K, synth.Q6_K),    # down rows of 38 blocks at byte phases
     (512, 768, synth.Q8_0, synth.Q8_0),      # unfused gate/up: norm kernel first
 ]
 

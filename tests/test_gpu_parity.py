@@ -145,14 +145,14 @@ GEMV_CASES = [
     (synth.Q6_K, 4096, 12288),    # FFN down shape
     (synth.Q6_K, 300, 2048),
     (synth.Q6_K, 151936, 2048),   # the lm_head shape as a plain GEMV (one segment, staged digits)
-    (synth.Q6_K, 7, 768),         # row stride not 16-byte aligned -> generic kernel
+    (synth.Q6_K, 7, 768),         # rows of 630 bytes: segments at byte phases (streamed kernel)
     (synth.Q8_0, 4096, 4096),
     (synth.Q8_0, 11, 2304),       # partial 64-block segment
-    (synth.Q8_0, 6, 96),          # generic kernel
+    (synth.Q8_0, 6, 96),          # 3 blocks a row, at byte phases
     (synth.IQ4_NL, 2048, 1024),   # an SSM-projection-sized IQ4_NL matrix
     (synth.IQ4_NL, 1000, 4096),   # two 64-block segments per row
     (synth.IQ4_NL, 13, 2304),     # partial segment (72 blocks)
-    (synth.IQ4_NL, 5, 96),        # generic kernel
+    (synth.IQ4_NL, 5, 96),        # 3 blocks a row, at byte phases
 ]
 
 
@@ -204,6 +204,9 @@ def test_gemv_host_mirror_and_weight_cache(t):
 #     or more waves of a segment) and 9..12, 16 waves for 7..8 Q6_K / IQ4_NL
 #     segments and 13..16 (waves past the segments idle), partial last
 #     segments, chunks that end inside a workgroup's last round;
+#   rows that are not 16-byte multiples (Q6_K rows of any block count, Q8_0 and
+#     IQ4_NL rows of any multiple of 32 columns): segments copied from the
+#     unit below them, at byte phases 2..14, 1 to 16 segments;
 #   rows past 16 segments: the byte-granular kernel.
 LAUNCH_SHAPES = [
     (synth.Q4_K, 1037, 4096), (synth.Q5_K, 515, 4608), (synth.Q4_K, 9, 8448),
@@ -216,8 +219,28 @@ LAUNCH_SHAPES = [
     (synth.Q6_K, 300, 24576), (synth.Q8_0, 129, 18688), (synth.Q6_K, 40, 32768),
     (synth.IQ4_NL, 70, 30720), (synth.Q6_K, 1031, 20480),
     (synth.Q6_K, 1029, 14336), (synth.IQ4_NL, 260, 16384),
+    (synth.Q6_K, 1029, 9728), (synth.Q6_K, 300, 2560), (synth.Q6_K, 5, 256), (synth.Q6_K, 77, 17408),
+    (synth.Q6_K, 33, 2304), (synth.Q8_0, 13, 896), (synth.Q8_0, 1000, 2336), (synth.IQ4_NL, 9, 2336),
+    (synth.IQ4_NL, 517, 4640), (synth.Q6_K, 1031, 32512), (synth.Q8_0, 3, 32),
     (synth.Q8_0, 5, 34816),
 ]
+
+
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q6_K, synth.Q8_0])
+def test_gemv_misaligned_weight_pointer(t):
+    """A weight at an address that is not 16-byte aligned takes the
+    byte-granular kernel and gives the same sums."""
+    from inferno_hip import device as D
+    outer, inner = 37, 2560
+    say(f"gemv misaligned weight type={t}")
+    rng = synth.rng_for(0x3A + t)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner)
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    buf[2:2 + w.size] = dev(w)
+    y = D.gemv(D.DeviceWeight(buf[2:2 + w.size], t, inner, outer), dev(x)).cpu().numpy()
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    assert_within(y, ref, oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), f"type {t} misaligned")
 
 
 @pytest.mark.parametrize("t,outer,inner", LAUNCH_SHAPES)
@@ -445,6 +468,9 @@ def test_fused_elementwise_kernels():
     (synth.Q6_K, 4099, 8192, 8),       # four segments: rows meet in LDS per chunk
     (synth.Q8_0, 3001, 20480, 9),      # ten segments: 16-wave streamed kernel
     (synth.Q8_0, 777, 34816, 11),      # 17 segments: GEMV + standalone argmax
+    (synth.Q6_K, 151936, 2560, 0xD1),  # 10 blocks a row (2100 bytes): segments at byte phases
+    (synth.Q6_K, 4099, 2560, 0xD2),
+    (synth.Q8_0, 3001, 2336, 0xD4),
     (synth.Q4_K, 5003, 1024, 7),       # GEMV + standalone argmax path
 ])
 def test_lm_head_argmax(t, vocab, hidden, seed):

@@ -93,27 +93,45 @@ def test_fused_argmax_launches(chk, t, vocab, hidden):
 def test_every_segment_count(chk, t):
     """Rows of 1..16 segments (full and partial last segments): 8 waves for
     one segment, 12 for 2..6 and 9..12, 16 for 7..8 (Q8_0: 8) and 13..16; two
-    ring slots; 32 rows per chunk for one segment, else 16."""
+    ring slots; 32 rows per chunk for one segment, else 16 (at 4096 rows)."""
     unit = 2048 if t == Q6_K else 256  # the host's row-alignment unit
     for nseg in range(1, 17):
         for inner in {2048 * nseg, 2048 * nseg - (2048 - unit)}:
-            st = _ok(chk(t, inner, 1037, False), f"type {t} inner {inner}")
+            st = _ok(chk(t, inner, 4096, False), f"type {t} inner {inner}")
             want = (8 if nseg == 1 else 12 if nseg <= 6 else (8 if t == Q8_0 else 16) if nseg <= 8
                     else 12 if nseg <= 12 else 16)
             assert (st[1], st[2], st[4]) == (want, 2, nseg), (inner, st)
             assert st[3] == (32 if nseg == 1 else 16), (inner, st)
     n, msg, _ = chk(t, 2048 * 16 + unit, 7)
     assert n > 0 and "does not take" in msg  # 17 segments: the byte-granular kernel's
+    for nseg in range(1, 17):  # ragged row counts
+        _ok(chk(t, 2048 * nseg - (2048 - unit), 1037, False), f"type {t} {nseg} segments, 1037 rows")
+
+
+def test_plans_past_one_round_of_workgroups(chk):
+    """Rows per chunk and waves where the chunks outnumber the workgroups a
+    device holds at once: 5120 rows of 9 Q6_K segments (320 chunks of 16 on
+    256 one-per-CU workgroups) take 8-row chunks, 4096 rows (256 chunks) keep
+    16; two-segment rows of more than 256 chunks take two 8-wave workgroups per
+    CU (grid, waves, rows per chunk)."""
+    assert _ok(chk(Q6_K, 17408, 5120), "5120x17408")[3] == 8
+    assert _ok(chk(Q6_K, 16384, 4096), "4096x16384")[3] == 16
+    assert _ok(chk(Q6_K, 9728, 1037), "1037x9728")[3] == 16
+    assert _ok(chk(Q8_0, 4096, 4096), "Q8_0 4096x4096")[:4] == [256, 12, 2, 16]
+    assert _ok(chk(Q6_K, 4096, 4097), "4097x4096")[:4] == [257, 8, 2, 16]
+    assert _ok(chk(Q6_K, 2560, 9728), "9728x2560")[:4] == [512, 8, 2, 16]
+    assert _ok(chk(Q6_K, 2560, 151936), "151936x2560")[:4] == [512, 8, 2, 16]
+    assert _ok(chk(Q6_K, 2560, 151936, True), "151936x2560 argmax")[:4] == [512, 8, 2, 16]
 
 
 def test_argmax_grid_stays_within_the_partials(chk):
     """One partial per workgroup: whatever the CU count, the fused-argmax grid
     is at most 16384 workgroups (the 256 KiB workspace)."""
-    for ncu in (256, 304, 1024, 4096, 5000):
+    for ncu in (256, 304, 1024, 4096, 5000, 20000):
         st = _ok(chk(Q6_K, 2048, 1_000_003, True, ncu=ncu), f"ncu {ncu}")
         assert st[0] == min(16384, 3 * ncu)
         st = _ok(chk(Q8_0, 8192, 600_000, True, ncu=ncu), f"ncu {ncu}")
-        assert st[0] == min(16384, 4 * ncu)
+        assert st[0] == min(16384, ncu)
         st = _ok(chk(Q8_0, 20480, 600_000, True, ncu=ncu), f"ncu {ncu}")
         assert st[0] == min(16384, ncu)
 
@@ -125,12 +143,35 @@ def test_small_and_odd_devices(chk):
             _ok(chk(t, inner, outer, False, ncu=ncu), f"ncu {ncu} type {t} {outer}x{inner}")
 
 
+# rows that are not 16-byte multiples: segments at byte phases 2..14
+PHASED_SHAPES = ((Q6_K, 7, 768), (Q6_K, 1029, 9728), (Q6_K, 300, 2560), (Q6_K, 5, 256),
+                 (Q6_K, 77, 17408), (Q6_K, 33, 2304), (Q8_0, 13, 896), (Q8_0, 31, 480),
+                 (Q8_0, 1000, 2336), (IQ4_NL, 9, 2336), (IQ4_NL, 517, 4640), (Q6_K, 1031, 32512),
+                 (Q8_0, 3, 32), (IQ4_NL, 1, 32))
+
+
+@pytest.mark.parametrize("t,outer,inner", PHASED_SHAPES)
+def test_phased_launches(chk, t, outer, inner):
+    """Rows of any whole number of blocks: every copy starts on a 16-byte unit
+    at or below its segment, covers it, and reads nothing past the 16-byte unit
+    holding W's last byte; the dot's offsets at each phase land on the block."""
+    bb = {Q6_K: 210, Q8_0: 34, IQ4_NL: 18}[t]
+    nblk = inner // (256 if t == Q6_K else 32)
+    assert (nblk * bb) % 16, "an aligned shape"
+    for argmax in (False, True):
+        st = _ok(chk(t, inner, outer, argmax), f"type {t} {outer}x{inner} argmax={argmax}")
+        w_bytes = outer * nblk * bb
+        assert w_bytes <= st[7] <= -(-w_bytes // 16) * 16, (w_bytes, st[7])
+
+
+def test_phased_full_lm_head(chk):
+    """The Q6_K lm_head of a 2560-wide model (151936 x 2560, 10 blocks a row)."""
+    for argmax in (False, True):
+        _ok(chk(Q6_K, 2560, 151936, argmax), f"151936x2560 argmax={argmax}")
+
+
 def test_checker_flags_shapes_the_host_never_sends(chk):
-    # 3 Q6_K blocks (630 bytes) or 15 Q8_0 blocks are not whole 16-byte units:
-    # the host routes them to the byte-granular kernel, and the check says why
-    n, msg, _ = chk(Q6_K, 768, 7)
-    assert n > 0 and "16-byte" in msg
-    n, msg, _ = chk(Q8_0, 480, 7)
-    assert n > 0 and "16-byte" in msg
     n, msg, _ = chk(Q6_K, 2048 * 17, 7)  # 17 segments: more than the kernel takes
     assert n > 0
+    n, msg, _ = chk(Q8_0, 100, 7)  # not a whole number of blocks
+    assert n > 0 and "bad shape" in msg
