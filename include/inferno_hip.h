@@ -281,6 +281,14 @@ int ihip_lm_head_argmax_norm_dev(int ggml_type, const void *w, const float *norm
 int ihip_quantize_row_q8_k_dev(const float *x, void *y, int64_t k, ihip_stream stream);
 int ihip_gemv_q8k_dev(int ggml_type, const void *w, const void *q8, float *out, int inner,
                       int outer, ihip_stream stream);
+/* The same with x as fp32, quantized to Q8_K as ihip_quantize_row_q8_k_dev
+ * does -- the reference's q{4,5,6}_k_gemv (src/kernels/quant_kernels.c:602-650)
+ * as one device call.  Q4_K / Q5_K rows of at most 32768 columns with a
+ * 16-byte aligned x run as one launch, and q8 (when not NULL) receives the
+ * Q8_K blocks of x; other cases quantize x into q8 first, which they then
+ * require (inner/256 * IHIP_Q8_K_BYTES, 4-byte aligned). */
+int ihip_gemv_q8k_x_dev(int ggml_type, const void *w, const float *x, float *out, void *q8,
+                        int inner, int outer, ihip_stream stream);
 
 #ifdef __cplusplus
 }

@@ -538,9 +538,9 @@ int host_gemv_q8k(int type, const uint8_t *w, const float *x, float *out, void *
     RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)inner));
     RET_IF(ensure(c.t, q8k_bytes(inner)));
     RET_IF(ensure(c.y, sizeof(float) * (size_t)outer));
-    hipError_t e = launch_quantize_q8k((const float *)c.x.p, c.t.p, inner, c.stream);
-    if (e == hipSuccess)
-        e = launch_gemv_q8k(type, dw, c.t.p, (float *)c.y.p, inner, outer, c.stream);
+    // one launch quantizes x and runs the GEMV where the kernel takes the shape
+    hipError_t e = launch_gemv_q8k_x(type, dw, (const float *)c.x.p, q8_buf ? c.t.p : nullptr, c.t.p,
+                                     (float *)c.y.p, inner, outer, c.stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
     RET_IF(copy_out(c.y, out, sizeof(float) * (size_t)outer));
@@ -1126,6 +1126,33 @@ int ihip_gemv_q8k_dev(int ggml_type, const void *w, const void *q8, float *out, 
         return fail(IHIP_ERR_INVALID, "w must be %d-byte aligned, q8 and out 4-byte aligned",
                     (int)wa + 1);
     hipError_t e = launch_gemv_q8k(ggml_type, w, q8, out, inner, outer, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_gemv_q8k_x_dev(int ggml_type, const void *w, const float *x, float *out, void *q8,
+                        int inner, int outer, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(ggml_type, inner, outer));
+    if (!q8k_type(ggml_type))
+        return fail(IHIP_ERR_INVALID, "the Q8_K path takes Q4_K, Q5_K or Q6_K, not type %d",
+                    ggml_type);
+    if (!w || !x || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    const uintptr_t wa = ggml_type == kQ6_K ? 1u : 15u;
+    if (((uintptr_t)w & wa) || ((uintptr_t)x & 3u) || ((uintptr_t)q8 & 3u) || ((uintptr_t)out & 3u))
+        return fail(IHIP_ERR_INVALID, "w must be %d-byte aligned, x, q8 and out 4-byte aligned",
+                    (int)wa + 1);
+    const bool one_launch = (ggml_type == kQ4_K || ggml_type == kQ5_K) && inner <= 32768 &&
+                            ((uintptr_t)x & 15u) == 0;
+    if (!one_launch && !q8)
+        return fail(IHIP_ERR_INVALID, "this shape or type quantizes x into q8 first: pass q8 "
+                                      "(inner/256 Q8_K blocks)");
+    hipError_t e = launch_gemv_q8k_x(ggml_type, w, x, q8, nullptr, out, inner, outer, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "q8k gemv launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;

@@ -94,6 +94,26 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// fmaxf over the 64 lanes of a wavefront for values >= 0 (or NaN, which
+// fmaxf skips in any order), by the wave_sum pattern: lanes a DPP move does
+// not write see 0.  Every lane gets the maximum.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_fmax(float v)
+{
+    const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+    return fmaxf(v, __int_as_float(moved));
+}
+__device__ __forceinline__ float wave_fmax_nonneg(float v)
+{
+    v = dpp_fmax<0xb1, 0xf>(v);
+    v = dpp_fmax<0x4e, 0xf>(v);
+    v = dpp_fmax<0x141, 0xf>(v);
+    v = dpp_fmax<0x140, 0xf>(v);
+    v = dpp_fmax<0x142, 0xa>(v);
+    v = dpp_fmax<0x143, 0xc>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Read 8 bytes starting at byte `off` of a 4-byte-aligned LDS array as two
 // dwords.  The dword reads stay 4-byte aligned; the byte phase (off & 3) is
 // taken out with v_alignbyte.  `off` must be relative to the aligned array
@@ -209,6 +229,38 @@ __device__ __forceinline__ void wait_vmcnt(int n)
         __builtin_amdgcn_s_waitcnt(0);
     }
 #undef IHIP_VM
+}
+
+// ---- Q4_K / Q5_K blocks as lanes load them ------------------------------
+// Lane (block b, sub-block pair j): the block header (d, dmin, scales), the 32
+// qs bytes of pair j (low nibbles: sub-block 2j, high: 2j + 1) and (Q5_K) the
+// 32 qh bytes, as 128-bit loads (both block sizes are 16-byte multiples).
+template <int FMT>
+struct KFmt;
+template <>
+struct KFmt<kQ4_K> {
+    static constexpr int BYTES = 144, QS = 16;
+};
+template <>
+struct KFmt<kQ5_K> {
+    static constexpr int BYTES = 176, QS = 48;
+};
+
+struct KBytes {
+    uint4 h, q0, q1, e0, e1;
+};
+
+template <int FMT>
+__device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int j, KBytes &B)
+{
+    using F = KFmt<FMT>;
+    B.h = *reinterpret_cast<const uint4 *>(blk);
+    B.q0 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j);
+    B.q1 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j + 16);
+    if constexpr (FMT == kQ5_K) {
+        B.e0 = *reinterpret_cast<const uint4 *>(blk + 16);
+        B.e1 = *reinterpret_cast<const uint4 *>(blk + 32);
+    }
 }
 
 } // namespace ihip

@@ -41,16 +41,6 @@ namespace ihip {
 // ------------------------------------------------------------------------
 // Q4_K / Q5_K wide kernels
 // ------------------------------------------------------------------------
-template <int FMT>
-struct KFmt;
-template <>
-struct KFmt<kQ4_K> {
-    static constexpr int BYTES = 144, QS = 16;
-};
-template <>
-struct KFmt<kQ5_K> {
-    static constexpr int BYTES = 176, QS = 48;
-};
 
 // Lane geometry inside a 16-block (4096-column) pass: block b = lane >> 2,
 // sub-block pair j = lane & 3.  The lane's weights are qs[32j, 32j+32) of
@@ -80,24 +70,6 @@ __device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col
     }
 }
 
-// The block bytes one lane needs for one row: header (d, dmin, scales), its
-// 32 qs bytes and (Q5_K) the 32 qh bytes.
-struct KBytes {
-    uint4 h, q0, q1, e0, e1;
-};
-
-template <int FMT>
-__device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int j, KBytes &B)
-{
-    using F = KFmt<FMT>;
-    B.h = *reinterpret_cast<const uint4 *>(blk);
-    B.q0 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j);
-    B.q1 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j + 16);
-    if constexpr (FMT == kQ5_K) {
-        B.e0 = *reinterpret_cast<const uint4 *>(blk + 16);
-        B.e1 = *reinterpret_cast<const uint4 *>(blk + 32);
-    }
-}
 
 // ---- integer-digit activations -------------------------------------------
 // The dot of a lane's nibbles with x can run on the integer dot units

@@ -49,5 +49,11 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
 hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t s);
 hipError_t launch_gemv_q8k(int type, const void *w, const void *q8, float *out, int inner,
                            int outer, hipStream_t s);
+// x as fp32, quantized to Q8_K inside the launch where the kernel takes the
+// shape (Q4_K / Q5_K, at most 32768 columns, 16-byte aligned w and x); q8out
+// (optional) receives the Q8_K blocks; otherwise x is quantized into q8out or,
+// without it, into q8tmp (inner / 256 blocks) first.
+hipError_t launch_gemv_q8k_x(int type, const void *w, const float *x, void *q8out, void *q8tmp,
+                             float *out, int inner, int outer, hipStream_t s);
 
 } // namespace ihip

@@ -170,6 +170,21 @@ def gemv_q8k(w: DeviceWeight, q8: torch.Tensor, out: torch.Tensor = None, stream
     return out
 
 
+def gemv_q8k_x(w: DeviceWeight, x: torch.Tensor, out: torch.Tensor = None, q8: torch.Tensor = None,
+               stream=None) -> torch.Tensor:
+    """out = W x in the reference C path's numerics with x given as fp32 (the
+    reference's q{4,5,6}_k_gemv, src/kernels/quant_kernels.c:602-650): x is
+    quantized to Q8_K inside the call; q8, when given (inner/256 * 292 bytes),
+    receives the blocks."""
+    if out is None:
+        out = torch.empty(w.outer, dtype=torch.float32, device=x.device)
+    check(lib().ihip_gemv_q8k_x_dev(w.ggml_type, _ptr(w.data), _ptr(x, torch.float32, "x"),
+                                    _ptr(out, torch.float32, "out"),
+                                    None if q8 is None else _ptr(q8, torch.uint8, "q8"),
+                                    w.inner, w.outer, _stream(stream)))
+    return out
+
+
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor = None,
             stream=None) -> torch.Tensor:
     """rmsnorm_cpu! (src/ModelCPU.jl:111-123): x * (1/sqrt(mean(x^2) + eps)) .* w."""

@@ -124,6 +124,64 @@ def test_gemv_q8k_bit_exact(t, outer, inner):
         assert same_bits(y, oracle.ref_gemv(t, w, x, inner, outer))
 
 
+@pytest.mark.parametrize("t", K_TYPES)
+@pytest.mark.parametrize("outer,inner", Q8K_CASES)
+def test_gemv_q8k_x_bit_exact(t, outer, inner):
+    """x as fp32, quantized inside the call (one launch for Q4_K / Q5_K): the
+    same bits as the reference, and the same Q8_K blocks in q8."""
+    from inferno_hip import device as D
+    rng = synth.rng_for(0x980 + 16 * t + inner % 251)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner) * np.float32(rng.uniform(0.1, 30))
+    say(f"gemv_q8k_x type {t} {outer}x{inner}")
+    dw = D.DeviceWeight(dev(w), t, inner, outer)
+    want = oracle.gemv_q8k(t, w, x, inner, outer)
+    q8 = torch.full((inner // 256 * 292,), 0xAB, dtype=torch.uint8, device="cuda")
+    y = D.gemv_q8k_x(dw, dev(x), q8=q8).cpu().numpy()
+    assert same_bits(y, want)
+    assert np.array_equal(q8.cpu().numpy(), oracle.quantize_row_q8k(x))
+    if t != synth.Q6_K:  # one launch, no Q8_K output
+        assert same_bits(D.gemv_q8k_x(dw, dev(x)).cpu().numpy(), want)
+    if oracle.ref_lib() is not None:
+        assert same_bits(y, oracle.ref_gemv(t, w, x, inner, outer))
+
+
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K])
+def test_gemv_q8k_x_quantizer_edge_blocks(t):
+    """Zero blocks (d = 0), every .5 tie of both signs, tiny and huge scales,
+    quantized inside the GEMV launch."""
+    from inferno_hip import device as D
+    x = x_cases()["edge_blocks"]
+    inner, outer = x.size, 37
+    rng = synth.rng_for(0x9E0 + t)
+    w = synth.weight(rng, t, outer, inner)
+    say(f"gemv_q8k_x edge blocks type {t}")
+    q8 = torch.zeros(inner // 256 * 292, dtype=torch.uint8, device="cuda")
+    y = D.gemv_q8k_x(D.DeviceWeight(dev(w), t, inner, outer), dev(x), q8=q8).cpu().numpy()
+    assert np.array_equal(q8.cpu().numpy(), oracle.quantize_row_q8k(x))
+    assert same_bits(y, oracle.gemv_q8k(t, w, x, inner, outer))
+
+
+def test_gemv_q8k_x_fallbacks():
+    """x not 16-byte aligned: quantized into q8 first, same bits; Q6_K needs q8."""
+    from inferno_hip import device as D
+    from inferno_hip._lib import IHIPArgumentError
+    outer, inner = 65, 2048
+    rng = synth.rng_for(0x9F0)
+    x = synth.activations(rng, inner)
+    say("gemv_q8k_x fallbacks")
+    for t in (synth.Q4_K, synth.Q6_K):
+        w = synth.weight(rng, t, outer, inner)
+        dw = D.DeviceWeight(dev(w), t, inner, outer)
+        buf = torch.zeros(inner + 4, dtype=torch.float32, device="cuda")
+        buf[1:1 + inner] = dev(x)
+        q8 = torch.zeros(inner // 256 * 292, dtype=torch.uint8, device="cuda")
+        y = D.gemv_q8k_x(dw, buf[1:1 + inner], q8=q8).cpu().numpy()
+        assert same_bits(y, oracle.gemv_q8k(t, w, x, inner, outer))
+        with pytest.raises(IHIPArgumentError):
+            D.gemv_q8k_x(dw, buf[1:1 + inner])
+
+
 def test_gemv_q8k_full_size_q4k():
     from inferno_hip import QuantizedKernels as QK
     rng = synth.rng_for(0xC0)
