@@ -1005,9 +1005,8 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
     static_assert(sdig_seg_bytes(FMT) == F::SEG_BYTES && sdig_seg_blocks(FMT) == F::SEG_BLOCKS,
                   "segment geometry");
     static_assert(SLOT >= F::SEG_BYTES + 16, "Q8_0 / IQ4_NL read one dword past a segment");
-    // segments whose digits can be staged in LDS (none for the lm_head: its 32 KB
-    // workgroups run four to a CU, which the staging area would halve)
-    constexpr int SHC = ARGMAX ? 0 : sdig_share_cap(NW);
+    // segments whose digits can be staged in LDS for the segment's other waves
+    constexpr int SHC = sdig_share_cap(NW);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1159,7 +1158,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
                                                        int rpc, ArgPart *__restrict__ parts,
                                                        const float *resid, int epi)
 {
-    constexpr int SHC = ARGMAX ? 0 : sdig_share_cap(NW);
+    constexpr int SHC = sdig_share_cap(NW);
     __shared__ __attribute__((aligned(16))) uint8_t ring[NW * D * sdig_slot(FMT)];
     __shared__ __attribute__((aligned(16))) uint32_t digs[SHC > 0 ? SHC : 1][kDigQuads][64][4];
     __shared__ float part[kSdigMaxRows][NW]; // one column per segment (nseg <= NW)

@@ -55,17 +55,13 @@ __host__ __device__ constexpr int sdig_slot(int fmt) { return sdig_ipr(fmt) * 10
 __host__ __device__ constexpr int sdig_share_cap(int nw) { return nw == 12 ? 6 : nw == 8 ? 2 : 0; }
 
 // LDS of a workgroup of NW waves with D ring slots: the ring, the staged
-// digits (none with the argmax), the chunk partial sums (one column per wave)
-// and 2 KB for the rest; it must fit the 160 KB of a CU.
-__host__ __device__ constexpr int sdig_lds(int fmt, int nw, int d, bool argmax)
+// digits, the chunk partial sums (one column per wave) and 2 KB for the rest;
+// it must fit the 160 KB of a CU.
+__host__ __device__ constexpr int sdig_lds(int fmt, int nw, int d)
 {
-    return nw * d * sdig_slot(fmt) + (argmax ? 0 : sdig_share_cap(nw) * kDigQuads * 1024) +
-           kSdigMaxRows * nw * 4 + 2048;
+    return nw * d * sdig_slot(fmt) + sdig_share_cap(nw) * kDigQuads * 1024 + kSdigMaxRows * nw * 4 + 2048;
 }
-__host__ __device__ constexpr bool sdig_fits(int fmt, int nw, int d)
-{
-    return sdig_lds(fmt, nw, d, false) <= 160 * 1024;
-}
+__host__ __device__ constexpr bool sdig_fits(int fmt, int nw, int d) { return sdig_lds(fmt, nw, d) <= 160 * 1024; }
 
 __host__ __device__ inline int sdig_nseg(int fmt, int nblk)
 {
@@ -269,8 +265,9 @@ struct SdigPlan {
 // Waves per workgroup, rows per chunk and workgroups per CU by segment count,
 // measured on MI355X (us per GEMV in sweeps of HBM-resident copies; the
 // previous plan in parentheses where it differed):
-//   1 segment     8 waves, 32 rows, 3 per CU: the 151936 x 2048 Q6_K lm_head
-//                 (54-55 us; 57 with 4 per CU).  Rows finish inside their wave.
+//   1 segment     8 waves, 2 per CU (LDS), 32 rows for the 151936 x 2048
+//                 Q6_K lm_head (53-55 us), by size for plain rows (sdig_plan).
+//                 Rows finish inside their wave.
 //   2..6          12 waves, 16 rows, 1 per CU (all of 113-137 KB of LDS a CU
 //                 holds; 4 per CU queued three more in rounds: 12288 x 4096
 //                 Q6_K 11.2 us against 15.6): 4096 x 4096 Q8_0 6.47, Q6_K 6.48,
@@ -318,6 +315,17 @@ inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, int ncu)
     p.rpc = sd_min(sdig_rows(p.nseg), kSdigMaxRows);
     const int ncu1 = sd_max(1, ncu);
     int per_cu = sdig_wg_per_cu(fmt, p.nseg);
+    // One-segment rows: the staged digits put a workgroup at 56-72 KB of LDS,
+    // two per CU.  With the argmax (the lm_head) 32 rows per chunk (151936 x
+    // 2048 Q6_K 53.3-54.6 us against 55.3-57.2 with one x load per wave and
+    // three workgroups per CU); plain, rows per chunk by matrix size (151936 x
+    // 2048 52.1 us against 61.0 with 3 per CU and 32 rows; 4096 x 2048 Q8_0
+    // 4.72 against 6.30; 2048 x 2048 Q6_K with 8-row chunks 4.39 against 6.12).
+    if (p.nseg == 1) {
+        per_cu = 2;
+        if (!argmax)
+            p.rpc = outer >= 64 * ncu1 ? 32 : outer >= 16 * ncu1 ? 16 : 8;
+    }
     // Two-segment rows of more chunks than one 12-wave workgroup per CU holds
     // at once: 8-wave workgroups, two per CU, keep 16 waves working on a CU
     // instead of 12 (12288 x 4096 Q6_K 10.75 us against 11.2; 9728 x 2560

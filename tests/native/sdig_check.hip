@@ -77,7 +77,7 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
     const SdigPlan p = sdig_plan(fmt, nblk, outer, argmax != 0, ncu);
     const int NW = p.nw, D = p.d, rpc = p.rpc, grid = p.grid;
     const int IPR = sdig_ipr(fmt), SLOT = sdig_slot(fmt), bb = block_bytes(fmt);
-    const int SHC = argmax ? 0 : sdig_share_cap(NW);
+    const int SHC = sdig_share_cap(NW);
     const size_t row_bytes = (size_t)nblk * bb, w_bytes = (size_t)outer * row_bytes;
     const size_t w_units_end = (w_bytes + 15) & ~(size_t)15; // end of the unit holding W's last byte
     const int ring_bytes = NW * D * SLOT;
