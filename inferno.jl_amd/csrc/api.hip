@@ -924,6 +924,8 @@ int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inn
     RET_IF(check_shape(kQ4_K, inner, outer));
     if (T <= 0)
         return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if (!prefill_fits(T, inner, outer))
+        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes)");
     if (!w || !X || !Y)
         return fail(IHIP_ERR_INVALID, "null pointer");
     const void *dw;
@@ -1082,6 +1084,8 @@ int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int
     RET_IF(check_shape(kQ4_K, inner, outer));
     if (T <= 0)
         return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if (!prefill_fits(T, inner, outer))
+        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes)");
     if (!w || !X || !xh || !Y)
         return fail(IHIP_ERR_INVALID, "null pointer");
     if (!al16(w) || !al16(X) || !al16(xh) || !al16(Y))

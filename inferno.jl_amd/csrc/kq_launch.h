@@ -42,6 +42,13 @@ hipError_t launch_silu_gate_mul(float *out, const float *x, const float *gate, i
                                 hipStream_t s);
 
 // kq_prefill.hip
+// The prefill GEMM addresses its operands as 32-bit byte offsets from the
+// start of Xh (T x inner fp16) and W (outer Q4_K rows).
+inline bool prefill_fits(int T, int inner, int outer)
+{
+    return 2 * (int64_t)T * inner <= (int64_t)UINT32_MAX &&
+           (int64_t)outer * (inner / 256) * 144 <= (int64_t)UINT32_MAX;
+}
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s);
 

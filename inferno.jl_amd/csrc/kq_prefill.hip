@@ -11,12 +11,13 @@
 // Tile: 64 tokens x 128 weight rows per workgroup of 8 waves (256
 // workgroups at 512 x 4096 x 4096).  Both operands of one Q4_K block column
 // (256 k: 32 KB of fp16 activations, 18 KB of weight blocks) stream through
-// a three-slot LDS ring filled by direct-to-LDS 128-bit copies issued two
-// block columns ahead, so two columns' loads are in flight while one is
-// reduced.  Wave (rh, j) reduces weight rows 64 rh .. 64 rh + 63 of the tile
-// over sub-block pair j of every column, dequantizing its matrix-core
-// operand straight from the block bytes into registers (every weight is
-// dequantized once per workgroup).  The weights are the A operand, so each
+// a three-slot LDS ring filled by direct-to-LDS 128-bit copies: while a wave
+// reduces column kb from registers it reads column kb + 1 out of the ring,
+// and the copies of columns kb + 2 and kb + 3 are in flight.  Wave (rh, j)
+// reduces weight rows 64 rh .. 64 rh + 63 of the tile over sub-block pair j
+// of every column, dequantizing its matrix-core operand straight from the
+// block bytes into registers (every weight is dequantized once per
+// workgroup; the two lane halves decode one row's scales each).  The weights are the A operand, so each
 // lane ends with 4 consecutive output rows of one token: the four K-quarter
 // partial sums meet in LDS and leave as 16-byte stores.
 #include "kq_common.h"
@@ -64,59 +65,61 @@ constexpr int PF_B_COPIES = PF_B_STAGE / 1024;   // 18 wave copies of 1 KB
 static_assert(PF_B_STAGE % 1024 == 0, "weight stage is whole wave copies");
 static_assert(PF_NSLOT * PF_SLOT <= 160 * 1024, "ring fits the 160 KB of LDS");
 
-// One direct-to-LDS copy: lane l's 16 bytes at `src` land at LDS byte
-// lds + 16 l.  Written as inline assembly so that the compiler, which would
+// One direct-to-LDS copy: lane l's 16 bytes at base + off land at LDS byte
+// lds + 16 l.  The base is wave-uniform (scalar registers) and the lane's
+// offset a 32-bit register, so a column's copies cost no vector address
+// arithmetic.  Written as inline assembly so that the compiler, which would
 // otherwise make every later LDS read wait for all copies in flight
 // (including those issued ahead for later block columns), leaves the waits to
 // the explicit per-wave s_waitcnt of the main loop.
-__device__ __forceinline__ void pf_copy16(const void *src, uint32_t lds)
+__device__ __forceinline__ void pf_copy16(const void *base, uint32_t off, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(src), "s"(lds)
+                 : "v"(off), "s"(base), "s"(lds)
                  : "memory", "m0");
 }
 
-// Per-lane sources of the copies of block column 0; column kb adds 512 kb
-// bytes (activations) or 144 kb bytes (weights).  Wave w issues activation
+// Per-lane byte offsets of the copies of block column 0 (from Xh and from W);
+// column kb adds 512 kb bytes (activations) or 144 kb bytes (weights) to the
+// wave-uniform base.  Wave w issues activation
 // copies w, w + 8, w + 16, w + 24 (64 chunks each: chunk q = stage row q / 32,
 // activation chunk (q % 32) ^ (row & 15)) and weight copies w, w + 8 and, for
 // w < 2, w + 16 (chunk q = tile row q / 9, 16-byte piece q % 9): 7 copies for
 // waves 0-1, 6 for the others.  Rows past T (tokens) or N (weights) re-read
 // the last row.
 struct PfSrc {
-    const uint8_t *a0, *a1, *a2, *a3, *b0, *b1, *b2; // plain members: kept in registers
+    uint32_t a0, a1, a2, a3, b0, b1, b2; // plain members: kept in registers
 };
 
-__device__ __forceinline__ const uint8_t *pf_src_a(const _Float16 *Xh, int m0, int T, int K,
-                                                   int w, int lane, int k)
+__device__ __forceinline__ uint32_t pf_src_a(int m0, int T, int K, int w, int lane, int k)
 {
     const int q = (8 * k + w) * 64 + lane;
     const int rp = q >> 5, c = (q & 31) ^ (rp & 15);
-    return reinterpret_cast<const uint8_t *>(Xh + (size_t)min(m0 + rp, T - 1) * K + 8 * c);
+    return 2u * ((uint32_t)min(m0 + rp, T - 1) * (uint32_t)K + 8u * (uint32_t)c);
 }
 
-__device__ __forceinline__ const uint8_t *pf_src_b(const uint8_t *W, int n0, int N,
-                                                   size_t row_bytes, int lane, int i)
+__device__ __forceinline__ uint32_t pf_src_b(int n0, int N, uint32_t row_bytes, int lane, int i)
 {
     const int q = 64 * min(i, PF_B_COPIES - 1) + lane;
     const int row = q / 9, piece = q - 9 * row;
-    return W + (size_t)min(n0 + row, N - 1) * row_bytes + 16 * piece;
+    return (uint32_t)min(n0 + row, N - 1) * row_bytes + 16u * (uint32_t)piece;
 }
 
 // Issue this wave's copies of block column kb into the ring slot at LDS
 // address `slot`.
-__device__ __forceinline__ void pf_issue(const PfSrc &S, int kb, int w, uint32_t slot)
+__device__ __forceinline__ void pf_issue(const PfSrc &S, const uint8_t *Xb, const uint8_t *W, int kb,
+                                         int w, uint32_t slot)
 {
-    const size_t ao = (size_t)kb * 512, bo = (size_t)kb * 144;
-    pf_copy16(S.a0 + ao, slot + 1024 * w);
-    pf_copy16(S.a1 + ao, slot + 1024 * (w + 8));
-    pf_copy16(S.a2 + ao, slot + 1024 * (w + 16));
-    pf_copy16(S.a3 + ao, slot + 1024 * (w + 24));
-    pf_copy16(S.b0 + bo, slot + PF_A_STAGE + 1024 * w);
-    pf_copy16(S.b1 + bo, slot + PF_A_STAGE + 1024 * (w + 8));
+    const uint8_t *xa = Xb + (size_t)kb * 512, *wb = W + (size_t)kb * 144;
+    pf_copy16(xa, S.a0, slot + 1024 * w);
+    pf_copy16(xa, S.a1, slot + 1024 * (w + 8));
+    pf_copy16(xa, S.a2, slot + 1024 * (w + 16));
+    pf_copy16(xa, S.a3, slot + 1024 * (w + 24));
+    pf_copy16(wb, S.b0, slot + PF_A_STAGE + 1024 * w);
+    pf_copy16(wb, S.b1, slot + PF_A_STAGE + 1024 * (w + 8));
     if (w + 16 < PF_B_COPIES) // wave-uniform
-        pf_copy16(S.b2 + bo, slot + PF_A_STAGE + 1024 * (w + 16));
+        pf_copy16(wb, S.b2, slot + PF_A_STAGE + 1024 * (w + 16));
 }
 
 // 8 nibbles (the low or high nibble of 8 bytes) -> 8 fp16 weights
@@ -146,13 +149,14 @@ __device__ __forceinline__ half8 pf_dequant8(uint2 bytes, bool high, half2v dsc,
     return r;
 }
 
-// One column's operands of this lane, read from a ring slot: the block
-// headers and 2 x 8 quant bytes of weight rows `blk0` / `blk1` (rows li and
-// li + 32 of the wave's 64) for sub-block pair j, and the 16-byte fp16
-// activation chunks of tokens li and li + 32 for the four 16-wide K steps
-// (k = 64j + 16s + 8h + (0..7), chunk 8j + 2s + h).
+// One column's operands of this lane, read from a ring slot: 2 x 8 quant
+// bytes of weight rows `blk0` / `blk1` (rows li and li + 32 of the wave's 64)
+// for sub-block pair j, the block header of row li + 32 h only (the two lane
+// halves decode one row's scales each and exchange them), and the 16-byte
+// fp16 activation chunks of tokens li and li + 32 for the four 16-wide K
+// steps (k = 64j + 16s + 8h + (0..7), chunk 8j + 2s + h).
 struct PfOps {
-    uint4 hd[2];
+    uint4 hd;
     uint2 q0[2], q1[2];
     half8 x[4][2];
 };
@@ -160,10 +164,10 @@ struct PfOps {
 __device__ __forceinline__ void pf_read(const uint8_t *sa, const uint8_t *blk0, const uint8_t *blk1,
                                         int j, int h, int li, PfOps &o)
 {
+    o.hd = *reinterpret_cast<const uint4 *>(h ? blk1 : blk0);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const uint8_t *blk = u ? blk1 : blk0;
-        o.hd[u] = *reinterpret_cast<const uint4 *>(blk);
         o.q0[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 8 * h);
         o.q1[u] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * j + 16 + 8 * h);
     }
@@ -181,18 +185,28 @@ __device__ __forceinline__ void pf_read(const uint8_t *sa, const uint8_t *blk0, 
 // register r hold token 32t + l % 32, weight row 32u + 8 (r / 4) + 4 (l / 32) + r % 4.
 __device__ __forceinline__ void pf_mma(const PfOps &o, int j, float16v (&acc)[2][2])
 {
+    // Scale d*sc and min -dmin*m of sub-blocks 2j (A) and 2j + 1 (B), each
+    // rounded once to fp16, for this lane half's row, packed (A, B) ...
+    const float d = h2f(o.hd.x & 0xffffu), dmin = h2f(o.hd.x >> 16);
+    float scA, mA, scB, mB;
+    k_scale_min_pair(o.hd.y, o.hd.z, o.hd.w, j, scA, mA, scB, mB);
+    const half2v ds = {(_Float16)(d * scA), (_Float16)(d * scB)};
+    const half2v dm = {(_Float16)(-(dmin * mA)), (_Float16)(-(dmin * mB))};
+    // ... then exchanged between the lane halves: v_permlane32_swap of a
+    // register with itself leaves lanes 0-31's value (row li) in the first
+    // result and lanes 32-63's (row li + 32) in the second, in every lane.
+    const uint32_t dsu = __builtin_bit_cast(uint32_t, ds), dmu = __builtin_bit_cast(uint32_t, dm);
+    const auto xs = __builtin_amdgcn_permlane32_swap(dsu, dsu, false, false);
+    const auto xm = __builtin_amdgcn_permlane32_swap(dmu, dmu, false, false);
     half2v dsA[2], dmA[2], dsB[2], dmB[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const float d = h2f(o.hd[u].x & 0xffffu), dmin = h2f(o.hd[u].x >> 16);
-        float scA, mA, scB, mB;
-        k_scale_min_pair(o.hd[u].y, o.hd[u].z, o.hd[u].w, j, scA, mA, scB, mB);
-        const _Float16 a = (_Float16)(d * scA), ma = (_Float16)(-(dmin * mA));
-        const _Float16 bb = (_Float16)(d * scB), mb = (_Float16)(-(dmin * mB));
-        dsA[u] = half2v{a, a};
-        dmA[u] = half2v{ma, ma};
-        dsB[u] = half2v{bb, bb};
-        dmB[u] = half2v{mb, mb};
+        const half2v s2 = __builtin_bit_cast(half2v, (uint32_t)xs[u]);
+        const half2v m2 = __builtin_bit_cast(half2v, (uint32_t)xm[u]);
+        dsA[u] = half2v{s2[0], s2[0]};
+        dmA[u] = half2v{m2[0], m2[0]};
+        dsB[u] = half2v{s2[1], s2[1]};
+        dmB[u] = half2v{m2[1], m2[1]};
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -206,28 +220,19 @@ __device__ __forceinline__ void pf_mma(const PfOps &o, int j, float16v (&acc)[2]
         }
 }
 
-// Reduce sub-block pair j of one ring slot into the accumulators (all LDS
-// reads of the column first: one wait instead of one per step).
-__device__ __forceinline__ void pf_pair(const uint8_t *sa, const uint8_t *blk0,
-                                        const uint8_t *blk1, int j, int h, int li,
-                                        float16v (&acc)[2][2])
-{
-    PfOps o;
-    pf_read(sa, blk0, blk1, j, h, li, o);
-    __builtin_amdgcn_sched_barrier(0);
-    pf_mma(o, j, acc);
-}
-
-// Wait for this wave's copies: n is 0 or one column's copy count (6 or 7).
+// Wait for this wave's copies, leaving the last n in flight (n is 0 or one
+// or two columns' copy counts, 6 or 7 each), and for its LDS reads: after the
+// next barrier no wave still reads a slot that a copy is about to refill.
 static_assert(PF_B_COPIES == 18, "copy counts 7 (waves 0-1) and 6");
 __device__ __forceinline__ void pf_wait_copies(int n)
 {
-    if (n == 7)
-        __builtin_amdgcn_s_waitcnt(7 | 0x0F70); // vmcnt(7)
-    else if (n == 6)
-        __builtin_amdgcn_s_waitcnt(6 | 0x0F70); // vmcnt(6)
-    else
-        __builtin_amdgcn_s_waitcnt(0 | 0x0F70); // vmcnt(0)
+    switch (n) {
+    case 14: __builtin_amdgcn_s_waitcnt(14 | 0x0070); break; // vmcnt(14) lgkmcnt(0)
+    case 12: __builtin_amdgcn_s_waitcnt(12 | 0x0070); break;
+    case 7: __builtin_amdgcn_s_waitcnt(7 | 0x0070); break;
+    case 6: __builtin_amdgcn_s_waitcnt(6 | 0x0070); break;
+    default: __builtin_amdgcn_s_waitcnt(0 | 0x0070); break; // vmcnt(0) lgkmcnt(0)
+    }
 }
 
 // Y[t, n] = sum_k W[n, k] Xh[t, k] for one 64-token x 128-row tile.  Wave
@@ -270,34 +275,60 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[u][t][r] = 0.0f;
 
+    // byte offsets below 2^32: the launcher checks T * K * 2 and N * row_bytes
     PfSrc S;
-    S.a0 = pf_src_a(Xh, m0, T, K, wave, lane, 0);
-    S.a1 = pf_src_a(Xh, m0, T, K, wave, lane, 1);
-    S.a2 = pf_src_a(Xh, m0, T, K, wave, lane, 2);
-    S.a3 = pf_src_a(Xh, m0, T, K, wave, lane, 3);
-    S.b0 = pf_src_b(W, n0, N, row_bytes, lane, wave);
-    S.b1 = pf_src_b(W, n0, N, row_bytes, lane, wave + 8);
-    S.b2 = pf_src_b(W, n0, N, row_bytes, lane, wave + 16);
+    S.a0 = pf_src_a(m0, T, K, wave, lane, 0);
+    S.a1 = pf_src_a(m0, T, K, wave, lane, 1);
+    S.a2 = pf_src_a(m0, T, K, wave, lane, 2);
+    S.a3 = pf_src_a(m0, T, K, wave, lane, 3);
+    S.b0 = pf_src_b(n0, N, (uint32_t)row_bytes, lane, wave);
+    S.b1 = pf_src_b(n0, N, (uint32_t)row_bytes, lane, wave + 8);
+    S.b2 = pf_src_b(n0, N, (uint32_t)row_bytes, lane, wave + 16);
+    const uint8_t *Xb = reinterpret_cast<const uint8_t *>(Xh);
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
 
-    pf_issue(S, 0, wave, ring_lds);
-    if (nblk > 1)
-        pf_issue(S, 1, wave, ring_lds + PF_SLOT);
-    int cur = 0; // slot of column kb
-    for (int kb = 0; kb < nblk; ++kb) {
-        // this wave's copies of column kb have landed (those of kb + 1 may
-        // still be in flight); after the barrier every wave's have, and every
-        // wave is done reading column kb - 1, whose slot takes kb + 2
-        pf_wait_copies(kb + 1 < nblk ? copies : 0);
+    // Column kb lives in slot kb % 3.  A wave reads column kb + 1 into
+    // registers while it dequantizes and multiplies column kb, so the LDS
+    // reads of the next column overlap this column's matrix-core work; the
+    // copies of column kb + 3 go into column kb's slot, which every wave has
+    // read (into registers) before the barrier of iteration kb.
+    const int nfill = min(nblk, PF_NSLOT);
+    for (int c = 0; c < nfill; ++c)
+        pf_issue(S, Xb, W, c, wave, ring_lds + c * PF_SLOT);
+    pf_wait_copies((nfill - 1) * copies);
+    lds_barrier();
+    const uint8_t *ba = ring + PF_A_STAGE + brow * 144; // this lane's weight rows in slot 0
+    PfOps o0, o1;
+    pf_read(ring, ba, ba + 32 * 144, j, h, li, o0);
+
+    // Block column kb, which has a successor: wait for the successor's
+    // copies, publish it, refill column kb's slot (`slot` = kb % 3), read the
+    // successor into `nxt`, then reduce `cur`.  The last column is reduced
+    // after the loop, so that no branch inside the loop decides whether a
+    // read was issued (the compiler would then wait for every LDS read in
+    // flight, the successor's included, before the first matrix product).
+    auto step = [&](int kb, int slot, PfOps &cur, PfOps &nxt) {
+        pf_wait_copies(kb + 2 < nblk ? copies : 0);
         lds_barrier();
-        if (kb + 2 < nblk) {
-            const int nxt = cur == 0 ? 2 : cur - 1; // (kb + 2) % 3
-            pf_issue(S, kb + 2, wave, ring_lds + nxt * PF_SLOT);
-        }
-        const uint8_t *sl = ring + cur * PF_SLOT;
-        pf_pair(sl, sl + PF_A_STAGE + brow * 144, sl + PF_A_STAGE + (brow + 32) * 144, j, h, li,
-                acc);
-        cur = cur == 2 ? 0 : cur + 1;
+        if (kb + 3 < nblk)
+            pf_issue(S, Xb, W, kb + 3, wave, ring_lds + slot * PF_SLOT);
+        const int ns = slot == 2 ? 0 : slot + 1;
+        pf_read(ring + ns * PF_SLOT, ba + ns * PF_SLOT, ba + ns * PF_SLOT + 32 * 144, j, h, li, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        pf_mma(cur, j, acc);
+    };
+    int kb = 0, slot = 0;
+    for (; kb + 2 < nblk; kb += 2) {
+        step(kb, slot, o0, o1);
+        slot = slot == 2 ? 0 : slot + 1;
+        step(kb + 1, slot, o1, o0);
+        slot = slot == 2 ? 0 : slot + 1;
+    }
+    if (kb + 1 < nblk) {
+        step(kb, slot, o0, o1);
+        pf_mma(o1, j, acc);
+    } else {
+        pf_mma(o0, j, acc);
     }
     __syncthreads(); // every wave is done with the ring
 
@@ -365,6 +396,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s)
 {
+    if (T <= 0 || !prefill_fits(T, inner, outer))
+        return hipErrorInvalidValue;
     const int64_t n = (int64_t)T * inner;
     hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n / 8 + 255) / 256 + 1)), dim3(256), 0, s, X,
                        (_Float16 *)xh, n);

@@ -612,6 +612,9 @@ def test_argmax_errors_and_large_ties():
     (70, 300, 2048),     # ragged tiles
     (1, 128, 256),
     (33, 129, 1792),     # 7 block columns: the ring wraps twice, ragged tiles
+    (5, 64, 512),        # 2 block columns: no loop iteration, last column peeled
+    (40, 200, 768),      # 3 block columns: the odd tail
+    (64, 256, 1024),     # 4 block columns: one loop iteration, even tail
 ])
 def test_prefill_q4k(T, outer, inner):
     """Every token against the per-token GEMV oracle (src/ModelCPU.jl:1001-1017),
