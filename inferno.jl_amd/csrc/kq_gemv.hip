@@ -1214,16 +1214,30 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
     return hipGetLastError();
 }
 
+template <int FMT, bool ARGMAX, int NWV, int D, bool PH>
+static void launch_sdig_d(const void *w, const float *x, float *y, int nblk, int outer,
+                          const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
+{
+    if (!ARGMAX && resid) // the lm_head has no residual
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, D, ARGMAX, !ARGMAX, PH>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+    else
+        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, D, ARGMAX, false, PH>), dim3(p.grid), dim3(NWV * 64), 0,
+                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+}
+
+// Ring depth 3 only for the 8-wave (one-segment) plans that pick it.
 template <int FMT, bool ARGMAX, int NWV, bool PH>
 static void launch_sdig_ph(const void *w, const float *x, float *y, int nblk, int outer,
                            const SdigPlan &p, void *parts, hipStream_t s, const float *resid, int epi)
 {
-    if (!ARGMAX && resid) // the lm_head has no residual
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, !ARGMAX, PH>), dim3(p.grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
-    else
-        hipLaunchKernelGGL((k_gemv_sdig<FMT, NWV, 2, ARGMAX, false, PH>), dim3(p.grid), dim3(NWV * 64), 0,
-                           s, (const uint8_t *)w, x, y, outer, nblk, p.rpc, (ArgPart *)parts, resid, epi);
+    if constexpr (NWV == 8) {
+        if (p.d == 3) {
+            launch_sdig_d<FMT, ARGMAX, NWV, 3, PH>(w, x, y, nblk, outer, p, parts, s, resid, epi);
+            return;
+        }
+    }
+    launch_sdig_d<FMT, ARGMAX, NWV, 2, PH>(w, x, y, nblk, outer, p, parts, s, resid, epi);
 }
 
 template <int FMT, bool ARGMAX, int NWV>
@@ -1249,6 +1263,8 @@ static hipError_t launch_sdig(const void *w, const float *x, float *y, int inner
     if (!sdig_rows_ok(FMT, nblk))
         return ARGMAX ? hipErrorInvalidValue : launch_gemv_generic(FMT, w, x, y, inner, outer, s, resid, epi);
     const SdigPlan p = sdig_plan(FMT, nblk, outer, ARGMAX, device_cus());
+    if (p.d != 2 && !(p.d == 3 && p.nw == 8))
+        return hipErrorInvalidValue; // no such instantiation
     switch (p.nw) {
     case 8: launch_sdig_nw<FMT, ARGMAX, 8>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;
     case 12: launch_sdig_nw<FMT, ARGMAX, 12>(w, x, y, nblk, outer, p, parts, s, resid, epi); break;

@@ -303,7 +303,7 @@ inline bool sdig_rows_ok(int fmt, int nblk)
     return nblk > 0 && nseg >= 1 && nseg <= kSdigMaxSeg;
 }
 
-// The launch: waves, ring depth (two slots per wave), rows per chunk and grid.
+// The launch: waves, ring depth (slots per wave), rows per chunk and grid.
 // With the fused argmax every workgroup leaves one partial, so the grid stays
 // within kArgMaxParts whatever the device's CU count.
 inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, int ncu)
@@ -325,6 +325,12 @@ inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, int ncu)
         per_cu = 2;
         if (!argmax)
             p.rpc = outer >= 64 * ncu1 ? 32 : outer >= 16 * ncu1 ? 16 : 8;
+        // a third ring slot per wave where two workgroups still fit a CU
+        // (Q6_K / IQ4_NL: 2 x 71 KB; Q8_0's 3 KB slots would not): 151936 x
+        // 2048 Q6_K 49.4 us against 52.1 with two slots (four: 58.1, one
+        // workgroup per CU)
+        if (per_cu * sdig_lds(fmt, p.nw, 3) <= 160 * 1024)
+            p.d = 3;
     }
     // Two-segment rows of more chunks than one 12-wave workgroup per CU holds
     // at once: 8-wave workgroups, two per CU, keep 16 waves working on a CU

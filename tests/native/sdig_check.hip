@@ -83,7 +83,7 @@ extern "C" long long sdig_check(int fmt, int inner, int outer, int argmax, int n
     const int ring_bytes = NW * D * SLOT;
 
     // the instantiations the launcher can dispatch, and their LDS
-    if (!((NW == 8 || NW == 12 || NW == 16) && D == 2))
+    if (!((NW == 8 || NW == 12 || NW == 16) && (D == 2 || (D == 3 && NW == 8))))
         R.fail("plan picked %d waves x depth %d, which is not instantiated", NW, D);
     if (!sdig_fits(fmt, NW, D))
         R.fail("%d waves x depth %d do not fit the LDS", NW, D);

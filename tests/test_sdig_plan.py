@@ -64,11 +64,11 @@ def _ok(res, what):
 @pytest.mark.parametrize("argmax", [False, True])
 def test_lm_head_shape_151936x2048(chk, argmax):
     """The Q6_K lm_head shape, plain GEMV and fused argmax, default launch:
-    8 waves, two ring slots, 32 rows per chunk, 512 workgroups (the staged
-    digits leave LDS for two per CU)."""
+    8 waves, three ring slots, 32 rows per chunk, 512 workgroups (the ring
+    and the staged digits leave LDS for two per CU)."""
     st = _ok(chk(Q6_K, 2048, 151936, argmax), "Q6_K 151936x2048")
     grid, nw, d, rpc, nseg, copies, rows, w_hi = st
-    assert (grid, nw, d, rpc, nseg) == (512, 8, 2, 32, 1)
+    assert (grid, nw, d, rpc, nseg) == (512, 8, 3, 32, 1)
     assert rows == 151936 and w_hi == 151936 * 8 * 210  # reads reach the last byte, no further
     assert copies == 151936 * 2 * 64  # every wave has >= 2 rows: one pair of 64-lane copies per row
 
@@ -93,15 +93,17 @@ def test_fused_argmax_launches(chk, t, vocab, hidden):
 @pytest.mark.parametrize("t", [Q6_K, Q8_0, IQ4_NL])
 def test_every_segment_count(chk, t):
     """Rows of 1..16 segments (full and partial last segments): 8 waves for
-    one segment, 12 for 2..6 and 9..12, 16 for 7..8 (Q8_0: 8) and 13..16; two
-    ring slots; 32 rows per chunk for one segment, else 16 (at 4096 rows)."""
+    one segment, 12 for 2..6 and 9..12, 16 for 7..8 (Q8_0: 8) and 13..16; three
+    ring slots for one segment where two workgroups still fit a CU (not Q8_0's
+    3 KB slots), else two; 16 rows per chunk (at 4096 rows)."""
     unit = 2048 if t == Q6_K else 256  # the host's row-alignment unit
     for nseg in range(1, 17):
         for inner in {2048 * nseg, 2048 * nseg - (2048 - unit)}:
             st = _ok(chk(t, inner, 4096, False), f"type {t} inner {inner}")
             want = (8 if nseg == 1 else 12 if nseg <= 6 else (8 if t == Q8_0 else 16) if nseg <= 8
                     else 12 if nseg <= 12 else 16)
-            assert (st[1], st[2], st[4]) == (want, 2, nseg), (inner, st)
+            depth = 3 if nseg == 1 and t != Q8_0 else 2
+            assert (st[1], st[2], st[4]) == (want, depth, nseg), (inner, st)
             assert st[3] == 16, (inner, st)  # one segment: 16 rows per chunk at 4096 plain rows
     n, msg, _ = chk(t, 2048 * 16 + unit, 7)
     assert n > 0 and "does not take" in msg  # 17 segments: the byte-granular kernel's
