@@ -84,6 +84,23 @@ def test_argument_errors_are_raised_before_any_device_work():
         QK.q8_0_gemv_(o, np.zeros(4 * 8 * 34, np.uint8), x.astype(np.float64), 256, 4)
 
 
+def test_prefill_operands_past_32_bit_offsets_are_refused():
+    """The prefill GEMM forms its operand addresses as 32-bit byte offsets from
+    the start of Xh and W: shapes whose fp16 activations (T * inner * 2 bytes)
+    or weights pass 4 GiB are refused before any device work."""
+    import ctypes as C
+    from inferno_hip import _lib
+    L = _lib.lib()
+    fake = C.c_void_p(1 << 20)  # 16-byte aligned, never dereferenced
+    T = (1 << 31) // 4096 + 64  # 2 * T * 4096 > 2^32
+    rc = L.ihip_prefill_q4_k_dev(fake, fake, fake, fake, T, 4096, 4096, None)
+    assert rc == _lib.IHIP_ERR_INVALID
+    assert b"4 GiB" in L.ihip_last_error()
+    rows = (1 << 32) // (16 * 144) + 8  # weights of 4096 columns past 4 GiB
+    rc = L.ihip_prefill_q4_k_dev(fake, fake, fake, fake, 512, 4096, rows, None)
+    assert rc == _lib.IHIP_ERR_INVALID
+
+
 def test_no_device_is_an_error_not_a_fallback():
     import torch
     if torch.cuda.is_available():
