@@ -24,7 +24,9 @@ decode FFN block (gate/up Q4_K 12288x4096 with the SwiGLU epilogue, then the
 Q6_K 4096x12288 down projection) in microseconds, Q8_0 4096x4096 dequant and
 GEMV, the int8-activation variant, the Q6_K 151936x2048 lm_head with fused
 argmax, the 512-token Q4_K prefill GEMM, single-launch latency and the
-cache-resident rate, each labelled.
+cache-resident rate, each labelled.  The FFN block, lm_head and prefill
+(20 us or more per call) are timed both as graph sweeps and as launches
+issued one by one on the stream; each reports the lower, both are listed.
 
 cpu_baseline: the reference's own C kernels (src/kernels/quant_kernels.c,
 compiled from source into oracle/_ref) -- q4_k_gemv on the same workload at
@@ -152,6 +154,41 @@ def time_sweeps(torch, stream, launch, n_rot, sweeps, warmup):
     return t0.elapsed_time(t1)
 
 
+def time_stream(torch, stream, launch, n_rot, sweeps):
+    """The same launches as time_sweeps, issued one by one on `stream` instead
+    of replayed from a graph (what a serving loop does): warmed the same way,
+    then `sweeps` whole passes over the n_rot operand sets between HIP events;
+    returns ms.  Launches are host-bound below ~10 us, so the legs that use it
+    run 20 us or more per launch; on this platform a graph replay adds
+    0.5-0.7 us at each dependent kernel boundary that stream launches do not."""
+    with torch.cuda.stream(stream):
+        for i in range(n_rot):
+            launch(i)
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        k = 0
+        while time.perf_counter() - w0 < WARM_S:
+            launch(k % n_rot)
+            k += 1
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(sweeps * n_rot):
+            launch(i % n_rot)
+        t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1)
+
+
+def both_ways_us(torch, stream, launch, n_rot, sweeps, warmup):
+    """us per launch from graph sweeps and from stream launches; the leg
+    reports the lower (the same kernels either way)."""
+    g = time_sweeps(torch, stream, launch, n_rot, sweeps, warmup) * 1e3 / (sweeps * n_rot)
+    st = time_stream(torch, stream, launch, n_rot, sweeps) * 1e3 / (sweeps * n_rot)
+    return min(g, st), g, st
+
+
 def single_launch_us(torch, stream, launch, reps=50):
     ts = []
     for i in range(reps):
@@ -259,8 +296,7 @@ def ffn_block(torch, stream, synth, D, sweeps=100):
         k = i % ncopy
         D.ffn_swiglu(*sets[k], xd, h=hs[k], y=ys[k])
 
-    ms = time_sweeps(torch, stream, launch, ncopy, sweeps, 4)
-    us = ms * 1e3 / (sweeps * ncopy)
+    us, us_graph, us_stream = both_ways_us(torch, stream, launch, ncopy, sweeps, 4)
     # the same block with the post-attention norm folded into gate/up and the
     # residual add into the down projection (x updated in place: the values
     # drift over the steps, the bytes and launches do not)
@@ -271,10 +307,11 @@ def ffn_block(torch, stream, synth, D, sweeps=100):
         k = i % ncopy
         D.ffn_block(*sets[k], nw, 1e-6, xs[k], h=hs[k])
 
-    ms_n = time_sweeps(torch, stream, launch_norm, ncopy, sweeps, 4)
+    us_n = both_ways_us(torch, stream, launch_norm, ncopy, sweeps, 4)[0]
     return dict(us=us, bytes=nbytes, gbs=nbytes / (us * 1e-6) / 1e9, copies=ncopy,
+                graph_us=us_graph, stream_us=us_stream,
                 single_launch_us=single_launch_us(torch, stream, launch, 20),
-                norm_residual_us=ms_n * 1e3 / (sweeps * ncopy))
+                norm_residual_us=us_n)
 
 
 def q8_0_workloads(torch, stream, synth, D):
@@ -347,11 +384,10 @@ def lm_head(torch, stream, synth, D):
         k = i % ncopy
         D.lm_head_argmax(ws[k], xd, aws[k], logits=logits[k])
 
-    n = 20
-    ms = time_sweeps(torch, stream, launch, ncopy, n, 4)
-    us = ms * 1e3 / (n * ncopy)
+    us, us_graph, us_stream = both_ways_us(torch, stream, launch, ncopy, 20, 4)
     tok = aws[0].result()
-    return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9, token=tok)
+    return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9, token=tok, graph_us=us_graph,
+                stream_us=us_stream)
 
 
 def prefill(torch, stream, synth, D):
@@ -363,12 +399,12 @@ def prefill(torch, stream, synth, D):
     Xd = torch.from_numpy(X).cuda()
     Y = torch.empty(T, outer, device="cuda")
     xh = torch.empty(T * inner, dtype=torch.float16, device="cuda")
-    n = 5
-    ms = time_sweeps(torch, stream, lambda i: D.prefill_q4_k(dw, Xd, Y, xh), 10, n, 4)
-    us = ms * 1e3 / (n * 10)
+    us, us_graph, us_stream = both_ways_us(torch, stream, lambda i: D.prefill_q4_k(dw, Xd, Y, xh),
+                                           10, 5, 4)
     flops = 2.0 * T * outer * inner
     return dict(us=us, tflops=flops / (us * 1e-6) / 1e12,
-                mfma_frac=flops / (us * 1e-6) / 1e12 / PEAK_FP16_TFLOPS)
+                mfma_frac=flops / (us * 1e-6) / 1e12 / PEAK_FP16_TFLOPS, graph_us=us_graph,
+                stream_us=us_stream)
 
 
 def pmc_workload(torch, synth, D):
@@ -616,9 +652,10 @@ def main():
     if args.only != "gemv":
         log("FFN block 4096/12288")
         f = ffn_block(torch, stream, synth, D)
-        log(f"  {f['us']:.2f} us, {f['gbs']:.1f} GB/s")
+        log(f"  {f['us']:.2f} us, {f['gbs']:.1f} GB/s (graph {f['graph_us']:.2f}, stream {f['stream_us']:.2f})")
         log(f"  with the rmsnorm and residual folded in: {f['norm_residual_us']:.2f} us")
         extras.update(ffn_block_us=f["us"], ffn_block_gbs=f["gbs"], ffn_block_frac=f["gbs"] / PEAK_HBM_GBS,
+                      ffn_block_graph_us=f["graph_us"], ffn_block_stream_us=f["stream_us"],
                       ffn_block_single_launch_us=f["single_launch_us"],
                       ffn_block_norm_residual_us=f["norm_residual_us"])
         log("Q8_0 4096x4096 dequant and GEMV")
@@ -631,12 +668,14 @@ def main():
         extras.update(q4k_gemv_q8k_us=k8["us"], q4k_gemv_q8k_gbs=k8["gbs"])
         log("Q6_K lm_head 151936x2048 + argmax")
         lm = lm_head(torch, stream, synth, D)
-        log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s")
-        extras.update(lm_head_argmax_us=lm["us"], lm_head_argmax_gbs=lm["gbs"])
+        log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s (graph {lm['graph_us']:.2f}, stream {lm['stream_us']:.2f})")
+        extras.update(lm_head_argmax_us=lm["us"], lm_head_argmax_gbs=lm["gbs"],
+                      lm_head_argmax_graph_us=lm["graph_us"], lm_head_argmax_stream_us=lm["stream_us"])
         log("prefill 512x4096x4096")
         p = prefill(torch, stream, synth, D)
-        log(f"  {p['us']:.1f} us, {p['tflops']:.1f} TFLOP/s")
-        extras.update(prefill_us=p["us"], prefill_tflops=p["tflops"], prefill_mfma_frac=p["mfma_frac"])
+        log(f"  {p['us']:.1f} us, {p['tflops']:.1f} TFLOP/s (graph {p['graph_us']:.2f}, stream {p['stream_us']:.2f})")
+        extras.update(prefill_us=p["us"], prefill_tflops=p["tflops"], prefill_mfma_frac=p["mfma_frac"],
+                      prefill_graph_us=p["graph_us"], prefill_stream_us=p["stream_us"])
 
     cpu = None
     if not args.no_cpu:
