@@ -80,6 +80,7 @@ FFN_CASES = [
     (1024, 8448, synth.Q4_K, synth.Q4_K),    # residual in a three-pass down; persistent gate/up
     (2560, 9728, synth.Q4_K, synth.Q6_K),    # down rows of 38 blocks at byte phases
     (512, 768, synth.Q8_0, synth.Q8_0),      # unfused gate/up: norm kernel first
+    (4096, 1536, synth.Q4_K, synth.Q6_K),    # one GPU's share of the decode FFN over 8 GPUs
 ]
 
 

@@ -153,6 +153,8 @@ GEMV_CASES = [
     (synth.IQ4_NL, 1000, 4096),   # two 64-block segments per row
     (synth.IQ4_NL, 13, 2304),     # partial segment (72 blocks)
     (synth.IQ4_NL, 5, 96),        # 3 blocks a row, at byte phases
+    (synth.Q4_K, 1536, 4096),     # one GPU's gate/up rows of the FFN over 8 GPUs
+    (synth.Q6_K, 4096, 1536),     # one GPU's down-projection columns (6 blocks a row)
 ]
 
 
@@ -472,6 +474,7 @@ def test_fused_elementwise_kernels():
     (synth.Q6_K, 4099, 2560, 0xD2),
     (synth.Q8_0, 3001, 2336, 0xD4),
     (synth.Q4_K, 5003, 1024, 7),       # GEMV + standalone argmax path
+    (synth.Q6_K, 18992, 2048, 0xE0),   # one GPU's vocabulary rows of the lm_head over 8 GPUs
 ])
 def test_lm_head_argmax(t, vocab, hidden, seed):
     say(f"lm_head type={t} vocab={vocab} hidden={hidden} seed={seed}")
@@ -615,6 +618,7 @@ def test_argmax_errors_and_large_ties():
     (5, 64, 512),        # 2 block columns: no loop iteration, last column peeled
     (40, 200, 768),      # 3 block columns: the odd tail
     (64, 256, 1024),     # 4 block columns: one loop iteration, even tail
+    (512, 512, 4096),    # one GPU's weight rows of the prefill over 8 GPUs
 ])
 def test_prefill_q4k(T, outer, inner):
     """Every token against the per-token GEMV oracle (src/ModelCPU.jl:1001-1017),
