@@ -15,9 +15,17 @@ from ._lib import Q4_K, IHIPArgumentError, check, lib
 from .synth import BLOCK_BYTES, BLOCK_ELEMS
 
 
+# torch's current-stream handle without building a Stream object (2-3 us of
+# host time per call otherwise); the public API where torch lacks it.
+_raw_current_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(stream=None) -> int:
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return s.cuda_stream
+    if stream is not None:
+        return stream.cuda_stream
+    if _raw_current_stream is not None:
+        return _raw_current_stream(torch.cuda.current_device())
+    return torch.cuda.current_stream().cuda_stream
 
 
 def _ptr(t: torch.Tensor, dtype=None, what="tensor") -> int:

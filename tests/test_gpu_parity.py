@@ -642,3 +642,34 @@ def test_prefill_q4k(T, outer, inner):
     ratio32 = np.abs(Y.astype(np.float64) - ref32) / (1e-4 * nrm[None, :] * xn[:, None])
     assert np.all(ratio32 <= 1.0), f"fp32-x oracle: max err/tol {float(np.max(ratio32)):.3g}"
     say(f"prefill max err/tol = {worst:.3e}")
+
+
+def test_device_calls_launch_on_the_current_stream():
+    """Without a stream argument the device entry points launch on torch's
+    current stream (read without building a Stream object): the same handle
+    as torch.cuda.current_stream() by default, inside a stream context and
+    inside a graph capture."""
+    from inferno_hip import device as D
+    from inferno_hip.device import _stream
+    assert _stream() == torch.cuda.current_stream().cuda_stream
+    s2 = torch.cuda.Stream()
+    with torch.cuda.stream(s2):
+        assert _stream() == s2.cuda_stream
+    rng = synth.rng_for(0x57)
+    t, outer, inner = synth.Q4_K, 256, 4096
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner)
+    dw, xd = dweight(w, t, inner, outer), dev(x)
+    y = torch.zeros(outer, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=cs):
+        assert _stream() == cs.cuda_stream
+        D.gemv(dw, xd, y)
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
+    for _ in range(3):  # replays, with eager work between them
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_within(y.cpu().numpy(), ref, tol, "graph replay")
