@@ -111,6 +111,7 @@ module QuantizedKernels
 export quant_kernels_available
 export q4_k_gemv!, q5_k_gemv!, q6_k_gemv!, q8_0_gemv!
 export quantize_q8_k!, vec_dot_q4_k_q8_k, vec_dot_q5_k_q8_k, vec_dot_q6_k_q8_k
+export q4_k_gemv_q8k!, q5_k_gemv_q8k!, q6_k_gemv_q8k!, EXACT_C_NUMERICS
 
 import ..InfernoHIP: LIBIHIP, check, require, available
 
@@ -128,14 +129,67 @@ function check_dims(out, weight_data, x, inner_dim, outer_dim, elems, bytes)
 end
 
 """
+    EXACT_C_NUMERICS[] = true
+
+Routes `q4_k_gemv!`, `q5_k_gemv!` and `q6_k_gemv!` through the int8-activation
+kernels (`q*_k_gemv_q8k!`): x quantized to Q8_K per 256 values and integer
+dot products, bit-identical to the reference's C kernels
+(src/kernels/quant_kernels.c:602-650), which is what the reference's
+`q*_k_gemv!` computes.  Default `false`: fp32 activations, within
+1e-4 ||w_row|| ||x|| of the exact sum.  Initialised from the environment
+variable IHIP_EXACT_C_NUMERICS=1.
+"""
+const EXACT_C_NUMERICS = Ref(get(ENV, "IHIP_EXACT_C_NUMERICS", "0") == "1")
+
+"""
+    q4_k_gemv_q8k!(out, weight_data, x, inner_dim, outer_dim)
+
+src/kernels/quant_kernels.c:602-614 on the GPU, bit-identical: x quantized to
+Q8_K (quantize_row_q8_K), then the integer Q4_K x Q8_K dot products.
+"""
+function q4_k_gemv_q8k!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                        x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 144)
+    check(ccall((:ihip_q4_k_gemv_q8k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid}, Cint, Cint),
+                weight_data, x, out, C_NULL, inner_dim, outer_dim))
+    return out
+end
+
+"""src/kernels/quant_kernels.c:620-632 on the GPU, bit-identical (Q5_K)."""
+function q5_k_gemv_q8k!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                        x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 176)
+    check(ccall((:ihip_q5_k_gemv_q8k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid}, Cint, Cint),
+                weight_data, x, out, C_NULL, inner_dim, outer_dim))
+    return out
+end
+
+"""src/kernels/quant_kernels.c:638-650 on the GPU, bit-identical (Q6_K)."""
+function q6_k_gemv_q8k!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                        x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 210)
+    check(ccall((:ihip_q6_k_gemv_q8k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Ptr{Cvoid}, Cint, Cint),
+                weight_data, x, out, C_NULL, inner_dim, outer_dim))
+    return out
+end
+
+"""
     q4_k_gemv!(out, weight_data, x, inner_dim, outer_dim)
 
 src/QuantizedKernels.jl:84-96 on the GPU: `out = W x` for the Q4_K blocks of an
 `outer_dim x inner_dim` matrix, fp32 activations (within 1e-4 ||w_row|| ||x||
-of the exact sum).  The weight is uploaded on first use and cached.
+of the exact sum), or the reference C numerics when `EXACT_C_NUMERICS[]`.
+The weight is uploaded on first use and cached.
 """
 function q4_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
                     x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    EXACT_C_NUMERICS[] && return q4_k_gemv_q8k!(out, weight_data, x, inner_dim, outer_dim)
     require()
     check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 144)
     check(ccall((:ihip_q4_k_gemv, LIBIHIP), Cint,
@@ -144,9 +198,10 @@ function q4_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
     return out
 end
 
-"""src/QuantizedKernels.jl:103-115 on the GPU (Q5_K)."""
+"""src/QuantizedKernels.jl:103-115 on the GPU (Q5_K; `EXACT_C_NUMERICS` as q4_k_gemv!)."""
 function q5_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
                     x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    EXACT_C_NUMERICS[] && return q5_k_gemv_q8k!(out, weight_data, x, inner_dim, outer_dim)
     require()
     check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 176)
     check(ccall((:ihip_q5_k_gemv, LIBIHIP), Cint,
@@ -155,9 +210,10 @@ function q5_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
     return out
 end
 
-"""src/QuantizedKernels.jl:122-134 on the GPU (Q6_K)."""
+"""src/QuantizedKernels.jl:122-134 on the GPU (Q6_K; `EXACT_C_NUMERICS` as q4_k_gemv!)."""
 function q6_k_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
                     x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    EXACT_C_NUMERICS[] && return q6_k_gemv_q8k!(out, weight_data, x, inner_dim, outer_dim)
     require()
     check_dims(out, weight_data, x, inner_dim, outer_dim, 256, 210)
     check(ccall((:ihip_q6_k_gemv, LIBIHIP), Cint,

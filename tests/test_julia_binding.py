@@ -103,10 +103,13 @@ def test_modules_export_the_reference_names():
     assert {"dequantize_q8_0", "dequantize_q4_k", "dequantize_q5_k",
             "dequantize_q6_k"} <= exports["Dequant"]
     assert {"fused_mlp_gate_mul!", "fused_silu_gate_mul!", "gpu_argmax!"} <= exports["FusedKernels"]
-    # every exported name is defined in its module
+    # every exported name is defined in its module (a function or a const)
     for m, names in exports.items():
         for n in names:
-            assert re.search(r"(function\s+|^)" + re.escape(n) + r"\s*\(", mods[m], re.M), (m, n)
+            assert re.search(r"(function\s+|^)" + re.escape(n) + r"\s*\(", mods[m], re.M) or \
+                re.search(r"^const\s+" + re.escape(n) + r"\s*=", mods[m], re.M), (m, n)
+    # the opt-in C numerics reach the int8-activation entry points
+    assert {"q4_k_gemv_q8k!", "q5_k_gemv_q8k!", "q6_k_gemv_q8k!", "EXACT_C_NUMERICS"} <= exports["QuantizedKernels"]
 
 
 def test_julia_source_is_structurally_balanced():
