@@ -75,23 +75,14 @@ __device__ __forceinline__ float wave_sum(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Unsigned maximum over the 64 lanes of a wavefront (the wave_sum pattern
-// with max; lanes a DPP move does not write contribute 0).
+// Unsigned maximum of a value and its DPP-moved copy (lanes the move does
+// not write contribute 0): the x staging chains these over a sub-block's
+// lanes for its largest magnitude.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v)
 {
     const uint32_t moved = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
     return v > moved ? v : moved;
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
-{
-    v = dpp_max_u32<0xb1, 0xf>(v);
-    v = dpp_max_u32<0x4e, 0xf>(v);
-    v = dpp_max_u32<0x141, 0xf>(v);
-    v = dpp_max_u32<0x140, 0xf>(v);
-    v = dpp_max_u32<0x142, 0xa>(v);
-    v = dpp_max_u32<0x143, 0xc>(v);
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // fmaxf over the 64 lanes of a wavefront for values >= 0 (or NaN, which
@@ -158,15 +149,6 @@ __device__ __forceinline__ void lds_barrier()
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-}
-
-// Hide a value from the optimizer (no instruction is emitted).  Used on
-// nibble-masked dwords so that the byte converts stay v_cvt_f32_ubyte{0..3}
-// instead of being refolded into a bit-field extract plus convert.
-__device__ __forceinline__ uint32_t opaque(uint32_t v)
-{
-    asm volatile("" : "+v"(v));
-    return v;
 }
 
 // Signed byte k (0..3) of a dword, as float.

@@ -13,7 +13,6 @@
 namespace ihip {
 
 // ---- element-at-a-time decode (generic paths) ---------------------------
-__device__ __forceinline__ uint32_t rd8(const uint8_t *p) { return *p; }
 __device__ __forceinline__ uint32_t rd16(const uint8_t *p) { return p[0] | (p[1] << 8); }
 
 __device__ __forceinline__ void k_scale_min_bytes(const uint8_t *s, int i, uint32_t &sc,
