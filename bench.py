@@ -23,7 +23,8 @@ time (x in, y out over PCIe: what a Julia caller of q4_k_gemv! sees), the
 decode FFN block (gate/up Q4_K 12288x4096 with the SwiGLU epilogue, then the
 Q6_K 4096x12288 down projection) in microseconds, Q8_0 4096x4096 dequant and
 GEMV, the int8-activation variant, the Q6_K 151936x2048 lm_head with fused
-argmax, the 512-token Q4_K prefill GEMM, single-launch latency and the
+argmax, loading those weights from a GGUF file into the device registry,
+the 512-token Q4_K prefill GEMM, single-launch latency and the
 cache-resident rate, each labelled.  The FFN block, lm_head and prefill
 (20 us or more per call) are timed both as graph sweeps and as launches
 issued one by one on the stream; each reports the lower, both are listed.
@@ -407,6 +408,79 @@ def prefill(torch, stream, synth, D):
                 stream_us=us_stream)
 
 
+def write_gguf(path, tensors, alignment=32):
+    """A GGUF v3 file (the layout src/GGUF.jl:119-165 reads): no key/values,
+    tensor infos (name, dims with ne0 first, GGML type, offset), then the
+    aligned data section."""
+    import struct
+    infos, offs, off = b"", [], 0
+    for name, gt, dims, blob in tensors:
+        off = -(-off // alignment) * alignment
+        offs.append(off)
+        nb = name.encode()
+        infos += struct.pack("<Q", len(nb)) + nb + struct.pack("<I", len(dims))
+        infos += b"".join(struct.pack("<Q", d) for d in dims) + struct.pack("<IQ", gt, off)
+        off += blob.size
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 0) + infos
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * (-len(head) % alignment))
+        base = f.tell()
+        for (_, _, _, blob), o in zip(tensors, offs):
+            f.seek(base + o)
+            blob.tofile(f)
+
+
+def gguf_load(torch, synth, D):
+    """The GGUF-fed weight registry (inferno.jl_amd/csrc/gguf.hip) on the
+    decode weights benched above: a file holding the FFN block's three
+    weights and the 151936x2048 lm_head is opened (memory-mapped, header and
+    tensor infos parsed) and every tensor uploaded into the device registry;
+    the file is in the page cache, as after a first load.  Bytes per second
+    of the whole open + upload, and the uploaded bytes checked."""
+    import tempfile
+    from inferno_hip import GGUF, _lib
+    rng = synth.rng_for(0xC5)
+    specs = [("blk.0.ffn_gate.weight", synth.Q4_K, 4096, 12288),
+             ("blk.0.ffn_up.weight", synth.Q4_K, 4096, 12288),
+             ("blk.0.ffn_down.weight", synth.Q6_K, 12288, 4096),
+             ("output.weight", synth.Q6_K, 2048, 151936)]
+    tensors = [(n, t, (inner, outer), synth.weight(rng, t, outer, inner)) for n, t, inner, outer in specs]
+    nbytes = sum(b.size for *_, b in tensors)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        write_gguf(path, tensors)
+        times, opens = [], []
+        for rep in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            f = GGUF.read_gguf(path)
+            t1 = time.perf_counter()
+            handles = [GGUF.upload(f, n) for n, *_ in tensors]
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            opens.append(t1 - t0)
+            times.append(t2 - t0)
+            if rep == 0:  # the uploaded gate weight gives the same GEMV as its bytes
+                n, t, (inner, outer), blob = tensors[0]
+                x = torch.from_numpy(synth.activations(rng, inner)).cuda()
+                y_reg = torch.empty(outer, device="cuda")
+                _lib.check(_lib.lib().ihip_gemv_dev(t, GGUF.device_ptr(handles[0]), x.data_ptr(),
+                                                    y_reg.data_ptr(), inner, outer,
+                                                    torch.cuda.current_stream().cuda_stream))
+                y_ref = D.gemv(D.DeviceWeight(torch.from_numpy(blob).cuda(), t, inner, outer), x)
+                torch.cuda.synchronize()
+                if not torch.equal(y_reg, y_ref):
+                    raise AssertionError("GGUF-uploaded weight gives a different GEMV")
+            for h in handles:
+                _lib.check(_lib.lib().ihip_weight_release(h))
+            f.close()
+    finally:
+        os.unlink(path)
+    s = float(np.median(times))
+    return dict(bytes=nbytes, s=s, gbs=nbytes / s / 1e9, open_ms=float(np.median(opens)) * 1e3)
+
+
 def pmc_workload(torch, synth, D):
     """The program the rocprofv3 --pmc runs profile: a device copy of known
     size (to calibrate FETCH_SIZE / WRITE_SIZE) and a few launches of each
@@ -671,6 +745,11 @@ def main():
         log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s (graph {lm['graph_us']:.2f}, stream {lm['stream_us']:.2f})")
         extras.update(lm_head_argmax_us=lm["us"], lm_head_argmax_gbs=lm["gbs"],
                       lm_head_argmax_graph_us=lm["graph_us"], lm_head_argmax_stream_us=lm["stream_us"])
+        log("GGUF file -> device weight registry")
+        gg = gguf_load(torch, synth, D)
+        log(f"  {gg['bytes'] / 1e6:.0f} MB in {gg['s'] * 1e3:.1f} ms ({gg['gbs']:.1f} GB/s; open {gg['open_ms']:.2f} ms)")
+        extras.update(gguf_upload_bytes=gg["bytes"], gguf_upload_ms=gg["s"] * 1e3, gguf_upload_gbs=gg["gbs"],
+                      gguf_open_ms=gg["open_ms"])
         log("prefill 512x4096x4096")
         p = prefill(torch, stream, synth, D)
         log(f"  {p['us']:.1f} us, {p['tflops']:.1f} TFLOP/s (graph {p['graph_us']:.2f}, stream {p['stream_us']:.2f})")

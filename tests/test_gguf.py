@@ -8,6 +8,7 @@ The writer below is independent of the reader: it lays out bytes from the
 field list and computes where the data section must start by itself.
 """
 import struct
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -182,3 +183,26 @@ def test_uploaded_tensors_feed_the_gemv(tmp_path):
             tol = oracle.tolerance(oracle.row_norms(gt, w, inner, outer), x)
             assert np.all(np.abs(yd.cpu().numpy().astype(np.float64) - ref) <= tol)
             _lib.check(_lib.lib().ihip_weight_release(h))
+
+
+def test_bench_writer_round_trips(tmp_path):
+    """bench.py's GGUF writer (the file its registry-load leg times) is read
+    back by the native reader: names, types, dimensions and bytes."""
+    import sys
+    root = Path(__file__).resolve().parents[1]
+    if str(root) not in sys.path:
+        sys.path.insert(0, str(root))
+    import bench
+    from inferno_hip import GGUF
+    rng = synth.rng_for(0x66)
+    tensors = [("blk.0.ffn_gate.weight", synth.Q4_K, (512, 3), synth.weight(rng, synth.Q4_K, 3, 512)),
+               ("output.weight", synth.Q6_K, (256, 5), synth.weight(rng, synth.Q6_K, 5, 256)),
+               ("q8", synth.Q8_0, (64, 7), synth.weight(rng, synth.Q8_0, 7, 64))]
+    path = tmp_path / "bench.gguf"
+    bench.write_gguf(str(path), tensors)
+    with GGUF.read_gguf(path) as f:
+        assert f.version == 3 and f.alignment == 32
+        for name, t, dims, blob in tensors:
+            info = f.tensors[name]
+            assert (info.type, info.dimensions, info.nbytes) == (t, dims, blob.size)
+            assert np.array_equal(GGUF.get_tensor_raw_bytes(f, name), blob)
