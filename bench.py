@@ -22,8 +22,8 @@ same 9.4 MB that discards the bytes), the host-pointer drop-in's per-call
 time (x in, y out over PCIe: what a Julia caller of q4_k_gemv! sees), the
 decode FFN block (gate/up Q4_K 12288x4096 with the SwiGLU epilogue, then the
 Q6_K 4096x12288 down projection) in microseconds, Q8_0 4096x4096 dequant and
-GEMV, the int8-activation variant, the Q6_K 151936x2048 lm_head with fused
-argmax, loading those weights from a GGUF file into the device registry,
+GEMV, the IQ4_NL GEMV, the int8-activation variant, the Q6_K 151936x2048
+lm_head with fused argmax (and with the final rmsnorm in front), loading those weights from a GGUF file into the device registry,
 the 512-token Q4_K prefill GEMM, single-launch latency and the
 cache-resident rate, each labelled.  The FFN block, lm_head and prefill
 (20 us or more per call) are timed both as graph sweeps and as launches
@@ -343,6 +343,25 @@ def q8_0_workloads(torch, stream, synth, D):
                 gemv_us=gemv_us, gemv_gbs=gemv_bytes / (gemv_us * 1e-6) / 1e9)
 
 
+def iq4nl_gemv(torch, stream, synth, D):
+    """IQ4_NL GEMV at 4096x4096 (the keep-quantized format of the SSM
+    projections, src/ModelCPU.jl:381-408), weights rotated through HBM."""
+    outer = inner = 4096
+    rng = synth.rng_for(0xC6)
+    w = synth.weight(rng, synth.IQ4_NL, outer, inner)
+    x = synth.activations(rng, inner)
+    nbytes = w.size + 4 * inner + 4 * outer
+    ncopy = copies_for(w.size)
+    base = torch.from_numpy(w).cuda()
+    ws = [D.DeviceWeight(base.clone(), synth.IQ4_NL, inner, outer) for _ in range(ncopy)]
+    xd = torch.from_numpy(x).cuda()
+    ys = torch.empty(ncopy, outer, device="cuda")
+    n = 16
+    ms = time_sweeps(torch, stream, lambda i: D.gemv(ws[i % ncopy], xd, ys[i % ncopy]), ncopy, n, 2)
+    us = ms * 1e3 / (n * ncopy)
+    return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9)
+
+
 def q8k_gemv(torch, stream, synth, D):
     """The int8-activation variant (the reference C numerics) at 4096x4096
     Q4_K: one launch quantizes x to Q8_K and runs the GEMV, weights rotated
@@ -387,8 +406,18 @@ def lm_head(torch, stream, synth, D):
 
     us, us_graph, us_stream = both_ways_us(torch, stream, launch, ncopy, 20, 4)
     tok = aws[0].result()
+    # the final norm folded in front (src/ModelCPU.jl:1014-1015): rmsnorm of
+    # the hidden state into caller scratch, then the same lm_head
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, hidden).astype(np.float32)).cuda()
+    xn = torch.empty_like(xd)
+
+    def launch_norm(i):
+        k = i % ncopy
+        D.lm_head_argmax_norm(ws[k], nw, 1e-6, xd, aws[k], xn=xn, logits=logits[k])
+
+    us_n = both_ways_us(torch, stream, launch_norm, ncopy, 20, 4)[0]
     return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9, token=tok, graph_us=us_graph,
-                stream_us=us_stream)
+                stream_us=us_stream, norm_us=us_n)
 
 
 def prefill(torch, stream, synth, D):
@@ -736,6 +765,10 @@ def main():
         q = q8_0_workloads(torch, stream, synth, D)
         log(f"  dequant {q['dequant_us']:.2f} us ({q['dequant_gbs']:.0f} GB/s), gemv {q['gemv_us']:.2f} us ({q['gemv_gbs']:.0f} GB/s)")
         extras.update({f"q8_0_{k}": v for k, v in q.items()})
+        log("IQ4_NL 4096x4096 GEMV")
+        iq = iq4nl_gemv(torch, stream, synth, D)
+        log(f"  {iq['us']:.2f} us, {iq['gbs']:.0f} GB/s")
+        extras.update(iq4_nl_gemv_us=iq["us"], iq4_nl_gemv_gbs=iq["gbs"])
         log("Q4_K GEMV 4096x4096, int8-activation variant (quantize + GEMV)")
         k8 = q8k_gemv(torch, stream, synth, D)
         log(f"  {k8['us']:.2f} us, {k8['gbs']:.0f} GB/s")
@@ -743,8 +776,10 @@ def main():
         log("Q6_K lm_head 151936x2048 + argmax")
         lm = lm_head(torch, stream, synth, D)
         log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s (graph {lm['graph_us']:.2f}, stream {lm['stream_us']:.2f})")
+        log(f"  with the final rmsnorm in front: {lm['norm_us']:.2f} us")
         extras.update(lm_head_argmax_us=lm["us"], lm_head_argmax_gbs=lm["gbs"],
-                      lm_head_argmax_graph_us=lm["graph_us"], lm_head_argmax_stream_us=lm["stream_us"])
+                      lm_head_argmax_graph_us=lm["graph_us"], lm_head_argmax_stream_us=lm["stream_us"],
+                      lm_head_argmax_norm_us=lm["norm_us"])
         log("GGUF file -> device weight registry")
         gg = gguf_load(torch, synth, D)
         log(f"  {gg['bytes'] / 1e6:.0f} MB in {gg['s'] * 1e3:.1f} ms ({gg['gbs']:.1f} GB/s; open {gg['open_ms']:.2f} ms)")
