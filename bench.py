@@ -687,10 +687,12 @@ def cpu_baseline(synth, oracle):
                                  ("fp32 fallback, one thread", 1, f32_call)):
         if gomp is not None:
             gomp.omp_set_num_threads(threads)
+        call(0)  # cold first call, not counted
         t0 = time.perf_counter()
-        call(0)
-        one = time.perf_counter() - t0
-        per_rep = max(3, int(0.6 / max(one, 1e-5)))  # about 0.6 s per repetition
+        for k in range(10):
+            call(k % ncopy)
+        one = (time.perf_counter() - t0) / 10
+        per_rep = max(3, int(1.0 / max(one, 1e-5)))  # up to about 1 s per repetition
         ms = runs(call, per_rep)
         med = float(np.median(ms))
         results.append(dict(path=label, threads=threads, median_ms=med, min_ms=float(min(ms)),
