@@ -37,6 +37,9 @@ the oracle's restatement of the single-threaded fp32 fallback
 level cache, median and spread of 7 repetitions.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only gemv]
+       python bench.py --sweep     GEMV of every format over common model shapes,
+                                   beside a plain read of the same bytes (a markdown table)
+       python bench.py --floors    empty-launch and read floors over launch shapes
 """
 from __future__ import annotations
 
@@ -77,6 +80,8 @@ def parse():
                     help="run the short program the rocprofv3 --pmc runs profile")
     ap.add_argument("--floors", action="store_true",
                     help="sweep the empty-launch and read floors over launch shapes")
+    ap.add_argument("--sweep", action="store_true",
+                    help="GEMV of every format over common model shapes, beside a plain read of the same bytes")
     return ap.parse_args()
 
 
@@ -600,6 +605,69 @@ def floors_sweep(torch, stream):
               f"{nb / (r[1] - r[0]) / 1e3:.0f} |", flush=True)
 
 
+SWEEP_SHAPES = (
+    # (format name, outer, inner): the projections of 7B-70B-class and
+    # 1.5B-class decoders, and the vocabulary heads
+    ("Q4_K", 4096, 4096), ("Q4_K", 12288, 4096), ("Q4_K", 11008, 4096), ("Q4_K", 4096, 11008),
+    ("Q4_K", 14336, 4096), ("Q4_K", 4096, 14336), ("Q4_K", 2048, 2048), ("Q4_K", 5120, 5120),
+    ("Q4_K", 13824, 5120), ("Q4_K", 5120, 13824), ("Q4_K", 8192, 8192), ("Q4_K", 28672, 8192),
+    ("Q4_K", 8192, 28672),
+    ("Q5_K", 4096, 4096), ("Q5_K", 14336, 4096), ("Q5_K", 4096, 14336),
+    ("Q6_K", 4096, 4096), ("Q6_K", 4096, 14336), ("Q6_K", 32000, 4096), ("Q6_K", 151936, 2048),
+    ("Q6_K", 128256, 4096),
+    ("Q8_0", 4096, 4096), ("Q8_0", 14336, 4096), ("Q8_0", 4096, 14336),
+    ("IQ4_NL", 4096, 4096), ("IQ4_NL", 14336, 4096),
+)
+
+
+def shape_sweep(torch, stream, synth, D):
+    """One GEMV per shape of SWEEP_SHAPES, weights rotated through enough
+    copies to leave the 256 MB MALL, HIP graph sweeps; beside it a fully
+    coalesced read of the same weight bytes (the floor a launch of that size
+    cannot beat).  Prints a markdown table.  The weights repeat a slab of at
+    most 2048 synthetic rows (the GEMV's time does not depend on the values)."""
+    F = floors_lib()
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cs = lambda: torch.cuda.current_stream().cuda_stream
+    print("| format | outer x inner | weight MB | copies | GEMV us | GB/s | % of 8 TB/s | read us | GEMV / read |\n"
+          "|---|---|---|---|---|---|---|---|---|", flush=True)
+    for name, outer, inner in SWEEP_SHAPES:
+        t = getattr(synth, name)
+        rows = min(outer, 2048)
+        rng = synth.rng_for(0xD0 + t)
+        slab = torch.from_numpy(synth.weight(rng, t, rows, inner)).cuda()
+        row_bytes = slab.numel() // rows
+        reps = -(-outer // rows)
+        base = slab.repeat(reps)[: outer * row_bytes].contiguous()
+        del slab
+        wbytes = base.numel()
+        nbytes = wbytes + 4 * inner + 4 * outer
+        ncopy = copies_for(wbytes)
+        ws = [D.DeviceWeight(base.clone(), t, inner, outer) for _ in range(ncopy)]
+        del base
+        xd = torch.from_numpy(synth.activations(rng, inner)).cuda()
+        ys = torch.empty(ncopy, outer, device="cuda")
+        sweeps = max(4, min(32, int(2e9 // (wbytes * ncopy))))
+        ms = time_sweeps(torch, stream, lambda i: D.gemv(ws[i % ncopy], xd, ys[i % ncopy]), ncopy, sweeps, 2)
+        us = ms * 1e3 / (sweeps * ncopy)
+        read = ""
+        ratio = ""
+        if F is not None:
+            n = wbytes // 16 * 16
+            grid = max(1024, -(-(n // 16) // (256 * 8)))
+            rms = time_sweeps(torch, stream, lambda i: F.ifl_read(ws[i % ncopy].data.data_ptr(), n, 0x9E3779B9,
+                                                                  out.data_ptr(), grid, 256, cs()),
+                              ncopy, sweeps, 2)
+            rus = rms * 1e3 / (sweeps * ncopy)
+            read = f"{rus:.2f}"
+            ratio = f"{us / rus:.2f}"
+        gbs = nbytes / (us * 1e-6) / 1e9
+        print(f"| {name} | {outer} x {inner} | {wbytes / 1e6:.1f} | {ncopy} | {us:.2f} | {gbs:.0f} | "
+              f"{100 * gbs / PEAK_HBM_GBS:.1f} | {read} | {ratio} |", flush=True)
+        del ws, xd, ys
+        torch.cuda.empty_cache()
+
+
 # --------------------------------------------------------------- CPU baseline --
 
 def _host_info():
@@ -736,6 +804,9 @@ def main():
     stream = torch.cuda.Stream()
     if args.floors:
         floors_sweep(torch, stream)
+        return
+    if args.sweep:
+        shape_sweep(torch, stream, synth, D)
         return
     steps, warmup = max(1, args.steps), max(0, args.warmup)
 
