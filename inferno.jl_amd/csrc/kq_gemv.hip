@@ -520,6 +520,173 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
                                             xexp, ssw);
 }
 
+// Persistent form for rows of more than 16 blocks (2..MP passes of 4096
+// columns).  One workgroup per CU stages x's digits for every pass once, in
+// LDS (x loads of all passes issued together, clamped to the last pass so
+// none is predicated).  Each wave then walks items (row group, pass) --
+// groups grid-stride, a group's passes in order -- through NB register
+// buffers, so the next items' weights are in flight while one is reduced
+// and a row's short last pass costs its own bytes rather than a whole
+// pass's latency.  Lanes accumulate across a group's passes and the row sum
+// is taken after its last pass: the same arithmetic in the same order as
+// k_gemv_kwide's serial passes, so the outputs are bit-identical.
+template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB, int MP>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kpm(const uint8_t *__restrict__ W,
+                                                       const uint8_t *__restrict__ W2,
+                                                       const float *__restrict__ x,
+                                                       float *y, int outer, int nblk,
+                                                       const float *__restrict__ nw, float eps,
+                                                       const float *resid, int epi)
+{
+    using F = KFmt<FMT>;
+    constexpr int NM = GATEUP ? 2 : 1;
+    constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
+    constexpr int NT = NWV * 64, NXV = xnv(NT);
+    __shared__ __attribute__((aligned(16))) uint32_t xbuf[MP * 3 * kDigPlaneDw];
+    __shared__ __attribute__((aligned(16))) float xsum[MP * 128];
+    __shared__ __attribute__((aligned(8))) int xexp[MP * 128];
+    __shared__ float ssw[NWV];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = lane >> 2, j = lane & 3;
+    const int inner = nblk * 256;
+    const int npass = (nblk + 15) >> 4; // 2..MP (the launcher checks)
+    const size_t row_bytes = (size_t)nblk * F::BYTES;
+    const int ngroups = (outer + R - 1) / R;
+    const int stride = gridDim.x * NWV;
+    const int g0 = blockIdx.x * NWV + wave;
+    // this wave's items: groups g0, g0 + stride, ... each with npass passes
+    const int nitems = g0 < ngroups ? ((ngroups - 1 - g0) / stride + 1) * npass : 0;
+
+    auto load = [&](KBytes (&B)[NM][R], float (&RV)[R], int t) {
+        const int k = t / npass, p = t - k * npass; // wave-uniform
+        const int gi = min(g0 + k * stride, ngroups - 1);
+        const int blk = p * 16 + (b < min(16, nblk - p * 16) ? b : 0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(gi * R + r, outer - 1);
+            if constexpr (RESID)
+                RV[r] = resid[row]; // wave-uniform: a scalar load
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+                kbytes_load<FMT>((m == 0 ? W : W2) + (size_t)row * row_bytes + (size_t)blk * F::BYTES,
+                                 j, B[m][r]);
+        }
+    };
+
+    // x of every pass (MP passes of loads, the ones past npass repeating the
+    // last), then the first NB items' weights, then the digits into LDS
+    float4 xv[MP][NXV];
+#pragma unroll
+    for (int p = 0; p < MP; ++p)
+        x_load_pass<NT>(x, min(p, npass - 1) * 4096, inner, xv[p]);
+    float ssq = 0.0f;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int p = 0; p < MP; ++p) {
+            float4 wv[NXV];
+            x_load_pass<NT>(nw, min(p, npass - 1) * 4096, inner, wv);
+            if (p < npass) { // wave-uniform; the loads above are not under it
+#pragma unroll
+                for (int k = 0; k < NXV; ++k) {
+                    ssq = fmaf(xv[p][k].x, xv[p][k].x, ssq);
+                    ssq = fmaf(xv[p][k].y, xv[p][k].y, ssq);
+                    ssq = fmaf(xv[p][k].z, xv[p][k].z, ssq);
+                    ssq = fmaf(xv[p][k].w, xv[p][k].w, ssq);
+                    xv[p][k] = make_float4(xv[p][k].x * wv[k].x, xv[p][k].y * wv[k].y,
+                                           xv[p][k].z * wv[k].z, xv[p][k].w * wv[k].w);
+                }
+            }
+        }
+    }
+    KBytes B[NB][NM][R];
+    float RV[NB][R];
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+        load(B[q], RV[q], q);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < MP; ++p)
+        if (p < npass)
+            x_stage_dig<NT>(xbuf + p * 3 * kDigPlaneDw, xsum + p * 128, xexp + p * 128, xv[p]);
+    float scale = 1.0f;
+    if constexpr (NORM) {
+        const float t = wave_sum(ssq);
+        if (lane == 0)
+            ssw[wave] = t;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NWV; ++i)
+            tot += ssw[i];
+        scale = 1.0f / sqrtf(tot / (float)inner + eps);
+    } else {
+        __syncthreads();
+    }
+
+    float acc[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+    auto reduce = [&](const KBytes (&Bq)[NM][R], const float (&RVq)[R], int t) {
+        const int k = t / npass, p = t - k * npass; // wave-uniform
+        const int gi = g0 + k * stride;
+        const bool active = b < min(16, nblk - p * 16);
+        XDig X;
+        x_from_lds_dig(xbuf + p * 3 * kDigPlaneDw, xsum + p * 128, xexp + p * 128, b, j, X);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const float c = kdig_dot<FMT>(Bq[m][r], j, X);
+                acc[m][r] += active ? c : 0.0f;
+            }
+        if (p == npass - 1) { // the group's last pass: its rows are done
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = gi * R + r;
+                float v[NM];
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    v[m] = wave_sum(acc[m][r]) * scale;
+                    acc[m][r] = 0.0f;
+                }
+                float o = v[0];
+                if constexpr (GATEUP)
+                    o = (v[0] / (1.0f + expf(-v[0]))) * v[1]; // src/ModelCPU.jl:492-503
+                // every lane holds the row's value: an unpredicated store (a
+                // row past `outer` rewrites row outer - 1 with its own value)
+                y[min(row, outer - 1)] = RESID ? epi_apply(RVq[r], o, epi) : o;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // steady state: every buffer is refilled with an item that exists
+    int t = 0;
+    for (; t + (2 * NB - 1) < nitems; t += NB) { // wave-uniform
+#pragma unroll
+        for (int q = 0; q < NB; ++q) {
+            reduce(B[q], RV[q], t + q);
+            load(B[q], RV[q], t + q + NB);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+        if (t + q < nitems)
+            reduce(B[q], RV[q], t + q);
+        if (t + q + NB < nitems)
+            load(B[q], RV[q], t + q + NB);
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+        if (t + q + NB < nitems)
+            reduce(B[q], RV[q], t + q + NB);
+}
+
 // ------------------------------------------------------------------------
 // Streamed kernels (Q6_K, Q8_0, IQ4_NL)
 // ------------------------------------------------------------------------
@@ -1179,12 +1346,32 @@ static int device_cus()
     return ncu;
 }
 
+// k_gemv_kpm with the smallest pass capacity that holds the row.
+template <int FMT, bool GATEUP, bool EXT>
+static void launch_kpm(int npass, int grid, const uint8_t *W, const uint8_t *W2, const float *x,
+                       float *y, int outer, int nblk, const float *nw, float eps, const float *resid,
+                       int epi, hipStream_t s)
+{
+    constexpr int NWV = 8, NB = 2;
+    if (npass <= 2)
+        hipLaunchKernelGGL((k_gemv_kpm<FMT, 1, GATEUP, EXT, NWV, NB, 2>), dim3(grid), dim3(NWV * 64), 0, s,
+                           W, W2, x, y, outer, nblk, nw, eps, resid, epi);
+    else
+        hipLaunchKernelGGL((k_gemv_kpm<FMT, 1, GATEUP, EXT, NWV, NB, 4>), dim3(grid), dim3(NWV * 64), 0, s,
+                           W, W2, x, y, outer, nblk, nw, eps, resid, epi);
+}
+
 // Q4_K / Q5_K: 8-wave workgroups; two rows per wave for the GEMV, one gate and
 // one up row per wave for the fused gate/up (measured on MI355X at 4096 x 4096
 // and 2 x 12288 x 4096).  Rows of at most 4096 columns with at least four row
 // groups per wave over one workgroup per CU take the persistent kernel (2 x
 // 12288 x 4096 gate/up 12.7 us against 13.9 us; at 4096 x 4096 one row group
-// per wave is all there is and the plain kernel is faster).
+// per wave is all there is and the plain kernel is faster).  Rows of 17..64
+// blocks take the persistent multi-pass kernel when the serial kernel's
+// workgroups do not divide evenly over the CUs (5120 x 5120 7.8-8.8 us
+// against 8.5-8.6, 5120 x 13824 13.9-15.1 against 16.2-16.4, 13824 x 5120
+// 14.6-14.9 against 15.4-15.6); at 4096 rows the serial kernel's one
+// workgroup per CU is faster (4096 x 11008 9.7-10.0 us against 10.7-11.2).
 template <int FMT, bool GATEUP>
 static hipError_t launch_kwide(const void *w, const void *w2, const float *x, float *y,
                                int inner, int outer, hipStream_t s, const float *nw = nullptr,
@@ -1202,6 +1389,13 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
         else
             hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, false, NWV, NB>), dim3(grid), dim3(NWV * 64),
                                0, s, W, W2, x, y, outer, nblk, nw, eps, resid, epi);
+    } else if (nblk > 16 && nblk <= 4 * 16 && ((outer + NWV * R - 1) / (NWV * R)) % device_cus() != 0) {
+        const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
+        const int npass = (nblk + 15) / 16;
+        if (ext)
+            launch_kpm<FMT, GATEUP, true>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
+        else
+            launch_kpm<FMT, GATEUP, false>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
     } else {
         const dim3 grid((outer + NWV * R - 1) / (NWV * R));
         if (ext)

@@ -81,6 +81,8 @@ FFN_CASES = [
     (2560, 9728, synth.Q4_K, synth.Q6_K),    # down rows of 38 blocks at byte phases
     (512, 768, synth.Q8_0, synth.Q8_0),      # unfused gate/up: norm kernel first
     (4096, 1536, synth.Q4_K, synth.Q6_K),    # one GPU's share of the decode FFN over 8 GPUs
+    (2048, 5120, synth.Q5_K, synth.Q5_K),    # residual in a persistent two-pass down
+    (12288, 512, synth.Q4_K, synth.Q4_K),    # norm folded into a persistent four-pass gate/up
 ]
 
 

@@ -155,6 +155,12 @@ GEMV_CASES = [
     (synth.IQ4_NL, 5, 96),        # 3 blocks a row, at byte phases
     (synth.Q4_K, 1536, 4096),     # one GPU's gate/up rows of the FFN over 8 GPUs
     (synth.Q6_K, 4096, 1536),     # one GPU's down-projection columns (6 blocks a row)
+    (synth.Q4_K, 300, 5120),      # 16 + 4 blocks: persistent multi-pass kernel, 2-pass capacity
+    (synth.Q5_K, 77, 11008),      # 43 blocks: 3 passes, the last partial (4-pass capacity)
+    (synth.Q4_K, 2000, 13824),    # 54 blocks, many row groups per wave
+    (synth.Q4_K, 64, 28672),      # 112 blocks: 7 passes (8-pass capacity)
+    (synth.Q4_K, 10, 33024),      # 129 blocks: past the persistent kernel, serial passes
+    (synth.Q4_K, 4096, 5120),     # 256 workgroups over 256 CUs: serial passes, the last partial
 ]
 
 
@@ -225,6 +231,7 @@ LAUNCH_SHAPES = [
     (synth.Q6_K, 33, 2304), (synth.Q8_0, 13, 896), (synth.Q8_0, 1000, 2336), (synth.IQ4_NL, 9, 2336),
     (synth.IQ4_NL, 517, 4640), (synth.Q6_K, 1031, 32512), (synth.Q8_0, 3, 32),
     (synth.Q8_0, 5, 34816),
+    (synth.Q5_K, 100, 5120),    # persistent multi-pass kernel, 2-pass capacity
 ]
 
 
@@ -260,8 +267,11 @@ def test_gemv_every_launch(t, outer, inner):
 
 @pytest.mark.parametrize("hidden,inter", [
     (4096, 1030),   # wide kernel, one gate and one up row per wave
-    (8448, 515),    # three passes, the last partial
-    (14336, 300),   # four passes
+    (8448, 515),    # persistent multi-pass kernel: three passes, the last partial
+    (14336, 300),   # persistent multi-pass kernel: four passes
+    (5120, 600),    # persistent multi-pass kernel, 2-pass capacity
+    (5120, 2048),   # 256 workgroups over 256 CUs: serial passes
+    (20480, 64),    # 80 blocks: past the persistent kernel, serial passes
     (4096, 8195),   # persistent kernel
     (2560, 8200),   # persistent kernel, partial pass
 ])
