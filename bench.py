@@ -647,7 +647,7 @@ def shape_sweep(torch, stream, synth, D):
         del base
         xd = torch.from_numpy(synth.activations(rng, inner)).cuda()
         ys = torch.empty(ncopy, outer, device="cuda")
-        sweeps = max(4, min(32, int(2e9 // (wbytes * ncopy))))
+        sweeps = max(8, min(64, int(2e10 // (wbytes * ncopy))))  # 4-10 ms timed per shape
         ms = time_sweeps(torch, stream, lambda i: D.gemv(ws[i % ncopy], xd, ys[i % ncopy]), ncopy, sweeps, 2)
         us = ms * 1e3 / (sweeps * ncopy)
         read = ""

@@ -1396,6 +1396,18 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
             launch_kpm<FMT, GATEUP, true>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
         else
             launch_kpm<FMT, GATEUP, false>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
+    } else if (!GATEUP && (outer + NWV - 1) / NWV <= device_cus()) {
+        // no more one-row workgroups than CUs: one row per wave, all of them
+        // at once (2048 x 2048 2.8-3.1 us against 3.5-3.6 with two rows per
+        // wave; 3072 x 3072 keeps two rows: 1.5 one-row workgroups per CU
+        // measured 4.5 us against 4.1)
+        const dim3 grid((outer + NWV - 1) / NWV);
+        if (ext)
+            hipLaunchKernelGGL((k_gemv_kwide<FMT, 1, false, true, NWV>), grid, dim3(NWV * 64), 0, s, W,
+                               W2, x, y, outer, nblk, nw, eps, resid, epi);
+        else
+            hipLaunchKernelGGL((k_gemv_kwide<FMT, 1, false, false, NWV>), grid, dim3(NWV * 64), 0, s, W,
+                               W2, x, y, outer, nblk, nw, eps, resid, epi);
     } else {
         const dim3 grid((outer + NWV * R - 1) / (NWV * R));
         if (ext)
