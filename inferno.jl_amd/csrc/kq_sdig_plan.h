@@ -340,6 +340,16 @@ inline SdigPlan sdig_plan(int fmt, int nblk, int outer, bool argmax, int ncu)
         p.nw = 8;
         per_cu = 2;
     }
+    // Two-segment rows of fewer 16-row chunks than CUs: 8-row chunks on
+    // 8-wave workgroups, two per CU, so no CU idles (2048 x 4096 Q6_K 5.5 us
+    // against 6.2, IQ4_NL 4.9 against 5.8; at 4096 rows, one 16-row chunk per
+    // CU, the 12-wave plan stays: 6.3 us against 7.1 with 8-row chunks and
+    // 7.4 with 16 waves).
+    if (p.nseg == 2 && (outer + 15) / 16 < ncu1) {
+        p.nw = 8;
+        per_cu = 2;
+        p.rpc = 8;
+    }
     const int resident = ncu1 * per_cu;
     // rows of the busiest resident slot with r rows per chunk
     auto busiest = [&](int r) { return ((outer + r - 1) / r + resident - 1) / resident * r; };
