@@ -213,7 +213,7 @@ __device__ __forceinline__ void wait_vmcnt(int n)
 #undef IHIP_VM
 }
 
-// ---- Q4_K / Q5_K blocks as lanes load them ------------------------------
+// ---- Q4_K / Q5_K (and IQ4_NL) blocks as lanes load them -----------------
 // Lane (block b, sub-block pair j): the block header (d, dmin, scales), the 32
 // qs bytes of pair j (low nibbles: sub-block 2j, high: 2j + 1) and (Q5_K) the
 // 32 qh bytes, as 128-bit loads (both block sizes are 16-byte multiples).
@@ -228,6 +228,14 @@ struct KFmt<kQ5_K> {
     static constexpr int BYTES = 176, QS = 48;
 };
 
+// IQ4_NL as eight 18-byte blocks per 256 columns (144 bytes, a 16-byte
+// multiple): lane j's 36 bytes are blocks 2j and 2j + 1, which start j dwords
+// into the three 16-byte units at or below byte 36 j.
+template <>
+struct KFmt<kIQ4_NL> {
+    static constexpr int BYTES = 144, QS = 0;
+};
+
 struct KBytes {
     uint4 h, q0, q1, e0, e1;
 };
@@ -236,6 +244,13 @@ template <int FMT>
 __device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int j, KBytes &B)
 {
     using F = KFmt<FMT>;
+    if constexpr (FMT == kIQ4_NL) {
+        const uint8_t *u = blk + ((36 * j) & ~15);
+        B.h = *reinterpret_cast<const uint4 *>(u);
+        B.q0 = *reinterpret_cast<const uint4 *>(u + 16);
+        B.q1 = *reinterpret_cast<const uint4 *>(u + 32);
+        return;
+    }
     B.h = *reinterpret_cast<const uint4 *>(blk);
     B.q0 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j);
     B.q1 = *reinterpret_cast<const uint4 *>(blk + F::QS + 32 * j + 16);

@@ -201,13 +201,89 @@ __device__ __forceinline__ float dig_combine(uint32_t s0, uint32_t s1, int s2)
     return fmaf((float)(int)(((uint32_t)s2 << 8) + s1), 256.0f, (float)s0);
 }
 
+// IQ4_NL weights (src/Dequant.jl:683-693: element j = low nibble of qs[j],
+// element j + 16 = high nibble; weight = d * grid[nibble], grid
+// src/QuantsData.jl:384).  The grid, biased by +128 to unsigned bytes, is
+// looked up four nibbles at a time with byte permutes (grid[0..7] and
+// grid[8..15], then a choice by the nibble's bit 3); the bias comes back off
+// exactly in the integer sums (iq4nl_dot_dig).
+constexpr uint32_t kIQ4G0 = 0x3F2D1801u; // grid + 128: 1, 24, 45, 63
+constexpr uint32_t kIQ4G1 = 0x766A5D4Fu; // 79, 93, 106, 118
+constexpr uint32_t kIQ4G2 = 0xA6998D81u; // 129, 141, 153, 166
+constexpr uint32_t kIQ4G3 = 0xF1D9C5B5u; // 181, 197, 217, 241
+
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t nib) // four nibbles in bytes
+{
+    const uint32_t n7 = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIQ4G1, kIQ4G0, n7); // bytes 0-3 of G0, 4-7 of G1
+    const uint32_t hi = __builtin_amdgcn_perm(kIQ4G3, kIQ4G2, n7);
+    const uint32_t pick = 0x03020100u + ((nib & 0x08080808u) >> 1); // byte i of lo or of hi
+    return __builtin_amdgcn_perm(hi, lo, pick);
+}
+
+__device__ __forceinline__ uint32_t sel_u32(int c, uint32_t a, uint32_t b) { return c ? a : b; }
+
 // One lane's contribution to one row: its two sub-blocks (2j, 2j + 1) of
 // block b, d * (sc_A * sum_A + sc_B * sum_B) - dmin * (m_A * xsum_A + m_B *
 // xsum_B) (src/Dequant.jl:364-371), the weight sums formed exactly on the
 // integer dot units.
+//
+// IQ4_NL: blocks 2j and 2j + 1 of the 8 in the 144-byte unit, d * sum over
+// grid[q] x per block (no mins).  The looked-up bytes carry the grid's +128
+// bias; 128 * (the block's digit sums) takes it off again exactly.  A block
+// of x holding a non-finite value (its fp32 sum NaN) makes the lane's sum NaN.
 template <int FMT>
 __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
 {
+    if constexpr (FMT == kIQ4_NL) {
+        const uint32_t w[12] = {B.h.x,  B.h.y,  B.h.z,  B.h.w,  B.q0.x, B.q0.y,
+                                B.q0.z, B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w};
+        // the lane's 9 dwords start j dwords in: rotate by j, one select per
+        // dword and bit of j (selects of values: a conditional of two array
+        // elements is an lvalue, a select of addresses that keeps the arrays
+        // out of registers)
+        uint32_t t1[11], D[9];
+#pragma unroll
+        for (int k = 0; k < 11; ++k) t1[k] = sel_u32(j & 1, w[k + 1], w[k]);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) D[k] = sel_u32(j & 2, t1[k + 2], t1[k]);
+        // block A: d in bytes 0-1, qs in bytes 2-17; block B: d in 18-19, qs in 20-35
+        uint32_t a0 = 0, a1 = 0, c0 = 0, c1 = 0, z0a = 0, z1a = 0, z0c = 0, z1c = 0;
+        int a2 = 0, c2 = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t qa = __builtin_amdgcn_alignbyte(D[t + 1], D[t], 2);
+            const uint32_t qc = D[5 + t];
+            const uint32_t la = iq4nl_lookup(qa & 0x0f0f0f0fu);        // elements 4t + b of A
+            const uint32_t ha = iq4nl_lookup((qa >> 4) & 0x0f0f0f0fu); // 16 + 4t + b of A
+            const uint32_t lc = iq4nl_lookup(qc & 0x0f0f0f0fu);
+            const uint32_t hc = iq4nl_lookup((qc >> 4) & 0x0f0f0f0fu);
+            a0 = __builtin_amdgcn_udot4(la, X.p[0][t], a0, false);
+            a0 = __builtin_amdgcn_udot4(ha, X.p[0][4 + t], a0, false);
+            a1 = __builtin_amdgcn_udot4(la, X.p[1][t], a1, false);
+            a1 = __builtin_amdgcn_udot4(ha, X.p[1][4 + t], a1, false);
+            a2 = __builtin_amdgcn_sdot4((int)(la ^ 0x80808080u), (int)X.p[2][t], a2, false);
+            a2 = __builtin_amdgcn_sdot4((int)(ha ^ 0x80808080u), (int)X.p[2][4 + t], a2, false);
+            c0 = __builtin_amdgcn_udot4(lc, X.p[0][8 + t], c0, false);
+            c0 = __builtin_amdgcn_udot4(hc, X.p[0][12 + t], c0, false);
+            c1 = __builtin_amdgcn_udot4(lc, X.p[1][8 + t], c1, false);
+            c1 = __builtin_amdgcn_udot4(hc, X.p[1][12 + t], c1, false);
+            c2 = __builtin_amdgcn_sdot4((int)(lc ^ 0x80808080u), (int)X.p[2][8 + t], c2, false);
+            c2 = __builtin_amdgcn_sdot4((int)(hc ^ 0x80808080u), (int)X.p[2][12 + t], c2, false);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            z0a = __builtin_amdgcn_udot4(0x80808080u, X.p[0][t], z0a, false);
+            z1a = __builtin_amdgcn_udot4(0x80808080u, X.p[1][t], z1a, false);
+            z0c = __builtin_amdgcn_udot4(0x80808080u, X.p[0][8 + t], z0c, false);
+            z1c = __builtin_amdgcn_udot4(0x80808080u, X.p[1][8 + t], z1c, false);
+        }
+        const float vA = fmaf(fmaf((float)a2, 256.0f, (float)(int)(a1 - z1a)), 256.0f, (float)(int)(a0 - z0a));
+        const float vC = fmaf(fmaf((float)c2, 256.0f, (float)(int)(c1 - z1c)), 256.0f, (float)(int)(c0 - z0c));
+        const float dA = h2f(D[0] & 0xffffu), dC = h2f(D[4] >> 16);
+        return fmaf(dA, __builtin_ldexpf(vA, X.ea - 22) + X.sa * 0.0f,
+                    dC * (__builtin_ldexpf(vC, X.eb - 22) + X.sb * 0.0f));
+    }
     const uint32_t qw[8] = {B.q0.x, B.q0.y, B.q0.z, B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w};
     uint32_t a0 = 0, a1 = 0, c0 = 0, c1 = 0;
     int a2 = 0, c2 = 0;
@@ -712,26 +788,6 @@ struct SFmt<kIQ4_NL> {
 static_assert(SFmt<kQ6_K>::SEG_BYTES % 16 == 0, "Q6_K segment must be 16-byte aligned");
 static_assert(SFmt<kQ8_0>::SEG_BYTES % 16 == 0, "Q8_0 segment must be 16-byte aligned");
 static_assert(SFmt<kIQ4_NL>::SEG_BYTES % 16 == 0, "IQ4_NL segment must be 16-byte aligned");
-
-// IQ4_NL weights (src/Dequant.jl:683-693: element j = low nibble of qs[j],
-// element j + 16 = high nibble; weight = d * grid[nibble], grid
-// src/QuantsData.jl:384).  The grid, biased by +128 to unsigned bytes, is
-// looked up four nibbles at a time with byte permutes (grid[0..7] and
-// grid[8..15], then a choice by the nibble's bit 3); the bias comes back off
-// exactly in the integer sums (iq4nl_dot_dig).
-constexpr uint32_t kIQ4G0 = 0x3F2D1801u; // grid + 128: 1, 24, 45, 63
-constexpr uint32_t kIQ4G1 = 0x766A5D4Fu; // 79, 93, 106, 118
-constexpr uint32_t kIQ4G2 = 0xA6998D81u; // 129, 141, 153, 166
-constexpr uint32_t kIQ4G3 = 0xF1D9C5B5u; // 181, 197, 217, 241
-
-__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t nib) // four nibbles in bytes
-{
-    const uint32_t n7 = nib & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(kIQ4G1, kIQ4G0, n7); // bytes 0-3 of G0, 4-7 of G1
-    const uint32_t hi = __builtin_amdgcn_perm(kIQ4G3, kIQ4G2, n7);
-    const uint32_t pick = 0x03020100u + ((nib & 0x08080808u) >> 1); // byte i of lo or of hi
-    return __builtin_amdgcn_perm(hi, lo, pick);
-}
 
 // ---- greedy argmax partials ----------------------------------------------
 // key = (order-preserving bits of the value << 32) | (0xffffffff - index), so
@@ -1346,6 +1402,13 @@ static int device_cus()
     return ncu;
 }
 
+// Rows of 17..64 blocks whose 8-wave, R-rows-per-wave workgroups would not
+// divide evenly over the CUs take the persistent multi-pass kernel.
+static bool kwide_takes_kpm(int nblk, int outer, int R)
+{
+    return nblk > 16 && nblk <= 4 * 16 && ((outer + 8 * R - 1) / (8 * R)) % device_cus() != 0;
+}
+
 // k_gemv_kpm with the smallest pass capacity that holds the row.
 template <int FMT, bool GATEUP, bool EXT>
 static void launch_kpm(int npass, int grid, const uint8_t *W, const uint8_t *W2, const float *x,
@@ -1389,13 +1452,15 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
         else
             hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, false, NWV, NB>), dim3(grid), dim3(NWV * 64),
                                0, s, W, W2, x, y, outer, nblk, nw, eps, resid, epi);
-    } else if (nblk > 16 && nblk <= 4 * 16 && ((outer + NWV * R - 1) / (NWV * R)) % device_cus() != 0) {
-        const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
-        const int npass = (nblk + 15) / 16;
-        if (ext)
-            launch_kpm<FMT, GATEUP, true>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
-        else
-            launch_kpm<FMT, GATEUP, false>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
+    } else if (FMT != kIQ4_NL && kwide_takes_kpm(nblk, outer, R)) {
+        if constexpr (FMT != kIQ4_NL) {
+            const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
+            const int npass = (nblk + 15) / 16;
+            if (ext)
+                launch_kpm<FMT, GATEUP, true>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
+            else
+                launch_kpm<FMT, GATEUP, false>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
+        }
     } else if (!GATEUP && (outer + NWV - 1) / NWV <= device_cus()) {
         // no more one-row workgroups than CUs: one row per wave, all of them
         // at once (2048 x 2048 2.8-3.1 us against 3.5-3.6 with two rows per
@@ -1488,7 +1553,14 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
     case kQ6_K: return launch_sdig<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     case kQ8_0: return launch_sdig<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
-    case kIQ4_NL: return launch_sdig<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kIQ4_NL:
+        // rows of whole 256-column units take the wide kernels' lane layout,
+        // except where the persistent multi-pass kernel would run (its IQ4_NL
+        // dot from LDS digits measured slower than the streamed kernel:
+        // 5120 x 5120 10.9 us against 10.3)
+        return inner % 256 == 0 && !kwide_takes_kpm(inner / 256, outer, 2)
+                   ? launch_kwide<kIQ4_NL, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi)
+                   : launch_sdig<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     default: return hipErrorInvalidValue;
     }
 }

@@ -161,6 +161,8 @@ GEMV_CASES = [
     (synth.Q4_K, 64, 28672),      # 112 blocks: 7 passes (8-pass capacity)
     (synth.Q4_K, 10, 33024),      # 129 blocks: past the persistent kernel, serial passes
     (synth.Q4_K, 4096, 5120),     # 256 workgroups over 256 CUs: serial passes, the last partial
+    (synth.IQ4_NL, 8200, 2048),   # IQ4_NL in the persistent wide kernel
+    (synth.IQ4_NL, 4096, 4096),   # IQ4_NL in the wide kernel, one workgroup per CU
 ]
 
 
@@ -290,7 +292,7 @@ def test_gate_up_every_launch(t, hidden, inter):
     assert_within(h, g / (1 + np.exp(-g)) * u, hb, "h")
 
 
-@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0])
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0, synth.IQ4_NL])
 def test_gemv_activation_dynamic_range(t):
     """Sub-blocks of x spread over 10^-30 .. 10^30 (fp32 subnormals included):
     the integer-digit activations scale every 32-element sub-block on its own,
@@ -323,7 +325,7 @@ def test_gemv_nonfinite_activations():
     from inferno_hip import device as D
     rng = synth.rng_for(4343)
     outer, inner = 64, 4096
-    for t in (synth.Q4_K, synth.Q5_K):
+    for t in (synth.Q4_K, synth.Q5_K, synth.IQ4_NL):
         w = synth.weight(rng, t, outer, inner)
         dw = dweight(w, t, inner, outer)
         for bad in (np.nan, np.inf, -np.inf):
