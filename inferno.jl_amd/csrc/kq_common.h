@@ -236,6 +236,14 @@ struct KFmt<kIQ4_NL> {
     static constexpr int BYTES = 144, QS = 0;
 };
 
+// Q8_0 likewise: eight 34-byte blocks per 256 columns (272 bytes); lane j's
+// 68 bytes are blocks 2j and 2j + 1, starting j dwords into the five 16-byte
+// units at or below byte 68 j.
+template <>
+struct KFmt<kQ8_0> {
+    static constexpr int BYTES = 272, QS = 0;
+};
+
 struct KBytes {
     uint4 h, q0, q1, e0, e1;
 };
@@ -249,6 +257,15 @@ __device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int
         B.h = *reinterpret_cast<const uint4 *>(u);
         B.q0 = *reinterpret_cast<const uint4 *>(u + 16);
         B.q1 = *reinterpret_cast<const uint4 *>(u + 32);
+        return;
+    }
+    if constexpr (FMT == kQ8_0) {
+        const uint8_t *u = blk + ((68 * j) & ~15);
+        B.h = *reinterpret_cast<const uint4 *>(u);
+        B.q0 = *reinterpret_cast<const uint4 *>(u + 16);
+        B.q1 = *reinterpret_cast<const uint4 *>(u + 32);
+        B.e0 = *reinterpret_cast<const uint4 *>(u + 48);
+        B.e1 = *reinterpret_cast<const uint4 *>(u + 64);
         return;
     }
     B.h = *reinterpret_cast<const uint4 *>(blk);

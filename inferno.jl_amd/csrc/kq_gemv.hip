@@ -284,6 +284,41 @@ __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
         return fmaf(dA, __builtin_ldexpf(vA, X.ea - 22) + X.sa * 0.0f,
                     dC * (__builtin_ldexpf(vC, X.eb - 22) + X.sb * 0.0f));
     }
+    if constexpr (FMT == kQ8_0) {
+        const uint32_t w[20] = {B.h.x,  B.h.y,  B.h.z,  B.h.w,  B.q0.x, B.q0.y, B.q0.z,
+                                B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w, B.e0.x, B.e0.y,
+                                B.e0.z, B.e0.w, B.e1.x, B.e1.y, B.e1.z, B.e1.w};
+        uint32_t t1[19], D[17];
+#pragma unroll
+        for (int k = 0; k < 19; ++k) t1[k] = sel_u32(j & 1, w[k + 1], w[k]);
+#pragma unroll
+        for (int k = 0; k < 17; ++k) D[k] = sel_u32(j & 2, t1[k + 2], t1[k]);
+        // block A: d in bytes 0-1, qs in 2-33; block B: d in 34-35, qs in 36-67.
+        // Signed weights: q + 128 (q ^ 0x80) on the unsigned planes, the
+        // bias taken off as 128 * (digit sums); q itself on the signed plane.
+        uint32_t a0 = 0, a1 = 0, c0 = 0, c1 = 0, z0a = 0, z1a = 0, z0c = 0, z1c = 0;
+        int a2 = 0, c2 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t qa = __builtin_amdgcn_alignbyte(D[t + 1], D[t], 2);
+            const uint32_t qc = D[9 + t];
+            a0 = __builtin_amdgcn_udot4(qa ^ 0x80808080u, X.p[0][t], a0, false);
+            a1 = __builtin_amdgcn_udot4(qa ^ 0x80808080u, X.p[1][t], a1, false);
+            a2 = __builtin_amdgcn_sdot4((int)qa, (int)X.p[2][t], a2, false);
+            c0 = __builtin_amdgcn_udot4(qc ^ 0x80808080u, X.p[0][8 + t], c0, false);
+            c1 = __builtin_amdgcn_udot4(qc ^ 0x80808080u, X.p[1][8 + t], c1, false);
+            c2 = __builtin_amdgcn_sdot4((int)qc, (int)X.p[2][8 + t], c2, false);
+            z0a = __builtin_amdgcn_udot4(0x80808080u, X.p[0][t], z0a, false);
+            z1a = __builtin_amdgcn_udot4(0x80808080u, X.p[1][t], z1a, false);
+            z0c = __builtin_amdgcn_udot4(0x80808080u, X.p[0][8 + t], z0c, false);
+            z1c = __builtin_amdgcn_udot4(0x80808080u, X.p[1][8 + t], z1c, false);
+        }
+        const float vA = fmaf(fmaf((float)a2, 256.0f, (float)(int)(a1 - z1a)), 256.0f, (float)(int)(a0 - z0a));
+        const float vC = fmaf(fmaf((float)c2, 256.0f, (float)(int)(c1 - z1c)), 256.0f, (float)(int)(c0 - z0c));
+        const float dA = h2f(D[0] & 0xffffu), dC = h2f(D[8] >> 16);
+        return fmaf(dA, __builtin_ldexpf(vA, X.ea - 22) + X.sa * 0.0f,
+                    dC * (__builtin_ldexpf(vC, X.eb - 22) + X.sb * 0.0f));
+    }
     const uint32_t qw[8] = {B.q0.x, B.q0.y, B.q0.z, B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w};
     uint32_t a0 = 0, a1 = 0, c0 = 0, c1 = 0;
     int a2 = 0, c2 = 0;
@@ -1409,6 +1444,13 @@ static bool kwide_takes_kpm(int nblk, int outer, int R)
     return nblk > 16 && nblk <= 4 * 16 && ((outer + 8 * R - 1) / (8 * R)) % device_cus() != 0;
 }
 
+// Rows of at most 16 blocks with at least four 8-wave row groups per wave
+// over one workgroup per CU take the persistent kernel.
+static bool kwide_takes_kpers(int nblk, int outer) { return nblk <= 16 && outer >= 4 * 8 * 256; }
+
+// No more one-row workgroups of 8 waves than CUs: one row per wave.
+static bool kwide_one_row(int outer) { return (outer + 7) / 8 <= device_cus(); }
+
 // k_gemv_kpm with the smallest pass capacity that holds the row.
 template <int FMT, bool GATEUP, bool EXT>
 static void launch_kpm(int npass, int grid, const uint8_t *W, const uint8_t *W2, const float *x,
@@ -1444,7 +1486,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
     const int nblk = inner / 256;
     const bool ext = GATEUP ? nw != nullptr : resid != nullptr;
     const uint8_t *W = (const uint8_t *)w, *W2 = (const uint8_t *)w2;
-    if (nblk <= 16 && outer >= 4 * NWV * 256) {
+    if (kwide_takes_kpers(nblk, outer)) {
         const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
         if (ext)
             hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, true, NWV, NB>), dim3(grid), dim3(NWV * 64),
@@ -1452,8 +1494,8 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
         else
             hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, false, NWV, NB>), dim3(grid), dim3(NWV * 64),
                                0, s, W, W2, x, y, outer, nblk, nw, eps, resid, epi);
-    } else if (FMT != kIQ4_NL && kwide_takes_kpm(nblk, outer, R)) {
-        if constexpr (FMT != kIQ4_NL) {
+    } else if (FMT != kIQ4_NL && FMT != kQ8_0 && kwide_takes_kpm(nblk, outer, R)) {
+        if constexpr (FMT != kIQ4_NL && FMT != kQ8_0) {
             const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
             const int npass = (nblk + 15) / 16;
             if (ext)
@@ -1461,7 +1503,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
             else
                 launch_kpm<FMT, GATEUP, false>(npass, grid, W, W2, x, y, outer, nblk, nw, eps, resid, epi, s);
         }
-    } else if (!GATEUP && (outer + NWV - 1) / NWV <= device_cus()) {
+    } else if (!GATEUP && kwide_one_row(outer)) {
         // no more one-row workgroups than CUs: one row per wave, all of them
         // at once (2048 x 2048 2.8-3.1 us against 3.5-3.6 with two rows per
         // wave; 3072 x 3072 keeps two rows: 1.5 one-row workgroups per CU
@@ -1552,7 +1594,16 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     case kQ4_K: return launch_kwide<kQ4_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
     case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
     case kQ6_K: return launch_sdig<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
-    case kQ8_0: return launch_sdig<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
+    case kQ8_0:
+        // the wide lane layout where the persistent kernel runs or one row per
+        // wave fits the CUs at once (14336 x 4096 13.9 us against 14.9;
+        // 2048 x 4096 4.2 against 5.3, 1024 x 4096 3.5 against 4.7); at 4096
+        // rows and for several passes the streamed kernel is faster
+        // (4096 x 4096 6.2 against 6.6, 4096 x 14336 16.2 against 17.7)
+        return inner % 256 == 0 && inner <= 4096 &&
+                       (kwide_takes_kpers(inner / 256, outer) || kwide_one_row(outer))
+                   ? launch_kwide<kQ8_0, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi)
+                   : launch_sdig<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     case kIQ4_NL:
         // rows of whole 256-column units take the wide kernels' lane layout,
         // except where the persistent multi-pass kernel would run (its IQ4_NL

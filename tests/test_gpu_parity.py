@@ -163,6 +163,8 @@ GEMV_CASES = [
     (synth.Q4_K, 4096, 5120),     # 256 workgroups over 256 CUs: serial passes, the last partial
     (synth.IQ4_NL, 8200, 2048),   # IQ4_NL in the persistent wide kernel
     (synth.IQ4_NL, 4096, 4096),   # IQ4_NL in the wide kernel, one workgroup per CU
+    (synth.Q8_0, 8200, 2048),     # Q8_0 in the persistent wide kernel
+    (synth.Q8_0, 1024, 4096),     # Q8_0 in the wide kernel, one row per wave
 ]
 
 
@@ -325,7 +327,7 @@ def test_gemv_nonfinite_activations():
     from inferno_hip import device as D
     rng = synth.rng_for(4343)
     outer, inner = 64, 4096
-    for t in (synth.Q4_K, synth.Q5_K, synth.IQ4_NL):
+    for t in (synth.Q4_K, synth.Q5_K, synth.Q8_0, synth.IQ4_NL):
         w = synth.weight(rng, t, outer, inner)
         dw = dweight(w, t, inner, outer)
         for bad in (np.nan, np.inf, -np.inf):
