@@ -1437,11 +1437,17 @@ static int device_cus()
     return ncu;
 }
 
-// Rows of 17..64 blocks whose 8-wave, R-rows-per-wave workgroups would not
-// divide evenly over the CUs take the persistent multi-pass kernel.
-static bool kwide_takes_kpm(int nblk, int outer, int R)
+// Rows of 17..64 blocks whose 8-wave workgroups (two rows per wave for the
+// GEMV, one gate/up row pair for the fused gate/up) would not divide evenly
+// over the CUs take the persistent multi-pass kernel; the fused gate/up only
+// with more row pairs than one per wave of one workgroup per CU (5120 ->
+// 1280 5.5 us serial against 5.9, 8192 -> 1024 6.1 against 6.4; 5120 ->
+// 13824 20.6-21.2 against 26.0-26.4).
+static bool kwide_takes_kpm(int nblk, int outer, bool gateup)
 {
-    return nblk > 16 && nblk <= 4 * 16 && ((outer + 8 * R - 1) / (8 * R)) % device_cus() != 0;
+    const int R = gateup ? 1 : 2;
+    return nblk > 16 && nblk <= 4 * 16 && ((outer + 8 * R - 1) / (8 * R)) % device_cus() != 0 &&
+           (!gateup || (outer + 7) / 8 > device_cus());
 }
 
 // Rows of at most 16 blocks with at least four 8-wave row groups per wave
@@ -1494,7 +1500,7 @@ static hipError_t launch_kwide(const void *w, const void *w2, const float *x, fl
         else
             hipLaunchKernelGGL((k_gemv_kpers<FMT, 1, GATEUP, false, NWV, NB>), dim3(grid), dim3(NWV * 64),
                                0, s, W, W2, x, y, outer, nblk, nw, eps, resid, epi);
-    } else if (FMT != kIQ4_NL && FMT != kQ8_0 && kwide_takes_kpm(nblk, outer, R)) {
+    } else if (FMT != kIQ4_NL && FMT != kQ8_0 && kwide_takes_kpm(nblk, outer, GATEUP)) {
         if constexpr (FMT != kIQ4_NL && FMT != kQ8_0) {
             const int grid = std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV));
             const int npass = (nblk + 15) / 16;
@@ -1609,7 +1615,7 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
         // except where the persistent multi-pass kernel would run (its IQ4_NL
         // dot from LDS digits measured slower than the streamed kernel:
         // 5120 x 5120 10.9 us against 10.3)
-        return inner % 256 == 0 && !kwide_takes_kpm(inner / 256, outer, 2)
+        return inner % 256 == 0 && !kwide_takes_kpm(inner / 256, outer, false)
                    ? launch_kwide<kIQ4_NL, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi)
                    : launch_sdig<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     default: return hipErrorInvalidValue;

@@ -82,7 +82,9 @@ FFN_CASES = [
     (512, 768, synth.Q8_0, synth.Q8_0),      # unfused gate/up: norm kernel first
     (4096, 1536, synth.Q4_K, synth.Q6_K),    # one GPU's share of the decode FFN over 8 GPUs
     (2048, 5120, synth.Q5_K, synth.Q5_K),    # residual in a persistent two-pass down
-    (12288, 512, synth.Q4_K, synth.Q4_K),    # norm folded into a persistent four-pass gate/up
+    (12288, 512, synth.Q4_K, synth.Q4_K),    # norm folded into a serial four-pass gate/up
+    (5120, 2560, synth.Q5_K, synth.Q5_K),    # norm folded into a persistent two-pass gate/up
+    (12288, 2304, synth.Q4_K, synth.Q4_K),   # norm folded into a persistent four-pass gate/up
     (1024, 2048, synth.IQ4_NL, synth.IQ4_NL),  # SwiGLU and residual epilogues of the IQ4_NL wide kernel
 ]
 

@@ -271,9 +271,11 @@ def test_gemv_every_launch(t, outer, inner):
 
 @pytest.mark.parametrize("hidden,inter", [
     (4096, 1030),   # wide kernel, one gate and one up row per wave
-    (8448, 515),    # persistent multi-pass kernel: three passes, the last partial
-    (14336, 300),   # persistent multi-pass kernel: four passes
-    (5120, 600),    # persistent multi-pass kernel, 2-pass capacity
+    (8448, 515),    # three passes, the last partial (one row pair per wave: serial)
+    (14336, 300),   # four passes, serial
+    (5120, 600),    # two passes, serial
+    (5120, 2056),   # persistent multi-pass kernel, 2-pass capacity
+    (8448, 2100),   # persistent multi-pass kernel, 4-pass capacity, the last pass partial
     (5120, 2048),   # 256 workgroups over 256 CUs: serial passes
     (20480, 64),    # 80 blocks: past the persistent kernel, serial passes
     (4096, 8195),   # persistent kernel
