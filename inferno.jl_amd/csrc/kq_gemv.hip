@@ -29,6 +29,7 @@
 //     each workgroup writes one (value, index) partial to its own slot and a
 //     one-workgroup kernel reduces the partials, so no two workgroups touch
 //     the same address.
+#include <atomic>
 #include "inferno_hip.h"
 
 #include <algorithm>
@@ -1429,11 +1430,20 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
 // ------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------
+// CUs of the current device, queried once per device (launch plans ask on
+// every launch)
 static int device_cus()
 {
-    int dev = 0, ncu = 256;
-    if (hipGetDevice(&dev) == hipSuccess)
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    int ncu = cached[dev].load(std::memory_order_relaxed);
+    if (ncu <= 0) {
+        ncu = 256;
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        cached[dev].store(ncu, std::memory_order_relaxed);
+    }
     return ncu;
 }
 
