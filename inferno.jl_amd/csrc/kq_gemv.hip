@@ -213,13 +213,18 @@ constexpr uint32_t kIQ4G1 = 0x766A5D4Fu; // 79, 93, 106, 118
 constexpr uint32_t kIQ4G2 = 0xA6998D81u; // 129, 141, 153, 166
 constexpr uint32_t kIQ4G3 = 0xF1D9C5B5u; // 181, 197, 217, 241
 
-__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t nib) // four nibbles in bytes
+// Both nibbles of four packed index bytes q: lo gets grid + 128 of the low
+// nibbles, hi of the high nibbles.  The byte choice between the grid's two
+// halves comes straight from bit 3 (low) or bit 7 (high) of each byte.
+__device__ __forceinline__ void iq4nl_lookup2(uint32_t q, uint32_t &lo, uint32_t &hi)
 {
-    const uint32_t n7 = nib & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(kIQ4G1, kIQ4G0, n7); // bytes 0-3 of G0, 4-7 of G1
-    const uint32_t hi = __builtin_amdgcn_perm(kIQ4G3, kIQ4G2, n7);
-    const uint32_t pick = 0x03020100u + ((nib & 0x08080808u) >> 1); // byte i of lo or of hi
-    return __builtin_amdgcn_perm(hi, lo, pick);
+    const uint32_t nl = q & 0x07070707u, nh = (q >> 4) & 0x07070707u;
+    const uint32_t pl = ((q >> 1) & 0x04040404u) | 0x03020100u; // byte i of the low or high half
+    const uint32_t ph = ((q >> 5) & 0x04040404u) | 0x03020100u;
+    lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(kIQ4G3, kIQ4G2, nl), // grid[8..15]
+                               __builtin_amdgcn_perm(kIQ4G1, kIQ4G0, nl), pl); // grid[0..7]
+    hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(kIQ4G3, kIQ4G2, nh),
+                               __builtin_amdgcn_perm(kIQ4G1, kIQ4G0, nh), ph);
 }
 
 __device__ __forceinline__ uint32_t sel_u32(int c, uint32_t a, uint32_t b) { return c ? a : b; }
@@ -255,10 +260,9 @@ __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
         for (int t = 0; t < 4; ++t) {
             const uint32_t qa = __builtin_amdgcn_alignbyte(D[t + 1], D[t], 2);
             const uint32_t qc = D[5 + t];
-            const uint32_t la = iq4nl_lookup(qa & 0x0f0f0f0fu);        // elements 4t + b of A
-            const uint32_t ha = iq4nl_lookup((qa >> 4) & 0x0f0f0f0fu); // 16 + 4t + b of A
-            const uint32_t lc = iq4nl_lookup(qc & 0x0f0f0f0fu);
-            const uint32_t hc = iq4nl_lookup((qc >> 4) & 0x0f0f0f0fu);
+            uint32_t la, ha, lc, hc; // elements 4t + b and 16 + 4t + b of A, of C
+            iq4nl_lookup2(qa, la, ha);
+            iq4nl_lookup2(qc, lc, hc);
             a0 = __builtin_amdgcn_udot4(la, X.p[0][t], a0, false);
             a0 = __builtin_amdgcn_udot4(ha, X.p[0][4 + t], a0, false);
             a1 = __builtin_amdgcn_udot4(la, X.p[1][t], a1, false);
@@ -1188,8 +1192,8 @@ __device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t 
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const uint32_t q = __builtin_amdgcn_alignbyte(w[t + 1], w[t], sh); // qs[4t..4t+3]
-        const uint32_t ul = iq4nl_lookup(q & 0x0f0f0f0fu);          // grid + 128, elements 4t + b
-        const uint32_t uh = iq4nl_lookup((q >> 4) & 0x0f0f0f0fu);   // elements 16 + 4t + b
+        uint32_t ul, uh; // grid + 128, elements 4t + b and 16 + 4t + b
+        iq4nl_lookup2(q, ul, uh);
         a0 = __builtin_amdgcn_udot4(ul, X.p[0][t], a0, false);
         a1 = __builtin_amdgcn_udot4(ul, X.p[1][t], a1, false);
         a2 = __builtin_amdgcn_sdot4((int)(ul ^ 0x80808080u), (int)X.p[2][t], a2, false);
