@@ -701,8 +701,9 @@ def _host_info():
 
 
 def cpu_baseline(synth, oracle):
-    """BASELINE plan: the reference C int8 path at the reference's default
-    thread count and on all cores, the fp32 fallback single-threaded; weights
+    """The reference's CPU path timed three ways: the C int8 path at the
+    reference's default thread count and on all cores, and the fp32 fallback
+    single-threaded; weights
     rotated through more than twice the L3; median and spread of 7 runs."""
     import ctypes
     outer = inner = 4096
