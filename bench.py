@@ -433,7 +433,7 @@ def prefill(torch, stream, synth, D):
     dw = D.DeviceWeight(torch.from_numpy(w).cuda(), synth.Q4_K, inner, outer)
     Xd = torch.from_numpy(X).cuda()
     Y = torch.empty(T, outer, device="cuda")
-    xh = torch.empty(T * inner, dtype=torch.float16, device="cuda")
+    xh = D.prefill_scratch(T, inner)
     us, us_graph, us_stream = both_ways_us(torch, stream, lambda i: D.prefill_q4_k(dw, Xd, Y, xh),
                                            10, 5, 4)
     flops = 2.0 * T * outer * inner
@@ -570,7 +570,7 @@ def pmc_workload(torch, synth, D):
     dw = D.DeviceWeight(torch.from_numpy(w).cuda(), synth.Q4_K, 4096, 4096)
     X = torch.randn(512, 4096, device="cuda")
     Y = torch.empty(512, 4096, device="cuda")
-    xh = torch.empty(512 * 4096, dtype=torch.float16, device="cuda")
+    xh = D.prefill_scratch(512, 4096)
     for _ in range(10):
         D.prefill_q4_k(dw, X, Y, xh)
     torch.cuda.synchronize()

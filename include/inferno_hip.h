@@ -191,8 +191,12 @@ int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *
 int ihip_ffn_block(int gate_type, const uint8_t *wg, int up_type, const uint8_t *wu,
                    int down_type, const uint8_t *wd, const float *norm_w, float eps, float *x,
                    int hidden, int inter);
-/* Batched prefill: Y[t,:] = W X[t,:] for t < T (W: outer x inner Q4_K);
- * the activations are rounded to fp16 for the matrix cores. */
+/* Batched prefill: Y[t,:] = W X[t,:] for t < T (W: outer x inner Q4_K), for
+ * any finite fp32 X.  The activations are rounded to fp16 for the matrix
+ * cores, each token row first scaled by a power of two that puts its largest
+ * magnitude in [2^14, 2^15) (undone exactly on the outputs), so no finite
+ * value overflows and small ones keep fp16's 11 significant bits down to
+ * 2^-29 of their row's maximum. */
 int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inner,
                       int outer);
 
@@ -217,10 +221,11 @@ int ihip_ffn_swiglu_dev(int gate_type, const void *wg, int up_type, const void *
 #define IHIP_ARGMAX_WS_BYTES 262144
 /* GEMV + fused greedy argmax.  *token and *flags are device int32s (flags:
  * IHIP_FLAG_* bits; the token is meaningless when NAN or POSINF is set).
- * logits may be NULL when the argmax is fused into the GEMV
- * (ihip_lm_head_fused: Q6_K or Q8_0, 16-byte aligned w and x, hidden a
- * multiple of 2048 or 256); otherwise the GEMV writes logits and a second
- * kernel reduces them, and NULL logits is IHIP_ERR_INVALID. */
+ * logits may be NULL when the argmax is fused into the GEMV, which
+ * ihip_lm_head_fused reports: a Q6_K or Q8_0 weight, 16-byte aligned w and x,
+ * and hidden a whole number of blocks of at most 32768 columns.  Otherwise
+ * the GEMV writes logits and a second kernel reduces them, and NULL logits is
+ * IHIP_ERR_INVALID. */
 int ihip_lm_head_argmax_dev(int ggml_type, const void *w, const float *x, float *logits,
                             int32_t *token, uint32_t *flags, int hidden, int vocab,
                             void *workspace, ihip_stream stream);
@@ -249,9 +254,12 @@ int ihip_fused_mlp_gate_mul_dev(float *gate, const float *up, int64_t n, ihip_st
 int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, int64_t n,
                                  ihip_stream stream);
 /* X: T x inner fp32 (row-major), Y: T x outer fp32.  `xh` is caller scratch
- * of T*inner fp16 values (2 bytes each) for the rounded activations. */
+ * of ihip_prefill_scratch_bytes(T, inner) bytes: the rounded activations
+ * (T*inner fp16 values) and one scale exponent per token.  w, X, xh and Y are
+ * 16-byte aligned. */
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
+size_t ihip_prefill_scratch_bytes(int T, int inner);
 
 /* rmsnorm_cpu! (src/ModelCPU.jl:111-123): out = x * (1/sqrt(mean(x^2) + eps))
  * .* w over n values (out may alias x). */
@@ -260,9 +268,10 @@ int ihip_rmsnorm_dev(const float *x, const float *w, float eps, float *out, int 
 /* ihip_ffn_block on device pointers: the norm is folded into the fused gate/up
  * pass (its scale multiplies the row sums) and the residual add into the down
  * projection's epilogue.  h: caller scratch of ihip_ffn_block_scratch_floats()
- * floats -- inter for a matching Q4_K or Q5_K gate/up pair (which must then be
- * 16-byte aligned, as must x and norm_w), inter + hidden for any other pair
- * (the normed input goes to h + inter). */
+ * floats, inter + hidden for every pair: h receives silu(g) .* u, and a pair
+ * that does not run as one fused pass (not a matching Q4_K or Q5_K pair, or
+ * wg, wu, x or norm_w off 16-byte alignment) puts the normed input in
+ * h + inter. */
 int ihip_ffn_block_dev(int gate_type, const void *wg, int up_type, const void *wu, int down_type,
                        const void *wd, const float *norm_w, float eps, float *x, float *h,
                        int hidden, int inter, ihip_stream stream);

@@ -646,11 +646,14 @@ int ihip_shutdown(void)
     return IHIP_OK;
 }
 
-size_t ihip_ffn_block_scratch_floats(int gate_type, int up_type, int hidden, int inter)
+// inter + hidden for every pair: a Q4_K/Q5_K pair whose pointers rule the
+// fused pass out (alignment) takes the unfused path, which needs room for the
+// normed input after h.
+size_t ihip_ffn_block_scratch_floats(int, int, int hidden, int inter)
 {
     if (hidden <= 0 || inter <= 0)
         return 0;
-    return gate_up_fusable(gate_type, up_type) ? (size_t)inter : (size_t)inter + (size_t)hidden;
+    return (size_t)inter + (size_t)hidden;
 }
 
 int ihip_lm_head_fused(int ggml_type, const void *w, const float *x, int hidden, int vocab)
@@ -889,8 +892,10 @@ int ihip_lm_head_argmax(int ggml_type, const uint8_t *w, const float *x, float *
     const void *dw;
     RET_IF(resolve_locked(w, ggml_type, hidden, vocab, &dw));
     RET_IF(copy_in(c.x, x, sizeof(float) * (size_t)hidden));
+    // logits on the device: wanted by the caller, or needed because the
+    // argmax runs as a second kernel over them (not fused into the GEMV)
     float *dlog = nullptr;
-    if (logits) {
+    if (logits || !lm_head_fused(ggml_type, dw, (const float *)c.x.p, hidden, vocab)) {
         RET_IF(ensure(c.y, sizeof(float) * (size_t)vocab));
         dlog = (float *)c.y.p;
     }
@@ -931,7 +936,7 @@ int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inn
     const void *dw;
     RET_IF(resolve_locked(w, kQ4_K, inner, outer, &dw));
     RET_IF(copy_in(c.x, X, sizeof(float) * (size_t)T * inner));
-    RET_IF(ensure(c.h, 2 * (size_t)T * inner));
+    RET_IF(ensure(c.h, prefill_scratch_bytes(T, inner)));
     RET_IF(ensure(c.y, sizeof(float) * (size_t)T * outer));
     hipError_t e = launch_prefill_q4k(dw, (const float *)c.x.p, c.h.p, (float *)c.y.p, T, inner,
                                       outer, c.stream);
@@ -1075,6 +1080,13 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
     return IHIP_OK;
 }
 
+size_t ihip_prefill_scratch_bytes(int T, int inner)
+{
+    if (T <= 0 || inner <= 0)
+        return 0;
+    return prefill_scratch_bytes(T, inner);
+}
+
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T, int inner,
                           int outer, ihip_stream stream)
 {
@@ -1188,13 +1200,9 @@ int ihip_ffn_block_dev(int gate_type, const void *wg, int up_type, const void *w
     RET_IF(check_shape(down_type, inter, hidden));
     if (!wd || !norm_w || !x || !h)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    float *xn = nullptr;
-    if (!gate_up_fused(gate_type, wg, up_type, wu, x, hidden, norm_w)) {
-        if (gate_up_fusable(gate_type, up_type)) // h was sized for the fused pass
-            return fail(IHIP_ERR_INVALID, "a Q4_K/Q5_K gate/up pair takes 16-byte aligned wg, wu, "
-                                          "x and norm_w");
-        xn = h + inter; // h holds inter + hidden floats for other pairs
-    }
+    // h holds inter + hidden floats (ihip_ffn_block_scratch_floats): the
+    // unfused pass puts the normed input after h
+    float *xn = gate_up_fused(gate_type, wg, up_type, wu, x, hidden, norm_w) ? nullptr : h + inter;
     RET_IF(gate_up_dev_locked(gate_type, wg, up_type, wu, x, h, hidden, inter, (hipStream_t)stream,
                               norm_w, eps, xn));
     return gemv_dev_locked(down_type, wd, h, x, inter, hidden, (hipStream_t)stream, x);

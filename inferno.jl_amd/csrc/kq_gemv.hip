@@ -78,10 +78,12 @@ __device__ __forceinline__ void x_load_pass(const float *__restrict__ x, int col
 // instruction) when x is written as an integer.  Each 32-element sub-block of
 // x is scaled by 2^(22-e), e the binary exponent of the sub-block's largest
 // |x| (|x| < 2^e), and truncated to an integer X with |X| < 2^22: the error of
-// x ~ X * 2^(e-22) is below 2^(e-22) <= |x|max * 2^-21, so a dot product of n
-// such values is off by less than sqrt(n) * 2^-21 * ||w||_2 ||x||_2 (3.1e-5
-// relative at n = 4096, against the 1e-4 row bound, whatever the data; about
-// 1e-7 for random data).  X is split into three byte digits,
+// x ~ X * 2^(e-22) is below 2^(e-22) <= |x|max * 2^-21.  The sub-block's
+// |x|max is at most its own 2-norm, so the error vector of 32 values has a
+// norm below sqrt(32) * 2^-21 times theirs, and over any number of sub-blocks
+// ||x - X 2^(e-22)||_2 < sqrt(32) * 2^-21 * ||x||_2: a dot product is off by
+// less than 2.7e-6 * ||w||_2 ||x||_2 whatever its length and data (the row
+// bound is 1e-4; about 1e-7 for random data).  X is split into three byte digits,
 // X = 65536 * b2 + 256 * b1 + b0 (b0, b1 unsigned, b2 signed); the products
 // q * b are exact integers, so the per-sub-block sums are exact and
 // independent of summation order.  A sub-block holding a non-finite value has
@@ -1105,17 +1107,15 @@ __device__ __forceinline__ void lds_read8_at(const uint8_t *p, uint32_t sh, uint
     b = __builtin_amdgcn_alignbyte(w2, w1, sh);
 }
 
-// The lane's share of one Q6_K block of the ring slot starting at `slot`
-// (dword-aligned).
-__device__ __forceinline__ float q6_dot_dig(const uint8_t *slot, const Q6DigLane &L,
-                                            const SXD &X)
+// The lane's share of one Q6_K block from its bytes, two dwords each:
+// A = ql[64n + l0, +8), B = ql[64n + 32 + l0, +8), H = qh[32n + l0, +8),
+// S = sc[8n, 8n + 8); dbits = the block's fp16 d; c = l0 >> 4 (which of the
+// scale pairs the lane's positions use).
+__device__ __forceinline__ float q6_dot_words(const uint32_t (&A)[2], const uint32_t (&B)[2],
+                                              const uint32_t (&H)[2], const uint32_t (&S)[2],
+                                              uint32_t dbits, int c, const SXD &X)
 {
-    uint32_t A[2], B[2], H[2], S[2];
-    lds_read8_at(slot + L.a, L.sh, A[0], A[1]);
-    lds_read8_at(slot + L.a + 32, L.sh, B[0], B[1]);
-    lds_read8_at(slot + L.h, L.sh, H[0], H[1]);
-    lds_read8_at(slot + L.s, L.sh, S[0], S[1]);
-    const float d = h2f(*reinterpret_cast<const uint16_t *>(slot + L.d));
+    const float d = h2f(dbits);
     int acc[3][4];
 #pragma unroll
     for (int p = 0; p < 3; ++p)
@@ -1137,7 +1137,6 @@ __device__ __forceinline__ float q6_dot_dig(const uint8_t *slot, const Q6DigLane
         }
     }
     // scale-weighted sums per plane: |acc| <= 8 * 63 * 255, |sc| <= 128 (24-bit products)
-    const int c = L.c;
     int T[3] = {0, 0, 0};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -1150,17 +1149,25 @@ __device__ __forceinline__ float q6_dot_dig(const uint8_t *slot, const Q6DigLane
     return d * __builtin_ldexpf(v + X.poison, X.e - 22);
 }
 
-// Q8_0 block at byte `off` of an LDS row.
-__device__ __forceinline__ float q80_dot_dig(const uint8_t *row_lds, uint32_t off, const SXD &X)
+// The lane's share of one Q6_K block of the ring slot starting at `slot`
+// (dword-aligned).
+__device__ __forceinline__ float q6_dot_dig(const uint8_t *slot, const Q6DigLane &L,
+                                            const SXD &X)
 {
-    const float d = h2f(lds_read_u16(row_lds, off));
-    const uint32_t o = off + 2;
-    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
-    const uint32_t sh = o & 3u;
-    constexpr int NDW = sdig_blk_dwords(kQ8_0);
-    uint32_t w[NDW];
-#pragma unroll
-    for (int i = 0; i < NDW; ++i) w[i] = p[i];
+    uint32_t A[2], B[2], H[2], S[2];
+    lds_read8_at(slot + L.a, L.sh, A[0], A[1]);
+    lds_read8_at(slot + L.a + 32, L.sh, B[0], B[1]);
+    lds_read8_at(slot + L.h, L.sh, H[0], H[1]);
+    lds_read8_at(slot + L.s, L.sh, S[0], S[1]);
+    return q6_dot_words(A, B, H, S, *reinterpret_cast<const uint16_t *>(slot + L.d), L.c, X);
+}
+
+// A Q8_0 block from its bytes: w = the 9 dwords from the one at or below its
+// first quant, sh = that quant's byte within it, dbits = its fp16 d.
+__device__ __forceinline__ float q80_dot_words(const uint32_t (&w)[9], uint32_t sh, uint32_t dbits,
+                                               const SXD &X)
+{
+    const float d = h2f(dbits);
     uint32_t a0 = (uint32_t)X.init[0][0], a1 = (uint32_t)X.init[1][0];
     int a2 = 0;
 #pragma unroll
@@ -1175,18 +1182,24 @@ __device__ __forceinline__ float q80_dot_dig(const uint8_t *row_lds, uint32_t of
     return d * __builtin_ldexpf(v + X.poison, X.e - 22);
 }
 
-// IQ4_NL block at byte `off` of an LDS row (element j = low nibble of qs[j],
-// element j + 16 = high nibble).
-__device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t off, const SXD &X)
+// Q8_0 block at byte `off` of an LDS row.
+__device__ __forceinline__ float q80_dot_dig(const uint8_t *row_lds, uint32_t off, const SXD &X)
 {
-    const float d = h2f(lds_read_u16(row_lds, off));
     const uint32_t o = off + 2;
     const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
-    const uint32_t sh = o & 3u;
-    constexpr int NDW = sdig_blk_dwords(kIQ4_NL);
-    uint32_t w[NDW];
+    uint32_t w[9];
 #pragma unroll
-    for (int i = 0; i < NDW; ++i) w[i] = p[i];
+    for (int i = 0; i < 9; ++i) w[i] = p[i];
+    return q80_dot_words(w, o & 3u, lds_read_u16(row_lds, off), X);
+}
+
+// An IQ4_NL block from its bytes (element j = low nibble of qs[j], element
+// j + 16 = high nibble): w = the 5 dwords from the one at or below its first
+// quant, sh = that quant's byte within it, dbits = its fp16 d.
+__device__ __forceinline__ float iq4nl_dot_words(const uint32_t (&w)[5], uint32_t sh, uint32_t dbits,
+                                                 const SXD &X)
+{
+    const float d = h2f(dbits);
     uint32_t a0 = (uint32_t)X.init[0][0], a1 = (uint32_t)X.init[1][0];
     int a2 = 0;
 #pragma unroll
@@ -1203,6 +1216,17 @@ __device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t 
     }
     const float v = fmaf(fmaf((float)a2, 256.0f, (float)(int)a1), 256.0f, (float)(int)a0);
     return d * __builtin_ldexpf(v + X.poison, X.e - 22);
+}
+
+// IQ4_NL block at byte `off` of an LDS row.
+__device__ __forceinline__ float iq4nl_dot_dig(const uint8_t *row_lds, uint32_t off, const SXD &X)
+{
+    const uint32_t o = off + 2;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row_lds + (o & ~3u));
+    uint32_t w[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) w[i] = p[i];
+    return iq4nl_dot_words(w, o & 3u, lds_read_u16(row_lds, off), X);
 }
 
 // Staged digits of one segment in LDS: per lane 24 digit-plane dwords, 12

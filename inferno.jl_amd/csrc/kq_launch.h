@@ -49,6 +49,16 @@ inline bool prefill_fits(int T, int inner, int outer)
     return 2 * (int64_t)T * inner <= (int64_t)UINT32_MAX &&
            (int64_t)outer * (inner / 256) * 144 <= (int64_t)UINT32_MAX;
 }
+// The caller's scratch xh: the fp16 activations (T x inner), then one int
+// per token (its power-of-two scale) from the next 16-byte boundary.
+inline size_t prefill_scale_offset(int T, int inner)
+{
+    return ((size_t)2 * (size_t)T * (size_t)inner + 15) & ~(size_t)15;
+}
+inline size_t prefill_scratch_bytes(int T, int inner)
+{
+    return prefill_scale_offset(T, inner) + (size_t)4 * (size_t)T;
+}
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s);
 

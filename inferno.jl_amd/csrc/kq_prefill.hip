@@ -5,7 +5,8 @@
 // runs T independent GEMVs, so the semantics are the Q4_K GEMV applied row
 // by row.  On MI355X the T tokens share every weight byte, which makes this
 // a dense contraction: X is rounded once to fp16 (the matrix-core operand
-// type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not) and
+// type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not), each
+// token row on its own power-of-two scale (k_x_to_f16), and
 // v_mfma_f32_32x32x16_f16 accumulates in fp32.
 //
 // Tile: 64 tokens x 128 weight rows per workgroup of 8 waves (256
@@ -31,22 +32,94 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_BM = 64, PF_BN = 128; // workgroup tile: tokens x weight rows
 
-// fp32 -> fp16 activations, 8 per thread (two 16-byte loads, one 16-byte store).
+// One token row of X to fp16 (one workgroup per row, 8 values per thread and
+// step: two 16-byte loads, one 16-byte store).  The reference multiplies fp32
+// activations of any finite size (src/ModelCPU.jl:285-307), while fp16 holds
+// magnitudes up to 65504 only and rounds those below 2^-14 to its subnormal
+// steps.  So every row is scaled by a power of two 2^s, chosen so that its
+// largest magnitude lands in [2^14, 2^15), before the rounding, and s goes to
+// xs[t]; the GEMM's epilogue multiplies the row's outputs by 2^-s, which is
+// exact.  Every value keeps fp16's 11 significant bits down to 2^-29 of the
+// row's maximum.  A row holding NaN or an infinity is converted unscaled
+// (s = 0), so the non-finite value reaches its outputs.  Rows of at most
+// 8192 values stay in registers between the maximum and the conversion;
+// longer rows are read twice.
+constexpr int PF_CVT_REG = 4; // 8-value steps a thread holds: 256 x 8 x 4 = 8192 values
 __global__ __launch_bounds__(256) void k_x_to_f16(const float *__restrict__ X,
-                                                  _Float16 *__restrict__ Xh, int64_t n)
+                                                  _Float16 *__restrict__ Xh, int *__restrict__ xs,
+                                                  int K)
 {
-    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-    if (i + 7 < n) {
-        const float4 v0 = *reinterpret_cast<const float4 *>(X + i);
-        const float4 v1 = *reinterpret_cast<const float4 *>(X + i + 4);
-        half8 h;
-        h[0] = (_Float16)v0.x; h[1] = (_Float16)v0.y; h[2] = (_Float16)v0.z; h[3] = (_Float16)v0.w;
-        h[4] = (_Float16)v1.x; h[5] = (_Float16)v1.y; h[6] = (_Float16)v1.z; h[7] = (_Float16)v1.w;
-        *reinterpret_cast<half8 *>(Xh + i) = h;
+    __shared__ uint32_t wmax[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *row = X + (size_t)t * K;
+    _Float16 *hrow = Xh + (size_t)t * K;
+    // |x| bits of eight values: NaN > +Inf > every finite value
+    auto absmax8 = [](float4 a, float4 b) {
+        const uint32_t m0 = max(__float_as_uint(a.x) & 0x7fffffffu, __float_as_uint(a.y) & 0x7fffffffu);
+        const uint32_t m1 = max(__float_as_uint(a.z) & 0x7fffffffu, __float_as_uint(a.w) & 0x7fffffffu);
+        const uint32_t m2 = max(__float_as_uint(b.x) & 0x7fffffffu, __float_as_uint(b.y) & 0x7fffffffu);
+        const uint32_t m3 = max(__float_as_uint(b.z) & 0x7fffffffu, __float_as_uint(b.w) & 0x7fffffffu);
+        return max(max(m0, m1), max(m2, m3));
+    };
+    const bool in_regs = K <= 256 * 8 * PF_CVT_REG; // workgroup-uniform
+    float4 v[PF_CVT_REG][2];
+    uint32_t m = 0;
+    if (in_regs) {
+#pragma unroll
+        for (int k = 0; k < PF_CVT_REG; ++k) {
+            const int i = 8 * (tid + 256 * k);
+            v[k][0] = v[k][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < K) { // K is a multiple of 256: whole 8-value steps
+                v[k][0] = *reinterpret_cast<const float4 *>(row + i);
+                v[k][1] = *reinterpret_cast<const float4 *>(row + i + 4);
+            }
+            m = max(m, absmax8(v[k][0], v[k][1]));
+        }
     } else {
-        for (int64_t j = i; j < n; ++j)
-            Xh[j] = (_Float16)X[j];
+        for (int i = 8 * tid; i < K; i += 8 * 256)
+            m = max(m, absmax8(*reinterpret_cast<const float4 *>(row + i),
+                               *reinterpret_cast<const float4 *>(row + i + 4)));
     }
+    // the row's maximum: DPP steps within each row of 16 lanes, then the
+    // four rows' and the four waves' values through LDS
+    m = dpp_max_u32<0xb1, 0xf>(m);
+    m = dpp_max_u32<0x4e, 0xf>(m);
+    m = dpp_max_u32<0x141, 0xf>(m);
+    m = dpp_max_u32<0x140, 0xf>(m);
+    {
+        const int lane = tid & 63, w = tid >> 6;
+        const uint32_t r0 = __builtin_amdgcn_readlane(m, 0), r1 = __builtin_amdgcn_readlane(m, 16);
+        const uint32_t r2 = __builtin_amdgcn_readlane(m, 32), r3 = __builtin_amdgcn_readlane(m, 48);
+        if (lane == 0)
+            wmax[w] = max(max(r0, r1), max(r2, r3));
+    }
+    __syncthreads();
+    m = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+    const bool finite = m < 0x7f800000u;
+    // m = 0 (an all-zero row): frexp's exponent is 0, any scale keeps the zeros
+    const int s = finite ? 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(m)) : 0;
+    auto cvt8 = [s](float4 a, float4 b) {
+        half8 h;
+        h[0] = (_Float16)__builtin_ldexpf(a.x, s); h[1] = (_Float16)__builtin_ldexpf(a.y, s);
+        h[2] = (_Float16)__builtin_ldexpf(a.z, s); h[3] = (_Float16)__builtin_ldexpf(a.w, s);
+        h[4] = (_Float16)__builtin_ldexpf(b.x, s); h[5] = (_Float16)__builtin_ldexpf(b.y, s);
+        h[6] = (_Float16)__builtin_ldexpf(b.z, s); h[7] = (_Float16)__builtin_ldexpf(b.w, s);
+        return h;
+    };
+    if (in_regs) {
+#pragma unroll
+        for (int k = 0; k < PF_CVT_REG; ++k) {
+            const int i = 8 * (tid + 256 * k);
+            if (i < K)
+                *reinterpret_cast<half8 *>(hrow + i) = cvt8(v[k][0], v[k][1]);
+        }
+    } else {
+        for (int i = 8 * tid; i < K; i += 8 * 256)
+            *reinterpret_cast<half8 *>(hrow + i) = cvt8(*reinterpret_cast<const float4 *>(row + i),
+                                                        *reinterpret_cast<const float4 *>(row + i + 4));
+    }
+    if (tid == 0)
+        xs[t] = s;
 }
 
 // One ring slot holds block column kb of both operands:
@@ -242,6 +315,7 @@ __device__ __forceinline__ void pf_wait_copies(int n)
 // its row half from the four waves' partial sums.
 __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__restrict__ W,
                                                             const _Float16 *__restrict__ Xh,
+                                                            const int *__restrict__ xs,
                                                             float *__restrict__ Y, int T, int K,
                                                             int N, int mtiles, int ntiles)
 {
@@ -373,6 +447,11 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
         const int m = m0 + 32 * t + li;
         if (m >= T)
             break;
+        const int sm = -xs[m]; // undo the row's power-of-two scale (exact)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            v[q] = make_float4(__builtin_ldexpf(v[q].x, sm), __builtin_ldexpf(v[q].y, sm),
+                               __builtin_ldexpf(v[q].z, sm), __builtin_ldexpf(v[q].w, sm));
         const int nb = n0 + 64 * rh + 32 * u + 4 * h; // + 8 q: 4 consecutive rows
         float *yrow = Y + (size_t)m * N;
         if ((N & 3) == 0) {
@@ -396,15 +475,14 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s)
 {
-    if (T <= 0 || !prefill_fits(T, inner, outer))
+    if (T <= 0 || inner % 256 || !prefill_fits(T, inner, outer))
         return hipErrorInvalidValue;
-    const int64_t n = (int64_t)T * inner;
-    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n / 8 + 255) / 256 + 1)), dim3(256), 0, s, X,
-                       (_Float16 *)xh, n);
+    int *xs = reinterpret_cast<int *>(static_cast<uint8_t *>(xh) + prefill_scale_offset(T, inner));
+    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)T), dim3(256), 0, s, X, (_Float16 *)xh, xs, inner);
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
     const int per_xcd = (mtiles * ntiles + 7) / 8;
     hipLaunchKernelGGL(k_prefill_q4k, dim3(per_xcd * 8), dim3(PF_THREADS), 0, s, (const uint8_t *)w,
-                       (const _Float16 *)xh, Y, T, inner, outer, mtiles, ntiles);
+                       (const _Float16 *)xh, (const int *)xs, Y, T, inner, outer, mtiles, ntiles);
     return hipGetLastError();
 }
 

@@ -143,13 +143,19 @@ def argmax(logits: torch.Tensor, ws: ArgmaxWorkspace, stream=None):
                                 _stream(stream)))
 
 
+def prefill_scratch(T: int, inner: int, device="cuda") -> torch.Tensor:
+    """Caller scratch of ihip_prefill_q4_k_dev: the fp16 activations and one
+    scale exponent per token (ihip_prefill_scratch_bytes bytes)."""
+    return torch.empty(lib().ihip_prefill_scratch_bytes(T, inner), dtype=torch.uint8, device=device)
+
+
 def prefill_q4_k(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, xh: torch.Tensor = None,
                  stream=None):
     if w.ggml_type != Q4_K:
         raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, "prefill takes a Q4_K weight")
     T = X.shape[0]
     if xh is None:
-        xh = torch.empty(T * w.inner, dtype=torch.float16, device=X.device)
+        xh = prefill_scratch(T, w.inner, X.device)
     if Y is None:
         Y = torch.empty(T, w.outer, dtype=torch.float32, device=X.device)
     check(lib().ihip_prefill_q4_k_dev(_ptr(w.data), _ptr(X, torch.float32, "X"), _ptr(xh), _ptr(Y, torch.float32, "Y"),

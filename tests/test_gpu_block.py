@@ -122,35 +122,42 @@ def test_ffn_block_with_norm_and_residual(hidden, inter, gt, dt):
     wg, wu, wd, x, nw = case
     say(f"ffn block hidden={hidden} inter={inter} gate/up={gt} down={dt}")
     xd = dev(x)
-    # caller scratch: inter floats for a fused Q4_K/Q5_K pair, inter + hidden otherwise
+    # caller scratch: inter + hidden floats for every pair
     from inferno_hip import _lib
     nh = _lib.lib().ihip_ffn_block_scratch_floats(gt, gt, hidden, inter)
-    assert nh == (inter if gt in (synth.Q4_K, synth.Q5_K) else inter + hidden)
+    assert nh == inter + hidden
     h = torch.full((nh,), float("nan"), device="cuda")
     D.ffn_block(dweight(wg, gt, hidden, inter), dweight(wu, gt, hidden, inter),
                 dweight(wd, dt, inter, hidden), dev(nw), eps, xd, h=h)
     _check_block(xd.cpu().numpy(), h[:inter].cpu().numpy(), x, case, gt, dt, hidden, inter, eps)
-    if nh > inter:  # the unfused pair's normed input went to h + inter
+    if gt not in (synth.Q4_K, synth.Q5_K):  # the unfused pair's normed input went to h + inter
         n = oracle.rmsnorm_f64(x, nw, eps)
         check_within(h[inter:].cpu().numpy(), n, 4 * np.spacing(np.abs(n).astype(np.float32)) + 1e-30,
                      "normed x in h + inter")
 
 
-def test_ffn_block_misaligned_fused_pair_is_refused():
-    """A Q4_K pair is sized for the fused pass (h of inter floats); pointers
-    that rule the fused pass out are an error, never a write past h."""
+def test_ffn_block_misaligned_fused_pair_takes_the_unfused_path():
+    """A Q4_K pair whose gate weight is off 16-byte alignment cannot run as
+    one fused pass: it runs unfused (norm kernel, gate GEMV, up GEMV with the
+    SwiGLU epilogue) inside the inter + hidden floats of scratch the header
+    asks for, and matches the oracle; nothing is written past h."""
     from inferno_hip import _lib
-    hidden, inter = 1024, 2816
+    hidden, inter, eps = 1024, 2816, 1e-6
     case = _block_case(hidden, inter, synth.Q4_K, synth.Q4_K, 0xB10E)
     wg, wu, wd, x, nw = case
     say("ffn block: misaligned Q4_K pair")
     wgd = dev(np.concatenate([np.zeros(4, np.uint8), wg]))[4:]   # 4 bytes past 16-byte alignment
-    xd, h = dev(x), torch.empty(inter, device="cuda")
-    rc = _lib.lib().ihip_ffn_block_dev(synth.Q4_K, wgd.data_ptr(), synth.Q4_K, dev(wu).data_ptr(),
-                                       synth.Q4_K, dev(wd).data_ptr(), dev(nw).data_ptr(), 1e-6,
-                                       xd.data_ptr(), h.data_ptr(), hidden, inter,
-                                       torch.cuda.current_stream().cuda_stream)
-    assert rc == _lib.IHIP_ERR_INVALID
+    nh = _lib.lib().ihip_ffn_block_scratch_floats(synth.Q4_K, synth.Q4_K, hidden, inter)
+    xd, wud, wdd, nwd = dev(x), dev(wu), dev(wd), dev(nw)  # held until the queued kernels have run
+    h = torch.full((nh + 64,), 7.0, device="cuda")  # 64 guard floats after the scratch
+    _lib.check(_lib.lib().ihip_ffn_block_dev(synth.Q4_K, wgd.data_ptr(), synth.Q4_K, wud.data_ptr(),
+                                             synth.Q4_K, wdd.data_ptr(), nwd.data_ptr(), eps,
+                                             xd.data_ptr(), h.data_ptr(), hidden, inter,
+                                             torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    _check_block(xd.cpu().numpy(), h[:inter].cpu().numpy(), x, case, synth.Q4_K, synth.Q4_K, hidden,
+                 inter, eps)
+    assert torch.all(h[nh:] == 7.0).item(), "write past the scratch"
 
 
 def test_ffn_block_host_entry_point():

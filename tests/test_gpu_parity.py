@@ -322,22 +322,30 @@ def test_gemv_activation_dynamic_range(t):
     assert_within(ys, refs, tols, f"type {t} small sub-blocks only")
 
 
-def test_gemv_nonfinite_activations():
-    """A NaN or an infinity in x makes every output non-finite (the fp32 sum
-    of the reference gives +-Inf or NaN per row; the integer-digit path gives
-    NaN for all of them)."""
+@pytest.mark.parametrize("t,outer,inner", [
+    (synth.Q4_K, 64, 4096), (synth.Q5_K, 64, 4096), (synth.Q8_0, 64, 4096), (synth.IQ4_NL, 64, 4096),
+    (synth.Q6_K, 64, 2048),      # one-segment rows: each row ends inside its wave
+    (synth.Q6_K, 64, 4096),      # two segments meet in LDS
+    (synth.Q6_K, 4096, 12288),   # the FFN down shape: six segments
+    (synth.Q6_K, 40, 2560),      # 10-block rows (at byte phases): a short second segment
+])
+def test_gemv_nonfinite_activations(t, outer, inner):
+    """A NaN or an infinity in x makes every output non-finite
+    (src/ModelCPU.jl:333-355: the reference's fp32 sum gives +-Inf or NaN per
+    row; the integer-digit path gives NaN for all of them), wherever in x it
+    sits: the first and last column, and a column of every segment."""
     from inferno_hip import device as D
-    rng = synth.rng_for(4343)
-    outer, inner = 64, 4096
-    for t in (synth.Q4_K, synth.Q5_K, synth.Q8_0, synth.IQ4_NL):
-        w = synth.weight(rng, t, outer, inner)
-        dw = dweight(w, t, inner, outer)
+    rng = synth.rng_for(4343 + t + inner)
+    w = synth.weight(rng, t, outer, inner)
+    dw = dweight(w, t, inner, outer)
+    cols = sorted({0, inner - 1, *range(1234 % inner, inner, 2048)})
+    for c in cols:
         for bad in (np.nan, np.inf, -np.inf):
             x = synth.activations(rng, inner)
-            x[1234] = bad
-            say(f"nonfinite type={t} x[1234]={bad}")
+            x[c] = bad
+            say(f"nonfinite type={t} {outer}x{inner} x[{c}]={bad}")
             y = D.gemv(dw, dev(x)).cpu().numpy()
-            assert not np.any(np.isfinite(y)), (t, bad)
+            assert not np.any(np.isfinite(y)), (t, c, bad)
 
 
 def test_gemv_special_inputs():
@@ -408,7 +416,7 @@ def test_ffn_block(hidden, inter, gt, dt):
     (synth.Q4_K, synth.Q5_K, 1024, 1030),           # mixed pair: wide kernel, SwiGLU epilogue
     (synth.Q4_K, synth.Q5_K, 4096, 8200),           # mixed pair: persistent kernel (>= 8192 rows)
     (synth.Q8_0, synth.Q8_0, 18432, 300),           # 9 segments: 16-wave streamed kernel
-    (synth.Q6_K, synth.Q6_K, 768, 301),             # 3-block rows: byte-granular kernel
+    (synth.Q6_K, synth.Q6_K, 768, 301),             # 3-block rows: streamed kernel at byte phases
 ])
 def test_gate_up_unfused_pairs(gt, ut, hidden, inter):
     """Pairs that are not a matching Q4_K/Q5_K pair: the gate GEMV writes g into
@@ -436,6 +444,26 @@ def test_gate_up_misaligned_pair_takes_the_epilogue_path():
     say("gate/up Q4_K pair 4 bytes past alignment")
     wgd = dev(np.concatenate([np.zeros(4, np.uint8), wg]))[4:]
     h = D.gate_up_swiglu(D.DeviceWeight(wgd, t, hidden, inter), dweight(wu, t, hidden, inter),
+                         dev(x)).cpu().numpy()
+    g = oracle.gemv_f64(t, wg, x, hidden, inter)
+    u = oracle.gemv_f64(t, wu, x, hidden, inter)
+    hb = _h_bound(g, u, oracle.row_norms(t, wg, hidden, inter), oracle.row_norms(t, wu, hidden, inter), x)
+    assert_within(h, g / (1 + np.exp(-g)) * u, hb, "h = silu(g)*u")
+
+
+@pytest.mark.parametrize("t,hidden,inter", [(synth.Q6_K, 2048, 301), (synth.Q8_0, 1024, 515)])
+def test_gate_up_misaligned_up_weight_takes_the_byte_granular_epilogue(t, hidden, inter):
+    """An up weight off 16-byte alignment runs on the byte-granular kernel, so
+    its SwiGLU epilogue (silu(g) * u against the gate row already in h) is the
+    one that kernel carries."""
+    from inferno_hip import device as D
+    rng = synth.rng_for(0x6A80 + t)
+    wg = synth.weight(rng, t, inter, hidden)
+    wu = synth.weight(rng, t, inter, hidden)
+    x = synth.activations(rng, hidden)
+    say(f"gate/up type={t} {hidden}->{inter}: up weight 2 bytes past alignment")
+    wud = dev(np.concatenate([np.zeros(2, np.uint8), wu]))[2:]
+    h = D.gate_up_swiglu(dweight(wg, t, hidden, inter), D.DeviceWeight(wud, t, hidden, inter),
                          dev(x)).cpu().numpy()
     g = oracle.gemv_f64(t, wg, x, hidden, inter)
     u = oracle.gemv_f64(t, wu, x, hidden, inter)
@@ -588,6 +616,31 @@ def test_lm_head_host_entry_point_and_nonfinite():
     assert rc == _lib.IHIP_ERR_NONFINITE
 
 
+@pytest.mark.parametrize("t,vocab,hidden", [
+    (synth.Q4_K, 5003, 1024),    # the argmax runs as a second kernel over the logits
+    (synth.Q8_0, 777, 34816),    # 17 segments: unfused Q8_0
+    (synth.Q6_K, 3001, 2048),    # fused
+])
+def test_lm_head_host_entry_point_null_logits(t, vocab, hidden):
+    """ihip_lm_head_argmax with logits NULL: the token is still the oracle's,
+    whether or not the argmax is fused into the GEMV (the unfused path puts
+    the logits in library staging)."""
+    from inferno_hip import _lib
+    import ctypes as C
+    rng = synth.rng_for(0x4E55 + t)
+    w = synth.weight(rng, t, vocab, hidden)
+    x = synth.activations(rng, hidden)
+    tok = C.c_int32(-1)
+    say(f"ihip_lm_head_argmax host, type {t} {vocab}x{hidden}, NULL logits")
+    _lib.check(_lib.lib().ihip_lm_head_argmax(t, w.ctypes.data, x.ctypes.data, None, C.byref(tok),
+                                              hidden, vocab))
+    ref = oracle.gemv_f64(t, w, x, hidden, vocab)
+    order = np.argsort(ref)
+    tol = oracle.tolerance(oracle.row_norms(t, w, hidden, vocab), x)
+    assert ref[order[-1]] - ref[order[-2]] > 2 * tol.max(), "seed gives an ambiguous maximum"
+    assert tok.value == int(order[-1])
+
+
 ARGMAX_CASES = {
     # tests/unit/test_common_ops.jl:85-93 and :61-62 (0-based here)
     "all -inf": (np.array([-np.inf, -np.inf], np.float32), 0),
@@ -626,6 +679,29 @@ def test_argmax_errors_and_large_ties():
 
 # ------------------------------------------------------------- prefill ----
 
+def prefill_operands(X):
+    """The activations the matrix cores take: each token row scaled by 2^s,
+    s = 15 - (the binary exponent of its largest magnitude), rounded to fp16
+    and scaled back (exact); rows holding NaN or an infinity unscaled."""
+    X = np.asarray(X, np.float32)
+    m = np.max(np.abs(X), axis=1)
+    e = np.frexp(np.where(np.isfinite(m), m, 1.0))[1]
+    s = np.where(np.isfinite(m), 15 - e, 0).astype(np.int64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        h = np.ldexp(X.astype(np.float64), s[:, None]).astype(np.float32).astype(np.float16)
+    return np.ldexp(h.astype(np.float64), -s[:, None]).astype(np.float32)
+
+
+def test_prefill_operand_rounding_matches_plain_fp16_in_range():
+    """For rows whose values sit in fp16's normal range the per-row scale is a
+    power of two, so the operands equal plain fp16 rounding (a check of the
+    restatement above, on the CPU data the prefill tests use)."""
+    rng = synth.rng_for(0xC5)
+    X = rng.standard_normal((64, 512)).astype(np.float32)
+    X[np.abs(X) < 1e-3] = 1e-3  # keep every value a normal fp16 number
+    assert np.array_equal(prefill_operands(X), X.astype(np.float16).astype(np.float32))
+
+
 @pytest.mark.parametrize("T,outer,inner", [
     (512, 4096, 4096),   # the batched prefill workload
     (70, 300, 2048),     # ragged tiles
@@ -645,7 +721,7 @@ def test_prefill_q4k(T, outer, inner):
     X = rng.standard_normal((T, inner)).astype(np.float32)
     from inferno_hip import device as D
     Y = D.prefill_q4_k(dweight(w, synth.Q4_K, inner, outer), dev(X)).cpu().numpy()
-    Xh = X.astype(np.float16).astype(np.float32)  # the matrix-core operand rounding
+    Xh = prefill_operands(X)  # the matrix-core operand rounding
     nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
     xn = np.linalg.norm(X.astype(np.float64), axis=1)
     xhn = np.linalg.norm(Xh.astype(np.float64), axis=1)
@@ -658,6 +734,60 @@ def test_prefill_q4k(T, outer, inner):
     ratio32 = np.abs(Y.astype(np.float64) - ref32) / (1e-4 * nrm[None, :] * xn[:, None])
     assert np.all(ratio32 <= 1.0), f"fp32-x oracle: max err/tol {float(np.max(ratio32)):.3g}"
     say(f"prefill max err/tol = {worst:.3e}")
+
+
+@pytest.mark.parametrize("scale", [1e5, 1e-6, 1e30, 1e-38])
+def test_prefill_any_finite_activations(scale):
+    """Token rows scaled to 1e5 (past fp16's 65504) and to 1e-6 (below its
+    normal range), beside unscaled rows; rows of 1e30 and of fp32 subnormals;
+    an all-zero row: every output against the fp32-x oracle (the reference
+    multiplies fp32 activations of any size, src/ModelCPU.jl:285-307)."""
+    from inferno_hip import device as D
+    T, outer, inner = 48, 320, 2048
+    rng = synth.rng_for(0xC6)
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    X = rng.standard_normal((T, inner)).astype(np.float64)
+    X[::3] *= scale                                  # every third row scaled
+    X[1::7] *= float(np.clip(1.0 / scale, 1e-30, 1e30))  # and some the other way
+    X[5] = 0.0
+    X = X.astype(np.float32)
+    say(f"prefill rows scaled by {scale:g}")
+    Y = D.prefill_q4_k(dweight(w, synth.Q4_K, inner, outer), dev(X)).cpu().numpy()
+    assert np.all(np.isfinite(Y))
+    nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+    xn = np.linalg.norm(X.astype(np.float64), axis=1)
+    ref = oracle.gemm_f64(synth.Q4_K, w, X, inner, outer)
+    tol = 1e-4 * nrm[None, :] * xn[:, None] + 1e-45
+    ratio = np.abs(Y.astype(np.float64) - ref) / tol
+    assert np.all(ratio <= 1.0), f"max err/tol {float(np.max(ratio)):.3g} at {np.unravel_index(np.argmax(ratio), ratio.shape)}"
+    assert np.all(Y[5] == 0.0)
+    # the operands the matrix cores took: the restatement's rounding
+    refh = oracle.gemm_f64(synth.Q4_K, w, prefill_operands(X), inner, outer)
+    xhn = np.linalg.norm(prefill_operands(X).astype(np.float64), axis=1)
+    assert np.all(np.abs(Y.astype(np.float64) - refh) <= 1e-4 * nrm[None, :] * xhn[:, None] + 1e-45)
+
+
+def test_prefill_nonfinite_activations_reach_their_rows():
+    """A NaN or an infinity in a token row makes that row's outputs
+    non-finite, as the reference's fp32 sum does, and leaves the other rows
+    exact to the bound."""
+    from inferno_hip import device as D
+    T, outer, inner = 8, 128, 1024
+    rng = synth.rng_for(0xC7)
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    X = rng.standard_normal((T, inner)).astype(np.float32)
+    X[2, 17] = np.nan
+    X[4, 1000] = np.inf
+    X[6, 3] = -np.inf
+    say("prefill with NaN / +Inf / -Inf rows")
+    Y = D.prefill_q4_k(dweight(w, synth.Q4_K, inner, outer), dev(X)).cpu().numpy()
+    for r in (2, 4, 6):
+        assert not np.any(np.isfinite(Y[r])), r
+    good = [0, 1, 3, 5, 7]
+    nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+    ref = oracle.gemm_f64(synth.Q4_K, w, X[good], inner, outer)
+    xn = np.linalg.norm(X[good].astype(np.float64), axis=1)
+    assert np.all(np.abs(Y[good].astype(np.float64) - ref) <= 1e-4 * nrm[None, :] * xn[:, None])
 
 
 def test_device_calls_launch_on_the_current_stream():

@@ -79,8 +79,8 @@ def test_noalloc_lm_head_flags_nonfinite_logits():
     say("noalloc lm_head with a NaN in x")
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     fl = torch.zeros(1, dtype=torch.int32, device="cuda")
-    rc = L.ihip_lm_head_argmax_noalloc_dev(t, torch.from_numpy(w).cuda().data_ptr(),
-                                           torch.from_numpy(x).cuda().data_ptr(), None,
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()  # held until the kernels have run
+    rc = L.ihip_lm_head_argmax_noalloc_dev(t, wd.data_ptr(), xd.data_ptr(), None,
                                            tok.data_ptr(), fl.data_ptr(), hidden, vocab,
                                            torch.cuda.current_stream().cuda_stream)
     assert rc == 0
