@@ -871,6 +871,13 @@ def main():
         cpu = cpu_baseline(synth, oracle)
         log(f"  {cpu['cpu_model']}, nproc {cpu['nproc']}, L3 {cpu['l3_bytes'] >> 20} MiB")
 
+    roofline = {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes()}
+    if "floor_read_us" in g:
+        # the same weight bytes read fully coalesced by a launch of the same
+        # grid: the per-launch time this launch shape cannot beat
+        roofline["floor_us"] = round(g["floor_read_us"], 4)
+        roofline["frac_of_floor"] = round(g["floor_read_us"] / g["us_per_launch"], 4)
     line = {
         "metric": METRIC,
         "value": round(g["gbs"], 2),
@@ -892,8 +899,7 @@ def main():
                    "us_per_launch": round(g["us_per_launch"], 4),
                    "algorithmic_bytes_per_launch": g["bytes"],
                    "algorithmic_bytes_per_step": g["bytes"] * NCOPY},
-        "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(g["gbs"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes()},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "extras": extras,
     }
