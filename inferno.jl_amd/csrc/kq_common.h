@@ -236,9 +236,9 @@ struct KFmt<kIQ4_NL> {
     static constexpr int BYTES = 144, QS = 0;
 };
 
-// Q8_0 likewise: eight 34-byte blocks per 256 columns (272 bytes); lane j's
-// 68 bytes are blocks 2j and 2j + 1, starting j dwords into the five 16-byte
-// units at or below byte 68 j.
+// Q8_0: eight 34-byte blocks per 256 columns (272 bytes); lane j's 68 bytes
+// are blocks 2j and 2j + 1, from byte 68 j (a dword boundary), loaded exactly:
+// four 16-byte loads and one dword at dword alignment.
 template <>
 struct KFmt<kQ8_0> {
     static constexpr int BYTES = 272, QS = 0;
@@ -260,12 +260,17 @@ __device__ __forceinline__ void kbytes_load(const uint8_t *__restrict__ blk, int
         return;
     }
     if constexpr (FMT == kQ8_0) {
-        const uint8_t *u = blk + ((68 * j) & ~15);
-        B.h = *reinterpret_cast<const uint4 *>(u);
-        B.q0 = *reinterpret_cast<const uint4 *>(u + 16);
-        B.q1 = *reinterpret_cast<const uint4 *>(u + 32);
-        B.e0 = *reinterpret_cast<const uint4 *>(u + 48);
-        B.e1 = *reinterpret_cast<const uint4 *>(u + 64);
+        typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+        const uint8_t *u = blk + 68 * j;
+        auto ld16 = [](const uint8_t *p) {
+            const u32x4_a4 v = *reinterpret_cast<const u32x4_a4 *>(p);
+            return make_uint4(v.x, v.y, v.z, v.w);
+        };
+        B.h = ld16(u);
+        B.q0 = ld16(u + 16);
+        B.q1 = ld16(u + 32);
+        B.e0 = ld16(u + 48);
+        B.e1 = make_uint4(*reinterpret_cast<const uint32_t *>(u + 64), 0u, 0u, 0u);
         return;
     }
     B.h = *reinterpret_cast<const uint4 *>(blk);

@@ -292,14 +292,9 @@ __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
                     dC * (__builtin_ldexpf(vC, X.eb - 22) + X.sb * 0.0f));
     }
     if constexpr (FMT == kQ8_0) {
-        const uint32_t w[20] = {B.h.x,  B.h.y,  B.h.z,  B.h.w,  B.q0.x, B.q0.y, B.q0.z,
-                                B.q0.w, B.q1.x, B.q1.y, B.q1.z, B.q1.w, B.e0.x, B.e0.y,
-                                B.e0.z, B.e0.w, B.e1.x, B.e1.y, B.e1.z, B.e1.w};
-        uint32_t t1[19], D[17];
-#pragma unroll
-        for (int k = 0; k < 19; ++k) t1[k] = sel_u32(j & 1, w[k + 1], w[k]);
-#pragma unroll
-        for (int k = 0; k < 17; ++k) D[k] = sel_u32(j & 2, t1[k + 2], t1[k]);
+        // the lane's 17 dwords, loaded from its own first byte (kbytes_load)
+        const uint32_t D[17] = {B.h.x,  B.h.y,  B.h.z,  B.h.w,  B.q0.x, B.q0.y, B.q0.z, B.q0.w, B.q1.x,
+                                B.q1.y, B.q1.z, B.q1.w, B.e0.x, B.e0.y, B.e0.z, B.e0.w, B.e1.x};
         // block A: d in bytes 0-1, qs in 2-33; block B: d in 34-35, qs in 36-67.
         // Signed weights: q + 128 (q ^ 0x80) on the unsigned planes, the
         // bias taken off as 128 * (digit sums); q itself on the signed plane.
@@ -1639,13 +1634,13 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     case kQ5_K: return launch_kwide<kQ5_K, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi);
     case kQ6_K: return launch_sdig<kQ6_K, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     case kQ8_0:
-        // the wide lane layout where the persistent kernel runs or one row per
-        // wave fits the CUs at once (14336 x 4096 13.9 us against 14.9;
-        // 2048 x 4096 4.2 against 5.3, 1024 x 4096 3.5 against 4.7); at 4096
-        // rows and for several passes the streamed kernel is faster
-        // (4096 x 4096 6.2 against 6.6, 4096 x 14336 16.2 against 17.7)
-        return inner % 256 == 0 && inner <= 4096 &&
-                       (kwide_takes_kpers(inner / 256, outer) || kwide_one_row(outer))
+        // rows of one pass (at most 4096 columns in whole 256-column units)
+        // on the wide lane layout, measured against the streamed kernel in one
+        // process: 151936 x 2048 60-62 us against 67.5, 5120 x 3072 6.6 against
+        // 8.2, 8192 x 4096 8.9 against 9.4, 4096 x 2048 4.6 against 4.8,
+        // 4096 x 4096 6.1-6.2 against 6.1-6.3; rows of several passes stay on
+        // the streamed kernel (4096 x 14336 16.2 against 17.7)
+        return inner % 256 == 0 && inner <= 4096
                    ? launch_kwide<kQ8_0, false>(w, nullptr, x, y, inner, outer, s, nullptr, 0.0f, resid, epi)
                    : launch_sdig<kQ8_0, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     case kIQ4_NL:
