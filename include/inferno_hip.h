@@ -255,8 +255,10 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
                                  ihip_stream stream);
 /* X: T x inner fp32 (row-major), Y: T x outer fp32.  `xh` is caller scratch
  * of ihip_prefill_scratch_bytes(T, inner) bytes: the rounded activations
- * (T*inner fp16 values) and one scale exponent per token.  w, X, xh and Y are
- * 16-byte aligned. */
+ * (T*inner fp16 values), one scale exponent per token and room for the
+ * partial sums of a weight of few rows, whose K is split over several
+ * workgroups (the size does not depend on outer).  w, X, xh and Y are
+ * 16-byte aligned; calls that share xh must not overlap on the GPU. */
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
 size_t ihip_prefill_scratch_bytes(int T, int inner);

@@ -1455,7 +1455,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_sdig(const uint8_t *__restrict
 // ------------------------------------------------------------------------
 // CUs of the current device, queried once per device (launch plans ask on
 // every launch)
-static int device_cus()
+int device_cus()
 {
     static std::atomic<int> cached[64];
     int dev = 0;

@@ -41,6 +41,9 @@ hipError_t launch_mlp_gate_mul(float *gate, const float *up, int64_t n, hipStrea
 hipError_t launch_silu_gate_mul(float *out, const float *x, const float *gate, int64_t n,
                                 hipStream_t s);
 
+// CUs of the current device (queried once per device)
+int device_cus();
+
 // kq_prefill.hip
 // The prefill GEMM addresses its operands as 32-bit byte offsets from the
 // start of Xh (T x inner fp16) and W (outer Q4_K rows).
@@ -49,15 +52,84 @@ inline bool prefill_fits(int T, int inner, int outer)
     return 2 * (int64_t)T * inner <= (int64_t)UINT32_MAX &&
            (int64_t)outer * (inner / 256) * 144 <= (int64_t)UINT32_MAX;
 }
-// The caller's scratch xh: the fp16 activations (T x inner), then one int
-// per token (its power-of-two scale) from the next 16-byte boundary.
+// The caller's scratch xh: the fp16 activations (T x inner), one int per
+// token (its power-of-two scale) from the next 16-byte boundary, then, from
+// the next 16-byte boundary, the partial sums of a split over K.  A split
+// keeps nsplit x (64-token x 128-row tiles) <= kPrefillMaxTiles, so its
+// nsplit - 1 partial planes of T x outer floats hold at most
+// T x 128 x kPrefillMaxTiles / ceil(T / 64) floats whatever outer is.
+constexpr int kPrefillMaxTiles = 256;
+constexpr int kPrefillBM = 64, kPrefillBN = 128; // workgroup tile: tokens x weight rows
 inline size_t prefill_scale_offset(int T, int inner)
 {
     return ((size_t)2 * (size_t)T * (size_t)inner + 15) & ~(size_t)15;
 }
+inline size_t prefill_part_offset(int T, int inner)
+{
+    return (prefill_scale_offset(T, inner) + (size_t)4 * (size_t)T + 15) & ~(size_t)15;
+}
+inline size_t prefill_part_floats(int T)
+{
+    const size_t mtiles = ((size_t)T + kPrefillBM - 1) / kPrefillBM;
+    return (size_t)T * kPrefillBN * (size_t)kPrefillMaxTiles / mtiles;
+}
+// XCD-aware order: workgroup bid's place `lin` in tile order, so that the
+// consecutive workgroups of one XCD (bid mod 8) walk consecutive tiles (the M
+// tiles of one N band of one split) and share the band's weight bytes in
+// their L2.  The grid is prefill_grid workgroups; lin >= tiles x nsplit exits.
+__host__ __device__ inline int prefill_grid(int tiles, int nsplit)
+{
+    return (tiles * nsplit + 7) / 8 * 8;
+}
+__host__ __device__ inline int prefill_lin(int bid, int tiles, int nsplit)
+{
+    const int per_xcd = (tiles * nsplit + 7) / 8;
+    return (bid % 8) * per_xcd + bid / 8;
+}
+// Workgroup `lin` (in tile order) of a launch of mtiles x ntiles tiles and
+// nsplit splits over K: its split, its tile and the split's block columns
+// kb0 .. kb0 + nk - 1 of the nblk.
+struct PrefillSplit {
+    int sp, mt, nt, kb0, nk;
+};
+__host__ __device__ inline PrefillSplit prefill_split_of(int lin, int mtiles, int ntiles, int nblk,
+                                                        int nsplit)
+{
+    PrefillSplit s;
+    const int tiles = mtiles * ntiles;
+    s.sp = lin / tiles;
+    const int tl = lin - s.sp * tiles;
+    s.mt = tl % mtiles;
+    s.nt = tl / mtiles;
+    s.kb0 = s.sp * nblk / nsplit;
+    s.nk = (s.sp + 1) * nblk / nsplit - s.kb0;
+    return s;
+}
 inline size_t prefill_scratch_bytes(int T, int inner)
 {
-    return prefill_scale_offset(T, inner) + (size_t)4 * (size_t)T;
+    return prefill_part_offset(T, inner) + 4 * prefill_part_floats(T);
+}
+// Splits over K of one prefill launch on a device of ncu CUs (1: none).  A
+// weight of few rows leaves most CUs without a tile (512 x 512 x 4096 is 32
+// tiles for 256 CUs), so each tile's block columns are shared out over
+// nsplit workgroups, as many as keep nsplit x tiles within the CUs (and
+// within the partial planes the scratch holds) and at least two columns per
+// split, and a second launch adds the partial sums.  Rows of fewer than 8
+// block columns are not split: a workgroup's fixed cost (the launch, the
+// first copies, the partial-sum exchange and the 32 KB of stores) is then
+// most of its time, and the summing launch adds to it (measured on MI355X,
+// us per call: 512 x 512 x 4096 18.9-21.4 against 27.6 unsplit, 64 x 4096 x
+// 4096 18.9-19.3 against 23.9, 512 x 2048 x 4096 25.5-25.8 against 28.1;
+// 512 x 1024 x 1024 split four ways 18.2-19.0 against 13.0).
+inline int prefill_splits(int T, int inner, int outer, int ncu)
+{
+    const int mtiles = (T + kPrefillBM - 1) / kPrefillBM, ntiles = (outer + kPrefillBN - 1) / kPrefillBN;
+    const int tiles = mtiles * ntiles, nblk = inner / 256;
+    const int cap = ncu < kPrefillMaxTiles ? ncu : kPrefillMaxTiles;
+    if (tiles * 2 > cap || nblk < 8)
+        return 1;
+    const int s = cap / tiles < nblk / 2 ? cap / tiles : nblk / 2;
+    return s > 1 ? s : 1;
 }
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s);

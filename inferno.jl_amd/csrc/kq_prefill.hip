@@ -30,7 +30,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int PF_BM = 64, PF_BN = 128; // workgroup tile: tokens x weight rows
+constexpr int PF_BM = kPrefillBM, PF_BN = kPrefillBN; // workgroup tile: tokens x weight rows
 
 // One token row of X to fp16 (one workgroup per row, 8 values per thread and
 // step: two 16-byte loads, one 16-byte store).  The reference multiplies fp32
@@ -308,29 +308,28 @@ __device__ __forceinline__ void pf_wait_copies(int n)
     }
 }
 
-// Y[t, n] = sum_k W[n, k] Xh[t, k] for one 64-token x 128-row tile.  Wave
-// (rh, j) = (wave & 1, wave >> 1) accumulates weight rows 64 rh .. +63 over
-// sub-block pair j of every block column; at the end wave (rh, j) finishes
-// tile combination c = j (weight half u = c >> 1, token half t = c & 1) of
-// its row half from the four waves' partial sums.
+// Y[t, n] = sum_k W[n, k] Xh[t, k] for one 64-token x 128-row tile, over
+// the block columns of one split of K: split sp of nsplit takes columns
+// sp * nblk / nsplit .. (sp + 1) * nblk / nsplit - 1 and writes its sums to
+// Y (split 0) or to partial plane sp - 1 of `part` (T x N floats each), which
+// k_prefill_splits_sum then adds into Y.  Wave (rh, j) = (wave & 1, wave >> 1)
+// accumulates weight rows 64 rh .. +63 over sub-block pair j of every block
+// column; at the end wave (rh, j) finishes tile combination c = j (weight
+// half u = c >> 1, token half t = c & 1) of its row half from the four
+// waves' partial sums.
 __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__restrict__ W,
                                                             const _Float16 *__restrict__ Xh,
                                                             const int *__restrict__ xs,
-                                                            float *__restrict__ Y, int T, int K,
-                                                            int N, int mtiles, int ntiles)
+                                                            float *__restrict__ Y,
+                                                            float *__restrict__ part, int T, int K,
+                                                            int N, int mtiles, int ntiles, int nsplit)
 {
     __shared__ __attribute__((aligned(16))) uint8_t ring[PF_NSLOT * PF_SLOT];
 
-    // XCD-aware tile order: consecutive workgroups of one XCD walk the M
-    // tiles of one N band, so the band's weight bytes are shared in its L2.
-    const int bid = blockIdx.x;
-    const int nxcd = 8;
-    const int per_xcd = (mtiles * ntiles + nxcd - 1) / nxcd;
-    const int lin = (bid % nxcd) * per_xcd + bid / nxcd;
-    if (lin >= mtiles * ntiles)
+    const int tiles = mtiles * ntiles;
+    const int lin = prefill_lin((int)blockIdx.x, tiles, nsplit);
+    if (lin >= tiles * nsplit)
         return; // whole workgroup
-    const int mt = lin % mtiles, nt = lin / mtiles;
-    const int m0 = mt * PF_BM, n0 = nt * PF_BN;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -338,6 +337,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     const int h = lane >> 5, li = lane & 31;
     const int nblk = K / 256;
     const size_t row_bytes = (size_t)nblk * 144;
+    const PrefillSplit ps = prefill_split_of(lin, mtiles, ntiles, nblk, nsplit);
+    const int m0 = ps.mt * PF_BM, n0 = ps.nt * PF_BN;
+    const int kb0 = ps.kb0, nk = ps.nk; // this split's block columns (nk >= 1)
+    float *const out = ps.sp == 0 ? Y : part + (size_t)(ps.sp - 1) * (size_t)T * (size_t)N;
     const int brow = 64 * rh + li;                        // this lane's first weight row
     const int copies = 4 + (PF_B_COPIES - wave + 7) / 8; // copies this wave issues per column
 
@@ -358,7 +361,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     S.b0 = pf_src_b(n0, N, (uint32_t)row_bytes, lane, wave);
     S.b1 = pf_src_b(n0, N, (uint32_t)row_bytes, lane, wave + 8);
     S.b2 = pf_src_b(n0, N, (uint32_t)row_bytes, lane, wave + 16);
-    const uint8_t *Xb = reinterpret_cast<const uint8_t *>(Xh);
+    // the split's first block column: activations 512 bytes and weight rows
+    // 144 bytes per column further on
+    const uint8_t *Xb = reinterpret_cast<const uint8_t *>(Xh) + (size_t)kb0 * 512;
+    W += (size_t)kb0 * 144;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)ring;
 
     // Column kb lives in slot kb % 3.  A wave reads column kb + 1 into
@@ -366,7 +372,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     // reads of the next column overlap this column's matrix-core work; the
     // copies of column kb + 3 go into column kb's slot, which every wave has
     // read (into registers) before the barrier of iteration kb.
-    const int nfill = min(nblk, PF_NSLOT);
+    const int nfill = min(nk, PF_NSLOT);
     for (int c = 0; c < nfill; ++c)
         pf_issue(S, Xb, W, c, wave, ring_lds + c * PF_SLOT);
     pf_wait_copies((nfill - 1) * copies);
@@ -382,9 +388,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     // read was issued (the compiler would then wait for every LDS read in
     // flight, the successor's included, before the first matrix product).
     auto step = [&](int kb, int slot, PfOps &cur, PfOps &nxt) {
-        pf_wait_copies(kb + 2 < nblk ? copies : 0);
+        pf_wait_copies(kb + 2 < nk ? copies : 0);
         lds_barrier();
-        if (kb + 3 < nblk)
+        if (kb + 3 < nk)
             pf_issue(S, Xb, W, kb + 3, wave, ring_lds + slot * PF_SLOT);
         const int ns = slot == 2 ? 0 : slot + 1;
         pf_read(ring + ns * PF_SLOT, ba + ns * PF_SLOT, ba + ns * PF_SLOT + 32 * 144, j, h, li, nxt);
@@ -392,13 +398,13 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
         pf_mma(cur, j, acc);
     };
     int kb = 0, slot = 0;
-    for (; kb + 2 < nblk; kb += 2) {
+    for (; kb + 2 < nk; kb += 2) {
         step(kb, slot, o0, o1);
         slot = slot == 2 ? 0 : slot + 1;
         step(kb + 1, slot, o1, o0);
         slot = slot == 2 ? 0 : slot + 1;
     }
-    if (kb + 1 < nblk) {
+    if (kb + 1 < nk) {
         step(kb, slot, o0, o1);
         pf_mma(o1, j, acc);
     } else {
@@ -453,7 +459,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
             v[q] = make_float4(__builtin_ldexpf(v[q].x, sm), __builtin_ldexpf(v[q].y, sm),
                                __builtin_ldexpf(v[q].z, sm), __builtin_ldexpf(v[q].w, sm));
         const int nb = n0 + 64 * rh + 32 * u + 4 * h; // + 8 q: 4 consecutive rows
-        float *yrow = Y + (size_t)m * N;
+        float *yrow = out + (size_t)m * N;
         if ((N & 3) == 0) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -472,17 +478,64 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     }
 }
 
+// Y += P[0] + P[1] + ... + P[nparts - 1] (n floats each), in that order, so
+// the result does not depend on which split finished first.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_prefill_splits_sum(float *__restrict__ Y,
+                                                            const float *__restrict__ P, int64_t n,
+                                                            int nparts)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if constexpr (VEC) { // n % 4 == 0: every plane starts 16-byte aligned
+        float4 *Y4 = reinterpret_cast<float4 *>(Y);
+        const float4 *P4 = reinterpret_cast<const float4 *>(P);
+        const int64_t n4 = n >> 2;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+            float4 v = Y4[i];
+            for (int q = 0; q < nparts; ++q) {
+                const float4 p = P4[q * n4 + i];
+                v.x += p.x;
+                v.y += p.y;
+                v.z += p.z;
+                v.w += p.w;
+            }
+            Y4[i] = v;
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+            float v = Y[i];
+            for (int q = 0; q < nparts; ++q)
+                v += P[q * n + i];
+            Y[i] = v;
+        }
+    }
+}
+
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s)
 {
     if (T <= 0 || inner % 256 || !prefill_fits(T, inner, outer))
         return hipErrorInvalidValue;
     int *xs = reinterpret_cast<int *>(static_cast<uint8_t *>(xh) + prefill_scale_offset(T, inner));
+    float *P = reinterpret_cast<float *>(static_cast<uint8_t *>(xh) + prefill_part_offset(T, inner));
     hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)T), dim3(256), 0, s, X, (_Float16 *)xh, xs, inner);
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
-    const int per_xcd = (mtiles * ntiles + 7) / 8;
-    hipLaunchKernelGGL(k_prefill_q4k, dim3(per_xcd * 8), dim3(PF_THREADS), 0, s, (const uint8_t *)w,
-                       (const _Float16 *)xh, (const int *)xs, Y, T, inner, outer, mtiles, ntiles);
+    const int nsplit = prefill_splits(T, inner, outer, device_cus());
+    hipLaunchKernelGGL(k_prefill_q4k, dim3(prefill_grid(mtiles * ntiles, nsplit)), dim3(PF_THREADS), 0, s,
+                       (const uint8_t *)w,
+                       (const _Float16 *)xh, (const int *)xs, Y, P, T, inner, outer, mtiles, ntiles,
+                       nsplit);
+    if (nsplit > 1) {
+        const int64_t n = (int64_t)T * outer;
+        const int64_t units = (n & 3) == 0 ? n >> 2 : n;
+        const unsigned grid = (unsigned)std::min<int64_t>((units + 255) / 256, 2048);
+        if ((n & 3) == 0)
+            hipLaunchKernelGGL(k_prefill_splits_sum<true>, dim3(grid), dim3(256), 0, s, Y,
+                               (const float *)P, n, nsplit - 1);
+        else
+            hipLaunchKernelGGL(k_prefill_splits_sum<false>, dim3(grid), dim3(256), 0, s, Y,
+                               (const float *)P, n, nsplit - 1);
+    }
     return hipGetLastError();
 }
 

@@ -107,7 +107,7 @@ def build_floors(verbose: bool = False) -> Path:
 def build_checks(verbose: bool = False) -> Path:
     """Host-side checkers of the kernels' index arithmetic (tests/native): they
     include the headers the kernels form their indices with and run on the CPU."""
-    return _hipcc(CHECK_LIB, [CHECKS / "sdig_check.hip"], verbose)
+    return _hipcc(CHECK_LIB, [CHECKS / "sdig_check.hip", CHECKS / "prefill_check.hip"], verbose)
 
 
 if __name__ == "__main__":

@@ -144,8 +144,9 @@ def argmax(logits: torch.Tensor, ws: ArgmaxWorkspace, stream=None):
 
 
 def prefill_scratch(T: int, inner: int, device="cuda") -> torch.Tensor:
-    """Caller scratch of ihip_prefill_q4_k_dev: the fp16 activations and one
-    scale exponent per token (ihip_prefill_scratch_bytes bytes)."""
+    """Caller scratch of ihip_prefill_q4_k_dev: the fp16 activations, one
+    scale exponent per token and the partial sums of a split over K
+    (ihip_prefill_scratch_bytes bytes)."""
     return torch.empty(lib().ihip_prefill_scratch_bytes(T, inner), dtype=torch.uint8, device=device)
 
 

@@ -710,7 +710,10 @@ def test_prefill_operand_rounding_matches_plain_fp16_in_range():
     (5, 64, 512),        # 2 block columns: no loop iteration, last column peeled
     (40, 200, 768),      # 3 block columns: the odd tail
     (64, 256, 1024),     # 4 block columns: one loop iteration, even tail
-    (512, 512, 4096),    # one GPU's weight rows of the prefill over 8 GPUs
+    (512, 512, 4096),    # one GPU's weight rows of the prefill over 8 GPUs: split over K
+    (100, 384, 4096),    # eight splits of two block columns
+    (17, 1000, 2816),    # 11 block columns in five uneven splits
+    (7, 129, 2048),      # four splits, T x outer odd: the scalar sum of the splits
 ])
 def test_prefill_q4k(T, outer, inner):
     """Every token against the per-token GEMV oracle (src/ModelCPU.jl:1001-1017),
