@@ -770,19 +770,21 @@ def test_prefill_any_finite_activations(scale):
     assert np.all(np.abs(Y.astype(np.float64) - refh) <= 1e-4 * nrm[None, :] * xhn[:, None] + 1e-45)
 
 
-def test_prefill_nonfinite_activations_reach_their_rows():
+@pytest.mark.parametrize("inner", [1024, 2048])  # 2048: K split four ways, the splits summed
+def test_prefill_nonfinite_activations_reach_their_rows(inner):
     """A NaN or an infinity in a token row makes that row's outputs
     non-finite, as the reference's fp32 sum does, and leaves the other rows
     exact to the bound."""
     from inferno_hip import device as D
-    T, outer, inner = 8, 128, 1024
+    T, outer = 8, 128
     rng = synth.rng_for(0xC7)
     w = synth.weight(rng, synth.Q4_K, outer, inner)
     X = rng.standard_normal((T, inner)).astype(np.float32)
     X[2, 17] = np.nan
     X[4, 1000] = np.inf
     X[6, 3] = -np.inf
-    say("prefill with NaN / +Inf / -Inf rows")
+    X[6, inner - 1] = np.inf  # -Inf and +Inf in one row (in different splits at 2048)
+    say(f"prefill with NaN / +Inf / -Inf rows, inner {inner}")
     Y = D.prefill_q4_k(dweight(w, synth.Q4_K, inner, outer), dev(X)).cpu().numpy()
     for r in (2, 4, 6):
         assert not np.any(np.isfinite(Y[r])), r
