@@ -1,0 +1,132 @@
+"""Seeded random shapes through the launch plans, against the oracle.
+
+The parity tests in test_gpu_parity.py pick their shapes by hand: the
+benchmark configurations, the edges of each launch plan, ragged tiles.  Here
+a fixed seed draws row, column and token counts across the ranges the plans
+split on, so a plan boundary the hand-picked shapes miss still meets the
+oracle. The ranges cover:
+* one row per wave or two, one 4096-column pass or several;
+* persistent or not;
+* 1..16 streamed 2048-column segments;
+* prefill tiles with and without the split over K.
+The bars are those of test_gpu_parity.py:
+* the row tolerance 1e-4 * ||w_row|| * ||x|| for GEMV and GEMM outputs
+  (src/ModelCPU.jl:285-379, 1001-1017);
+* the exact token wherever the top two logits lie further apart than the
+  tolerance (src/CommonOps.jl:142-163).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+FMTS = (synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0, synth.IQ4_NL)
+BLOCK = {synth.Q4_K: 256, synth.Q5_K: 256, synth.Q6_K: 256, synth.Q8_0: 32, synth.IQ4_NL: 32}
+MAX_ELEMS = 40_000_000  # outer x inner per case: seconds for the fp64 oracle
+
+
+def _draw():
+    r = np.random.default_rng(20261202)
+    gemv = []
+    for t in FMTS:
+        be = BLOCK[t]
+        for i in range(8):
+            # columns: one pass, a few passes, up to 16 segments (32768)
+            cols = [int(r.integers(1, 4097)), int(r.integers(4097, 16385)), int(r.integers(16385, 32769))][i % 3]
+            inner = max(be, cols // be * be)
+            # rows: below, around and above one workgroup per CU
+            rows = [int(r.integers(1, 600)), int(r.integers(600, 5000)), int(r.integers(5000, 20000))][(i // 3) % 3]
+            outer = max(1, min(rows, MAX_ELEMS // inner))
+            gemv.append((t, outer, inner))
+    prefill = []
+    for i in range(8):
+        T = int(r.integers(1, 700))
+        outer = int(r.integers(1, 3000))
+        inner = 256 * int(r.integers(1, 25))
+        prefill.append((T, outer, inner))
+    lm = []
+    for i, t in enumerate((synth.Q6_K, synth.Q8_0, synth.Q6_K, synth.Q8_0)):
+        vocab = int(r.integers(1000, 40000))
+        hidden = BLOCK[t] * int(r.integers(1, 6144 // BLOCK[t] + 1))
+        lm.append((t, vocab, hidden, 0x7000 + i))
+    return gemv, prefill, lm
+
+
+GEMV, PREFILL, LM = _draw()
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from inferno_hip import _lib
+    assert _lib.available(), "libinferno_hip.so reports no usable gfx950 device"
+    yield
+    torch.cuda.synchronize()
+
+
+def _dw(w, t, inner, outer):
+    from inferno_hip.device import DeviceWeight
+    return DeviceWeight(torch.from_numpy(w).cuda(), t, inner, outer)
+
+
+@pytest.mark.parametrize("t,outer,inner", GEMV)
+def test_random_gemv(t, outer, inner):
+    from inferno_hip import device as D
+    say(f"gemv type {t} {outer}x{inner}")
+    rng = synth.rng_for(0x6000 + 7 * outer + inner + t)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner)
+    y = D.gemv(_dw(w, t, inner, outer), torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
+    err = np.abs(y.astype(np.float64) - ref)
+    assert np.all(np.isfinite(y)), "non-finite outputs"
+    assert np.all(err <= tol), f"{int(np.sum(err > tol))} rows over the bound, max err/tol {float(np.max(err / tol)):.3g}"
+
+
+@pytest.mark.parametrize("T,outer,inner", PREFILL)
+def test_random_prefill(T, outer, inner):
+    from inferno_hip import device as D
+    say(f"prefill T={T} {outer}x{inner}")
+    rng = synth.rng_for(0x6100 + T + outer + inner)
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    X = rng.standard_normal((T, inner)).astype(np.float32)
+    Y = D.prefill_q4_k(_dw(w, synth.Q4_K, inner, outer), torch.from_numpy(X).cuda()).cpu().numpy()
+    ref = oracle.gemm_f64(synth.Q4_K, w, X, inner, outer)
+    nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+    xn = np.linalg.norm(X.astype(np.float64), axis=1)
+    ratio = np.abs(Y.astype(np.float64) - ref) / (1e-4 * nrm[None, :] * xn[:, None])
+    assert np.all(ratio <= 1.0), f"max err/tol {float(np.max(ratio)):.3g} at {np.unravel_index(np.argmax(ratio), ratio.shape)}"
+
+
+@pytest.mark.parametrize("t,vocab,hidden,seed", LM)
+def test_random_lm_head(t, vocab, hidden, seed):
+    from inferno_hip import device as D
+    say(f"lm_head type {t} vocab {vocab} hidden {hidden}")
+    rng = synth.rng_for(seed)
+    w = synth.weight(rng, t, vocab, hidden)
+    x = synth.activations(rng, hidden)
+    ws = D.ArgmaxWorkspace()
+    logits = torch.empty(vocab, device="cuda")
+    D.lm_head_argmax(_dw(w, t, hidden, vocab), torch.from_numpy(x).cuda(), ws, logits=logits)
+    tok = ws.result()
+    ref = oracle.gemv_f64(t, w, x, hidden, vocab)
+    tol = oracle.tolerance(oracle.row_norms(t, w, hidden, vocab), x)
+    err = np.abs(logits.cpu().numpy().astype(np.float64) - ref)
+    assert np.all(err <= tol)
+    best = int(np.argmax(ref))
+    gap = ref[best] - np.max(np.delete(ref, best))
+    if gap > 2 * tol.max():
+        assert tok == best
+    else:  # an ambiguous maximum: the token must be one of the near-maximal rows
+        assert ref[tok] >= ref[best] - 2 * tol.max()
