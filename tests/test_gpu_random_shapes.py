@@ -8,7 +8,8 @@ oracle. The ranges cover:
 * one row per wave or two, one 4096-column pass or several;
 * persistent or not;
 * 1..16 streamed 2048-column segments;
-* prefill tiles with and without the split over K.
+* prefill tiles with and without the split over K;
+* fused gate/up pairs of every hidden size class, then the down GEMV.
 The bars are those of test_gpu_parity.py:
 * the row tolerance 1e-4 * ||w_row|| * ||x|| for GEMV and GEMM outputs
   (src/ModelCPU.jl:285-379, 1001-1017);
@@ -54,10 +55,19 @@ def _draw():
         vocab = int(r.integers(1000, 40000))
         hidden = BLOCK[t] * int(r.integers(1, 6144 // BLOCK[t] + 1))
         lm.append((t, vocab, hidden, 0x7000 + i))
-    return gemv, prefill, lm
+    # FFN: matching Q4_K / Q5_K gate/up pairs (one fused pass, on the wide,
+    # persistent or multi-pass kernels by shape) and a Q6_K / Q4_K down
+    ffn = []
+    for i in range(6):
+        gt = (synth.Q4_K, synth.Q5_K)[i % 2]
+        dt = (synth.Q6_K, synth.Q4_K)[(i // 2) % 2]
+        hidden = 256 * int(r.integers(1, 33))
+        inter = 256 * int(r.integers(1, 57))
+        ffn.append((gt, dt, hidden, inter))
+    return gemv, prefill, lm, ffn
 
 
-GEMV, PREFILL, LM = _draw()
+GEMV, PREFILL, LM, FFN = _draw()
 
 
 def say(*a):
@@ -130,3 +140,32 @@ def test_random_lm_head(t, vocab, hidden, seed):
         assert tok == best
     else:  # an ambiguous maximum: the token must be one of the near-maximal rows
         assert ref[tok] >= ref[best] - 2 * tol.max()
+
+
+@pytest.mark.parametrize("gt,dt,hidden,inter", FFN)
+def test_random_ffn(gt, dt, hidden, inter):
+    """h = silu(Wg x) .* (Wu x) within the first-order bound of the gate and
+    up rows' tolerances through SiLU; y = Wd h within the row bound on h_ref
+    plus ||w_row|| * ||h - h_ref|| (src/ModelCPU.jl:482-508)."""
+    from inferno_hip import device as D
+    say(f"ffn gate/up {gt} down {dt} hidden {hidden} inter {inter}")
+    rng = synth.rng_for(0x6200 + hidden + inter + gt + dt)
+    wg = synth.weight(rng, gt, inter, hidden)
+    wu = synth.weight(rng, gt, inter, hidden)
+    wd = synth.weight(rng, dt, hidden, inter)
+    x = synth.activations(rng, hidden)
+    h = torch.empty(inter, device="cuda")
+    y = D.ffn_swiglu(_dw(wg, gt, hidden, inter), _dw(wu, gt, hidden, inter), _dw(wd, dt, inter, hidden),
+                     torch.from_numpy(x).cuda(), h=h).cpu().numpy()
+    h = h.cpu().numpy().astype(np.float64)
+    g, u, h_ref, y_ref = oracle.ffn_swiglu_f64(gt, wg, gt, wu, dt, wd, x, hidden, inter)
+    tg = oracle.tolerance(oracle.row_norms(gt, wg, hidden, inter), x)
+    tu = oracle.tolerance(oracle.row_norms(gt, wu, hidden, inter), x)
+    with np.errstate(over="ignore"):  # exp(-g) -> inf for very negative g: sigmoid 0
+        sg = 1 / (1 + np.exp(-g))
+    hb = np.abs(sg * (1 + g * (1 - sg)) * u) * tg + np.abs(g * sg) * tu + 1e-6 * np.abs(g * sg * u) + 1e-30
+    assert np.all(np.abs(h - h_ref) <= hb), f"h: max err/bound {float(np.max(np.abs(h - h_ref) / hb)):.3g}"
+    nd = oracle.row_norms(dt, wd, inter, hidden)
+    yb = 1e-4 * nd * np.linalg.norm(h_ref) + nd * np.linalg.norm(h - h_ref)
+    err = np.abs(y.astype(np.float64) - y_ref)
+    assert np.all(err <= yb), f"y: max err/bound {float(np.max(err / yb)):.3g}"
