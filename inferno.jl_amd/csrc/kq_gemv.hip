@@ -865,6 +865,32 @@ __device__ __forceinline__ void argmax_fold(float v, uint32_t i, unsigned long l
     key = k > key ? k : key;
 }
 
+// argmax_fold for a value every lane of the wave holds (a row sum after the
+// wave reduction), taken through readfirstlane: the same tests made on the
+// value's bits, so the compiler keeps the fold, and key and flags, on the
+// scalar unit instead of spending ~20 vector instructions per row on it.
+__device__ __forceinline__ void argmax_fold_uniform(float v, uint32_t i, unsigned long long &key,
+                                                    uint32_t &flags)
+{
+    uint32_t b = __builtin_amdgcn_readfirstlane(__float_as_uint(v));
+    const uint32_t a = b & 0x7fffffffu;
+    if (a > 0x7f800000u) { // NaN
+        flags |= 1u;
+        return;
+    }
+    if (b == 0x7f800000u) { // +Inf
+        flags |= 2u;
+        return;
+    }
+    if (b != 0xff800000u) // not -Inf
+        flags |= 4u;
+    if (a == 0u)
+        b = 0u; // -0 == +0, as ordered_bits
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    const unsigned long long k = ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - i);
+    key = k > key ? k : key;
+}
+
 __device__ __forceinline__ void argmax_wave_reduce(unsigned long long &key, uint32_t &flags)
 {
 #pragma unroll
@@ -1350,8 +1376,8 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
                 rv0 = resid[c0.row0 + tid];
         }
     }
-    unsigned long long key = 0;
-    uint32_t fl = 0;
+    unsigned long long key = 0, ukey = 0; // ukey / ufl: rows a wave holds whole (wave-uniform)
+    uint32_t fl = 0, ufl = 0;
     int k = 0;
     for (int ci = 0; ci < g.my_chunks; ++ci) {
         const SdigChunk c = sdig_chunk(g, ci, bid, grid, rpc, outer);
@@ -1380,7 +1406,7 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
                 if (y && lane == 0)
                     y[row] = v;
                 if constexpr (ARGMAX)
-                    argmax_fold(v, (uint32_t)row, key, fl); // every lane folds the same row
+                    argmax_fold_uniform(v, (uint32_t)row, ukey, ufl);
             } else if (lane == 0) {
                 part[sdig_chunk_row(g, rr)][sg] = v;
             }
@@ -1411,6 +1437,8 @@ __device__ __forceinline__ void sdig_run(const uint8_t *__restrict__ W, const fl
         lds_barrier(); // part[] is free for the next chunk
     }
     if constexpr (ARGMAX) {
+        key = ukey > key ? ukey : key;
+        fl |= ufl;
         argmax_wave_reduce(key, fl);
         if (lane == 0) {
             wkey[w] = key;
