@@ -522,9 +522,8 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
     const int nsplit = prefill_splits(T, inner, outer, device_cus());
     hipLaunchKernelGGL(k_prefill_q4k, dim3(prefill_grid(mtiles * ntiles, nsplit)), dim3(PF_THREADS), 0, s,
-                       (const uint8_t *)w,
-                       (const _Float16 *)xh, (const int *)xs, Y, P, T, inner, outer, mtiles, ntiles,
-                       nsplit);
+                       (const uint8_t *)w, (const _Float16 *)xh, (const int *)xs, Y, P, T, inner, outer,
+                       mtiles, ntiles, nsplit);
     if (nsplit > 1) {
         const int64_t n = (int64_t)T * outer;
         const int64_t units = (n & 3) == 0 ? n >> 2 : n;
