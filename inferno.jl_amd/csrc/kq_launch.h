@@ -74,9 +74,9 @@ inline size_t prefill_part_floats(int T)
     return (size_t)T * kPrefillBN * (size_t)kPrefillMaxTiles / mtiles;
 }
 // XCD-aware order: workgroup bid's place `lin` in tile order, so that the
-// consecutive workgroups of one XCD (bid mod 8) walk consecutive tiles (the M
-// tiles of one N band of one split) and share the band's weight bytes in
-// their L2.  The grid is prefill_grid workgroups; lin >= tiles x nsplit exits.
+// consecutive workgroups of one XCD (bid mod 8) take consecutive places and
+// share the operand bytes of those tiles in their L2 (tile order below).
+// The grid is prefill_grid workgroups; lin >= tiles x nsplit exits.
 __host__ __device__ inline int prefill_grid(int tiles, int nsplit)
 {
     return (tiles * nsplit + 7) / 8 * 8;
@@ -88,7 +88,17 @@ __host__ __device__ inline int prefill_lin(int bid, int tiles, int nsplit)
 }
 // Workgroup `lin` (in tile order) of a launch of mtiles x ntiles tiles and
 // nsplit splits over K: its split, its tile and the split's block columns
-// kb0 .. kb0 + nk - 1 of the nblk.
+// kb0 .. kb0 + nk - 1 of the nblk.  Tile order within a split: groups of
+// kPrefillGroupM M tiles (token bands), the group's M tiles fastest, then N.
+// An XCD's 32 consecutive tiles at 512 tokens are then 4 token bands x 8
+// weight bands, 2 MB of fp16 activations and 2.4 MB of weight blocks per
+// 4 MB L2, where all 8 token bands of 4 weight bands (M fastest over all of
+// them) need 4 MB + 1.2 MB.  Measured on MI355X (us per call, stream
+// launches, two runs each, interleaved): 512 x 4096 x 4096 30.5 against
+// 31.4-31.5, 512 x 14336 x 4096 102.8-103.0 against 104.7-105.0, 512 x 4096
+// x 14336 84.1-84.6 against 84.4-84.9; groups of 2 M tiles were no better at
+// 512 tokens and 0.7 us slower at 256 (2 x 16 bands per XCD).
+constexpr int kPrefillGroupM = 4;
 struct PrefillSplit {
     int sp, mt, nt, kb0, nk;
 };
@@ -99,8 +109,11 @@ __host__ __device__ inline PrefillSplit prefill_split_of(int lin, int mtiles, in
     const int tiles = mtiles * ntiles;
     s.sp = lin / tiles;
     const int tl = lin - s.sp * tiles;
-    s.mt = tl % mtiles;
-    s.nt = tl / mtiles;
+    const int g = tl / (kPrefillGroupM * ntiles);
+    const int gm = mtiles - kPrefillGroupM * g < kPrefillGroupM ? mtiles - kPrefillGroupM * g : kPrefillGroupM;
+    const int idx = tl - g * kPrefillGroupM * ntiles;
+    s.mt = kPrefillGroupM * g + idx % gm;
+    s.nt = idx / gm;
     s.kb0 = s.sp * nblk / nsplit;
     s.nk = (s.sp + 1) * nblk / nsplit - s.kb0;
     return s;
