@@ -714,6 +714,8 @@ def test_prefill_operand_rounding_matches_plain_fp16_in_range():
     (100, 384, 4096),    # eight splits of two block columns
     (17, 1000, 2816),    # 11 block columns in five uneven splits
     (7, 129, 2048),      # four splits, T x outer odd: the scalar sum of the splits
+    (9, 300, 14336),     # token rows past 8192 values: the conversion reads them twice
+    (3, 130, 8448),      # just past 8192 values, 33 block columns
 ])
 def test_prefill_q4k(T, outer, inner):
     """Every token against the per-token GEMV oracle (src/ModelCPU.jl:1001-1017),
