@@ -262,6 +262,17 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
 size_t ihip_prefill_scratch_bytes(int T, int inner);
+/* The per-token prefill loop (src/ModelCPU.jl:1001-1017 over
+ * mul_quant_mat_vec, :285-307) on fp32 operands: the weights dequantized to
+ * fp32 exactly and X as given, multiplied on the fp32 matrix cores.  The
+ * error is fp32 rounding, within 1e-4 * ||w_row|| * ||x|| for any finite X;
+ * ihip_prefill_q4_k_dev (which takes this path for rows of at most 512
+ * columns) rounds both operands of longer rows to fp16, which meets that
+ * bound for the benchmark's data but not for every X (a token equal to a
+ * weight row reaches 2-3x it).  Several times slower than the fp16 path on
+ * long rows; no scratch.  w, X and Y are 16-byte aligned; T * outer < 2^31. */
+int ihip_prefill_q4_k_f32_dev(const void *w, const float *X, float *Y, int T, int inner,
+                              int outer, ihip_stream stream);
 
 /* rmsnorm_cpu! (src/ModelCPU.jl:111-123): out = x * (1/sqrt(mean(x^2) + eps))
  * .* w over n values (out may alias x). */

@@ -930,7 +930,7 @@ int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inn
     if (T <= 0)
         return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
     if (!prefill_fits(T, inner, outer))
-        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes)");
+        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes) and T*outer below 2^31");
     if (!w || !X || !Y)
         return fail(IHIP_ERR_INVALID, "null pointer");
     const void *dw;
@@ -1097,12 +1097,33 @@ int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int
     if (T <= 0)
         return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
     if (!prefill_fits(T, inner, outer))
-        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes)");
+        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes) and T*outer below 2^31");
     if (!w || !X || !xh || !Y)
         return fail(IHIP_ERR_INVALID, "null pointer");
     if (!al16(w) || !al16(X) || !al16(xh) || !al16(Y))
         return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
     hipError_t e = launch_prefill_q4k(w, X, xh, Y, T, inner, outer, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_prefill_q4_k_f32_dev(const void *w, const float *X, float *Y, int T, int inner,
+                              int outer, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(kQ4_K, inner, outer));
+    if (T <= 0)
+        return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if ((int64_t)T * outer > (int64_t)INT32_MAX)
+        return fail(IHIP_ERR_INVALID, "T*outer must stay below 2^31");
+    if (!w || !X || !Y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (!al16(w) || !al16(X) || !al16(Y))
+        return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    hipError_t e = launch_prefill_q4k_f32(w, X, Y, T, inner, outer, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
     return IHIP_OK;

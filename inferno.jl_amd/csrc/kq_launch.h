@@ -46,12 +46,16 @@ int device_cus();
 
 // kq_prefill.hip
 // The prefill GEMM addresses its operands as 32-bit byte offsets from the
-// start of Xh (T x inner fp16) and W (outer Q4_K rows).
+// start of Xh (T x inner fp16) and W (outer Q4_K rows), and counts its
+// output tiles in ints.
 inline bool prefill_fits(int T, int inner, int outer)
 {
     return 2 * (int64_t)T * inner <= (int64_t)UINT32_MAX &&
-           (int64_t)outer * (inner / 256) * 144 <= (int64_t)UINT32_MAX;
+           (int64_t)outer * (inner / 256) * 144 <= (int64_t)UINT32_MAX &&
+           (int64_t)T * outer <= (int64_t)INT32_MAX; // tile counts stay ints
 }
+// Rows of at most this many columns run in the fp32 kernel (k_prefill_q4k_f32).
+constexpr int kPrefillF32MaxK = 512;
 // The caller's scratch xh: the fp16 activations (T x inner), one int per
 // token (its power-of-two scale) from the next 16-byte boundary, then, from
 // the next 16-byte boundary, the partial sums of a split over K.  A split
@@ -146,6 +150,10 @@ inline int prefill_splits(int T, int inner, int outer, int ncu)
 }
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s);
+// The same product on fp32 operands (k_prefill_q4k_f32), any inner; needs
+// T * outer <= INT32_MAX.
+hipError_t launch_prefill_q4k_f32(const void *w, const float *X, float *Y, int T, int inner,
+                                  int outer, hipStream_t s);
 
 // kq_q8k.hip
 hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t s);

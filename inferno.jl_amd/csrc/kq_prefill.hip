@@ -7,7 +7,9 @@
 // a dense contraction: X is rounded once to fp16 (the matrix-core operand
 // type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not), each
 // token row on its own power-of-two scale (k_x_to_f16), and
-// v_mfma_f32_32x32x16_f16 accumulates in fp32.
+// v_mfma_f32_32x32x16_f16 accumulates in fp32.  Rows of at most 512 columns,
+// where fp16 operands leave too little averaging to stay inside that bound,
+// and the fp32-operand entry point run k_prefill_q4k_f32 (below) instead.
 //
 // Tile: 64 tokens x 128 weight rows per workgroup of 8 waves (256
 // workgroups at 512 x 4096 x 4096).  Both operands of one Q4_K block column
@@ -511,11 +513,124 @@ __global__ __launch_bounds__(256) void k_prefill_splits_sum(float *__restrict__ 
     }
 }
 
+// Rows of at most kPrefillF32MaxK columns: an fp32 GEMM on the fp32 matrix
+// cores (v_mfma_f32_32x32x2_f32), with the weights dequantized to fp32 exactly
+// (src/Dequant.jl:364-371) and X read as it is.  With fp16 operands a dot
+// product's rounding error, relative to ||w_row|| ||x||, shrinks only as
+// 1/sqrt(K): over 512 x 2048 outputs of seeded random data the largest
+// error reached 1.7x the row bound 1e-4 ||w_row|| ||x|| at K = 256 and
+// 0.97-1.05x at K = 512 (0.73 at 768, 0.70 at 1024, 0.30 at 4096), so short
+// rows take this path, whose error is fp32 rounding.
+//
+// Tile: 64 tokens x 64 weight rows per workgroup of 4 waves; wave (rw, tw)
+// owns weight rows 32 rw.. and tokens 32 tw.. .  K goes through LDS 128
+// columns at a time, both operands stored k-major (W[k][row], X[k][token])
+// with rows of 96 floats, so a matrix-core operand read (32 consecutive
+// rows or tokens at k and at k + 1) hits 64 distinct banks.
+constexpr int PF32_KC = 128;  // columns per LDS chunk (one Q4_K half block)
+constexpr int PF32_LD = 96;   // floats per LDS row
+__global__ __launch_bounds__(256) void k_prefill_q4k_f32(const uint8_t *__restrict__ W,
+                                                         const float *__restrict__ X,
+                                                         float *__restrict__ Y, int T, int K, int N,
+                                                         int mtiles)
+{
+    __shared__ __attribute__((aligned(16))) float Wl[PF32_KC * PF32_LD];
+    __shared__ __attribute__((aligned(16))) float Xl[PF32_KC * PF32_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rw = wave & 1, tw = wave >> 1;
+    const int mt = (int)blockIdx.x % mtiles, nt = (int)blockIdx.x / mtiles;
+    const int m0 = mt * 64, n0 = nt * 64;
+    const int nblk = K / 256;
+    // fill roles: thread t stages row (or token) t / 4, 32 columns 32 (t % 4) ..
+    const int fr = tid >> 2, fp = tid & 3;
+    const uint8_t *wrow = W + (size_t)min(n0 + fr, N - 1) * (size_t)nblk * 144;
+    const float *xrow = X + (size_t)min(m0 + fr, T - 1) * (size_t)K;
+
+    float16v acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int c = 0; c < 2 * nblk; ++c) {
+        // weights: sub-block sb = 4 (c % 2) + fp of block c / 2, elements
+        // 64 j + 32 h + l = (d sc) q_l - dmin m, q_l the low (h = 0) or high
+        // nibble of qs[32 j + l] (src/Dequant.jl:364-371)
+        {
+            const uint8_t *blk = wrow + (size_t)(c >> 1) * 144;
+            const int sb = 4 * (c & 1) + fp, j = sb >> 1, h = sb & 1;
+            const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+            const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
+            uint32_t sc, m;
+            k_scale_min(hd.y, hd.z, hd.w, sb, sc, m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * j);
+            const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * j);
+            const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const uint32_t q = ((qw[i >> 2] >> (8 * (i & 3))) >> (4 * h)) & 0xfu;
+                Wl[(32 * fp + i) * PF32_LD + fr] = d1 * (float)q - m1;
+            }
+        }
+        // activations: token fr, columns 128 c + 32 fp ..
+        {
+            const float4 *xs = reinterpret_cast<const float4 *>(xrow + (size_t)c * PF32_KC + 32 * fp);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = xs[i];
+                Xl[(32 * fp + 4 * i + 0) * PF32_LD + fr] = v.x;
+                Xl[(32 * fp + 4 * i + 1) * PF32_LD + fr] = v.y;
+                Xl[(32 * fp + 4 * i + 2) * PF32_LD + fr] = v.z;
+                Xl[(32 * fp + 4 * i + 3) * PF32_LD + fr] = v.w;
+            }
+        }
+        __syncthreads();
+        // A = weights (lane l: row l % 32 at k + l / 32), B = activations
+        // (token l % 32 at k + l / 32)
+        const float *wa = Wl + (lane >> 5) * PF32_LD + 32 * rw + (lane & 31);
+        const float *xb = Xl + (lane >> 5) * PF32_LD + 32 * tw + (lane & 31);
+#pragma unroll 8
+        for (int k = 0; k < PF32_KC; k += 2)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[k * PF32_LD], xb[k * PF32_LD], acc, 0, 0, 0);
+        __syncthreads();
+    }
+    // lane l, register r: weight row 32 rw + 8 (r / 4) + 4 (l / 32) + r % 4,
+    // token 32 tw + l % 32
+    const int m = m0 + 32 * tw + (lane & 31);
+    if (m >= T)
+        return;
+    float *yrow = Y + (size_t)m * (size_t)N;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int n = n0 + 32 * rw + 8 * q + 4 * (lane >> 5);
+        const float4 v = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+        if ((N & 3) == 0 && n + 3 < N) {
+            *reinterpret_cast<float4 *>(yrow + n) = v;
+        } else {
+            if (n < N) yrow[n] = v.x;
+            if (n + 1 < N) yrow[n + 1] = v.y;
+            if (n + 2 < N) yrow[n + 2] = v.z;
+            if (n + 3 < N) yrow[n + 3] = v.w;
+        }
+    }
+}
+
+hipError_t launch_prefill_q4k_f32(const void *w, const float *X, float *Y, int T, int inner,
+                                  int outer, hipStream_t s)
+{
+    if (T <= 0 || outer <= 0 || inner <= 0 || inner % 256 || (int64_t)T * outer > (int64_t)INT32_MAX)
+        return hipErrorInvalidValue;
+    const int mtiles = (T + 63) / 64, ntiles = (outer + 63) / 64;
+    hipLaunchKernelGGL(k_prefill_q4k_f32, dim3((unsigned)(mtiles * ntiles)), dim3(256), 0, s,
+                       (const uint8_t *)w, X, Y, T, inner, outer, mtiles);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s)
 {
     if (T <= 0 || inner % 256 || !prefill_fits(T, inner, outer))
         return hipErrorInvalidValue;
+    if (inner <= kPrefillF32MaxK)
+        return launch_prefill_q4k_f32(w, X, Y, T, inner, outer, s);
     int *xs = reinterpret_cast<int *>(static_cast<uint8_t *>(xh) + prefill_scale_offset(T, inner));
     float *P = reinterpret_cast<float *>(static_cast<uint8_t *>(xh) + prefill_part_offset(T, inner));
     hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)T), dim3(256), 0, s, X, (_Float16 *)xh, xs, inner);

@@ -164,6 +164,20 @@ def prefill_q4_k(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, xh: t
     return Y
 
 
+def prefill_q4_k_f32(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, stream=None):
+    """The prefill on fp32 operands (ihip_prefill_q4_k_f32_dev): within the row
+    bound for any finite X, slower than prefill_q4_k on long rows."""
+    if w.ggml_type != Q4_K:
+        raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, "prefill takes a Q4_K weight")
+    T = X.shape[0]
+    if Y is None:
+        Y = torch.empty(T, w.outer, dtype=torch.float32, device=X.device)
+    check(lib().ihip_prefill_q4_k_f32_dev(_ptr(w.data), _ptr(X, torch.float32, "X"),
+                                          _ptr(Y, torch.float32, "Y"), T, w.inner, w.outer,
+                                          _stream(stream)))
+    return Y
+
+
 def quantize_row_q8k(x: torch.Tensor, y: torch.Tensor = None, stream=None) -> torch.Tensor:
     """x (fp32, a multiple of 256 elements) -> Q8_K blocks (uint8, 292 bytes
     per 256 elements), as quantize_row_q8_K (src/kernels/quant_kernels.c:166-194)."""

@@ -198,6 +198,7 @@ def test_lm_head_argmax_norm_graph(other_work):
     (512, 4096, 4096),   # the prefill workload: one workgroup per tile
     (64, 4096, 4096),    # K split eight ways, the partial planes summed
     (17, 1000, 2816),    # ragged tiles, K split
+    (100, 300, 512),     # short rows: the fp32 kernel
 ])
 def test_prefill_graph(T, outer, inner, other_work):
     from inferno_hip import device as D
