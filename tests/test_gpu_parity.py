@@ -855,3 +855,24 @@ def test_prefill_f32_operands_meet_the_bound_for_aligned_activations(T, outer, i
     ratio = np.abs(Y.astype(np.float64) - ref) / (1e-4 * nrm[None, :] * xn[:, None])
     # fp32 rounding over K terms of one sign (x = w_row): 0.06 of the bound at K = 4096
     assert float(np.max(ratio)) < 0.25, f"max err/tol {float(np.max(ratio)):.3g}"
+
+
+@pytest.mark.parametrize("t,outer,inner", [
+    (synth.Q4_K, 300, 4096), (synth.Q5_K, 64, 2048), (synth.Q6_K, 300, 12288),
+    (synth.Q8_0, 64, 4096), (synth.IQ4_NL, 64, 4096), (synth.Q4_K, 9, 256),
+])
+def test_gemv_activations_equal_to_a_weight_row(t, outer, inner):
+    """x equal to a weight row (the input that defeats fp16 operands, where
+    both roundings fall the same way): the integer-digit GEMV stays inside
+    the row bound, which its representation guarantees for every input."""
+    from inferno_hip import device as D
+    say(f"gemv x = w_row type={t} {outer}x{inner}")
+    rng = synth.rng_for(0xC9 + t + inner)
+    w = synth.weight(rng, t, outer, inner)
+    wf = oracle.dequant(t, w, outer * inner).reshape(outer, inner)
+    dw = dweight(w, t, inner, outer)
+    for r in (0, outer // 2, outer - 1):
+        x = wf[r].astype(np.float32)
+        y = D.gemv(dw, dev(x)).cpu().numpy()
+        assert_within(y, oracle.gemv_f64(t, w, x, inner, outer),
+                      oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), f"x = row {r}")
