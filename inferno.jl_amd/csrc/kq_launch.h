@@ -56,6 +56,9 @@ inline bool prefill_fits(int T, int inner, int outer)
 }
 // Rows of at most this many columns run in the fp32 kernel (k_prefill_q4k_f32).
 constexpr int kPrefillF32MaxK = 512;
+// Longer rows of at most this many columns take fp16 weights rounded once
+// from their exact values (k_prefill_q4k<true>).
+constexpr int kPrefillExactWMaxK = 2048;
 // The caller's scratch xh: the fp16 activations (T x inner), one int per
 // token (its power-of-two scale) from the next 16-byte boundary, then, from
 // the next 16-byte boundary, the partial sums of a split over K.  A split

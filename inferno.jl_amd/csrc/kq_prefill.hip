@@ -7,9 +7,12 @@
 // a dense contraction: X is rounded once to fp16 (the matrix-core operand
 // type; fp16 keeps the 1e-4*||w||*||x|| bound where bf16 does not), each
 // token row on its own power-of-two scale (k_x_to_f16), and
-// v_mfma_f32_32x32x16_f16 accumulates in fp32.  Rows of at most 512 columns,
-// where fp16 operands leave too little averaging to stay inside that bound,
-// and the fp32-operand entry point run k_prefill_q4k_f32 (below) instead.
+// v_mfma_f32_32x32x16_f16 accumulates in fp32.  A dot product over fp16
+// operands errs by about 2.8e-4 ||w|| ||x|| / sqrt(K) on random data, so short
+// rows need more care: rows of at most 512 columns, and the fp32-operand
+// entry point, run k_prefill_q4k_f32 (below); rows of at most 2048 columns
+// round each weight once from its exact value (k_prefill_q4k<true>) instead
+// of through fp16 sub-block scales.
 //
 // Tile: 64 tokens x 128 weight rows per workgroup of 8 waves (256
 // workgroups at 512 x 4096 x 4096).  Both operands of one Q4_K block column
@@ -224,6 +227,38 @@ __device__ __forceinline__ half8 pf_dequant8(uint2 bytes, bool high, half2v dsc,
     return r;
 }
 
+// The same 8 weights rounded once from their exact fp32 values,
+// rn16((d sc) q - dmin m): q exact in fp32 from the scaled convert, one fp32
+// FMA (d sc q is exact, so the FMA rounds only the difference), then
+// v_cvt_pk_f16_f32.  Rounding d sc and dmin m to fp16 first, as
+// pf_dequant8 does, puts one shared relative error on all 32 weights of a
+// sub-block; this form leaves each weight its own.
+__device__ __forceinline__ half8 pf_dequant8_exact(uint2 bytes, bool high, float dsc, float dmm)
+{
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    uint32_t w0 = bytes.x, w1 = bytes.y;
+    if (high) {
+        w0 >>= 4;
+        w1 >>= 4;
+    }
+    w0 &= 0x0f0f0f0fu;
+    w1 &= 0x0f0f0f0fu;
+    const f2v q01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w0, 512.0f, false);
+    const f2v q23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w0, 512.0f, true);
+    const f2v q45 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w1, 512.0f, false);
+    const f2v q67 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w1, 512.0f, true);
+    const f2v r01 = {fmaf(q01[0], dsc, dmm), fmaf(q01[1], dsc, dmm)};
+    const f2v r23 = {fmaf(q23[0], dsc, dmm), fmaf(q23[1], dsc, dmm)};
+    const f2v r45 = {fmaf(q45[0], dsc, dmm), fmaf(q45[1], dsc, dmm)};
+    const f2v r67 = {fmaf(q67[0], dsc, dmm), fmaf(q67[1], dsc, dmm)};
+    const half2v h01 = __builtin_convertvector(r01, half2v), h23 = __builtin_convertvector(r23, half2v);
+    const half2v h45 = __builtin_convertvector(r45, half2v), h67 = __builtin_convertvector(r67, half2v);
+    half8 r;
+    r[0] = h01[0]; r[1] = h01[1]; r[2] = h23[0]; r[3] = h23[1];
+    r[4] = h45[0]; r[5] = h45[1]; r[6] = h67[0]; r[7] = h67[1];
+    return r;
+}
+
 // One column's operands of this lane, read from a ring slot: 2 x 8 quant
 // bytes of weight rows `blk0` / `blk1` (rows li and li + 32 of the wave's 64)
 // for sub-block pair j, the block header of row li + 32 h only (the two lane
@@ -258,41 +293,72 @@ __device__ __forceinline__ void pf_read(const uint8_t *sa, const uint8_t *blk0, 
 // Dequantize the column's weights into matrix-core operands and accumulate.
 // acc[u][t] is the 32 x 32 tile (weight rows 32u.., tokens 32t..): lane l,
 // register r hold token 32t + l % 32, weight row 32u + 8 (r / 4) + 4 (l / 32) + r % 4.
+// EXACTW: each weight rounded once from its exact value (pf_dequant8_exact),
+// for rows of at most kPrefillExactWMaxK columns, where the shared rounding
+// of a sub-block's scale averages over too few sub-blocks.
+template <bool EXACTW>
 __device__ __forceinline__ void pf_mma(const PfOps &o, int j, float16v (&acc)[2][2])
 {
-    // Scale d*sc and min -dmin*m of sub-blocks 2j (A) and 2j + 1 (B), each
-    // rounded once to fp16, for this lane half's row, packed (A, B) ...
+    // Scale d*sc and min -dmin*m of sub-blocks 2j (A) and 2j + 1 (B) for
+    // this lane half's row (rounded once to fp16 and packed (A, B), or kept
+    // in fp32 when EXACTW) ...
     const float d = h2f(o.hd.x & 0xffffu), dmin = h2f(o.hd.x >> 16);
     float scA, mA, scB, mB;
     k_scale_min_pair(o.hd.y, o.hd.z, o.hd.w, j, scA, mA, scB, mB);
-    const half2v ds = {(_Float16)(d * scA), (_Float16)(d * scB)};
-    const half2v dm = {(_Float16)(-(dmin * mA)), (_Float16)(-(dmin * mB))};
     // ... then exchanged between the lane halves: v_permlane32_swap of a
     // register with itself leaves lanes 0-31's value (row li) in the first
     // result and lanes 32-63's (row li + 32) in the second, in every lane.
-    const uint32_t dsu = __builtin_bit_cast(uint32_t, ds), dmu = __builtin_bit_cast(uint32_t, dm);
-    const auto xs = __builtin_amdgcn_permlane32_swap(dsu, dsu, false, false);
-    const auto xm = __builtin_amdgcn_permlane32_swap(dmu, dmu, false, false);
-    half2v dsA[2], dmA[2], dsB[2], dmB[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const half2v s2 = __builtin_bit_cast(half2v, (uint32_t)xs[u]);
-        const half2v m2 = __builtin_bit_cast(half2v, (uint32_t)xm[u]);
-        dsA[u] = half2v{s2[0], s2[0]};
-        dmA[u] = half2v{m2[0], m2[0]};
-        dsB[u] = half2v{s2[1], s2[1]};
-        dmB[u] = half2v{m2[1], m2[1]};
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
+    if constexpr (EXACTW) {
+        const float dsa = d * scA, dsb = d * scB, dma = -(dmin * mA), dmb = -(dmin * mB);
+        const auto xa = __builtin_amdgcn_permlane32_swap(__float_as_uint(dsa), __float_as_uint(dsa), false, false);
+        const auto xb = __builtin_amdgcn_permlane32_swap(__float_as_uint(dsb), __float_as_uint(dsb), false, false);
+        const auto ya = __builtin_amdgcn_permlane32_swap(__float_as_uint(dma), __float_as_uint(dma), false, false);
+        const auto yb = __builtin_amdgcn_permlane32_swap(__float_as_uint(dmb), __float_as_uint(dmb), false, false);
+        float dsA[2], dmA[2], dsB[2], dmB[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const half8 wq = pf_dequant8((s & 1) ? o.q1[u] : o.q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
-                                         s >= 2 ? dmB[u] : dmA[u]);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, o.x[s][t], acc[u][t], 0, 0, 0);
+            dsA[u] = __uint_as_float((uint32_t)xa[u]);
+            dsB[u] = __uint_as_float((uint32_t)xb[u]);
+            dmA[u] = __uint_as_float((uint32_t)ya[u]);
+            dmB[u] = __uint_as_float((uint32_t)yb[u]);
         }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const half8 wq = pf_dequant8_exact((s & 1) ? o.q1[u] : o.q0[u], s >= 2,
+                                                   s >= 2 ? dsB[u] : dsA[u], s >= 2 ? dmB[u] : dmA[u]);
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, o.x[s][t], acc[u][t], 0, 0, 0);
+            }
+    } else {
+        const half2v ds = {(_Float16)(d * scA), (_Float16)(d * scB)};
+        const half2v dm = {(_Float16)(-(dmin * mA)), (_Float16)(-(dmin * mB))};
+        const uint32_t dsu = __builtin_bit_cast(uint32_t, ds), dmu = __builtin_bit_cast(uint32_t, dm);
+        const auto xs = __builtin_amdgcn_permlane32_swap(dsu, dsu, false, false);
+        const auto xm = __builtin_amdgcn_permlane32_swap(dmu, dmu, false, false);
+        half2v dsA[2], dmA[2], dsB[2], dmB[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const half2v s2 = __builtin_bit_cast(half2v, (uint32_t)xs[u]);
+            const half2v m2 = __builtin_bit_cast(half2v, (uint32_t)xm[u]);
+            dsA[u] = half2v{s2[0], s2[0]};
+            dmA[u] = half2v{m2[0], m2[0]};
+            dsB[u] = half2v{s2[1], s2[1]};
+            dmB[u] = half2v{m2[1], m2[1]};
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const half8 wq = pf_dequant8((s & 1) ? o.q1[u] : o.q0[u], s >= 2, s >= 2 ? dsB[u] : dsA[u],
+                                             s >= 2 ? dmB[u] : dmA[u]);
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq, o.x[s][t], acc[u][t], 0, 0, 0);
+            }
+    }
 }
 
 // Wait for this wave's copies, leaving the last n in flight (n is 0 or one
@@ -319,6 +385,7 @@ __device__ __forceinline__ void pf_wait_copies(int n)
 // column; at the end wave (rh, j) finishes tile combination c = j (weight
 // half u = c >> 1, token half t = c & 1) of its row half from the four
 // waves' partial sums.
+template <bool EXACTW>
 __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__restrict__ W,
                                                             const _Float16 *__restrict__ Xh,
                                                             const int *__restrict__ xs,
@@ -397,7 +464,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
         const int ns = slot == 2 ? 0 : slot + 1;
         pf_read(ring + ns * PF_SLOT, ba + ns * PF_SLOT, ba + ns * PF_SLOT + 32 * 144, j, h, li, nxt);
         __builtin_amdgcn_sched_barrier(0);
-        pf_mma(cur, j, acc);
+        pf_mma<EXACTW>(cur, j, acc);
     };
     int kb = 0, slot = 0;
     for (; kb + 2 < nk; kb += 2) {
@@ -408,9 +475,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_prefill_q4k(const uint8_t *__res
     }
     if (kb + 1 < nk) {
         step(kb, slot, o0, o1);
-        pf_mma(o1, j, acc);
+        pf_mma<EXACTW>(o1, j, acc);
     } else {
-        pf_mma(o0, j, acc);
+        pf_mma<EXACTW>(o0, j, acc);
     }
     __syncthreads(); // every wave is done with the ring
 
@@ -523,11 +590,13 @@ __global__ __launch_bounds__(256) void k_prefill_splits_sum(float *__restrict__ 
 // rows take this path, whose error is fp32 rounding.
 //
 // Tile: 64 tokens x 64 weight rows per workgroup of 4 waves; wave (rw, tw)
-// owns weight rows 32 rw.. and tokens 32 tw.. .  K goes through LDS 128
-// columns at a time, both operands stored k-major (W[k][row], X[k][token])
-// with rows of 96 floats, so a matrix-core operand read (32 consecutive
-// rows or tokens at k and at k + 1) hits 64 distinct banks.
-constexpr int PF32_KC = 128;  // columns per LDS chunk (one Q4_K half block)
+// owns weight rows 32 rw.. and tokens 32 tw.. .  K goes through LDS 64
+// columns at a time (48 KB, so that two or three workgroups share a CU and
+// one fills its chunk while another multiplies), both operands stored
+// k-major (W[k][row], X[k][token]) with rows of 96 floats, so a matrix-core
+// operand read (32 consecutive rows or tokens at k and at k + 1) hits 64
+// distinct banks.
+constexpr int PF32_KC = 64;   // columns per LDS chunk (two Q4_K sub-blocks): 48 KB of LDS
 constexpr int PF32_LD = 96;   // floats per LDS row
 __global__ __launch_bounds__(256) void k_prefill_q4k_f32(const uint8_t *__restrict__ W,
                                                          const float *__restrict__ X,
@@ -549,37 +618,37 @@ __global__ __launch_bounds__(256) void k_prefill_q4k_f32(const uint8_t *__restri
     float16v acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    for (int c = 0; c < 2 * nblk; ++c) {
-        // weights: sub-block sb = 4 (c % 2) + fp of block c / 2, elements
-        // 64 j + 32 h + l = (d sc) q_l - dmin m, q_l the low (h = 0) or high
-        // nibble of qs[32 j + l] (src/Dequant.jl:364-371)
+    for (int c = 0; c < 4 * nblk; ++c) {
+        // weights: columns 16 fp .. of chunk c are elements l0 .. l0 + 15 of
+        // sub-block sb = 2 (c % 4) + fp / 2 of block c / 4, element
+        // 64 j + 32 h + l = (d sc) q_l - dmin m with q_l the low (h = 0) or
+        // high nibble of qs[32 j + l] (src/Dequant.jl:364-371)
         {
-            const uint8_t *blk = wrow + (size_t)(c >> 1) * 144;
-            const int sb = 4 * (c & 1) + fp, j = sb >> 1, h = sb & 1;
+            const uint8_t *blk = wrow + (size_t)(c >> 2) * 144;
+            const int sb = 2 * (c & 3) + (fp >> 1), j = sb >> 1, h = sb & 1, l0 = 16 * (fp & 1);
             const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
             const float d = h2f(hd.x & 0xffffu), dmin = h2f(hd.x >> 16);
             uint32_t sc, m;
             k_scale_min(hd.y, hd.z, hd.w, sb, sc, m);
             const float d1 = d * (float)sc, m1 = dmin * (float)m;
-            const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * j);
-            const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * j);
-            const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * j + l0);
+            const uint32_t qw[4] = {qa.x, qa.y, qa.z, qa.w};
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
+            for (int i = 0; i < 16; ++i) {
                 const uint32_t q = ((qw[i >> 2] >> (8 * (i & 3))) >> (4 * h)) & 0xfu;
-                Wl[(32 * fp + i) * PF32_LD + fr] = d1 * (float)q - m1;
+                Wl[(16 * fp + i) * PF32_LD + fr] = d1 * (float)q - m1;
             }
         }
-        // activations: token fr, columns 128 c + 32 fp ..
+        // activations: token fr, columns 64 c + 16 fp ..
         {
-            const float4 *xs = reinterpret_cast<const float4 *>(xrow + (size_t)c * PF32_KC + 32 * fp);
+            const float4 *xs = reinterpret_cast<const float4 *>(xrow + (size_t)c * PF32_KC + 16 * fp);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < 4; ++i) {
                 const float4 v = xs[i];
-                Xl[(32 * fp + 4 * i + 0) * PF32_LD + fr] = v.x;
-                Xl[(32 * fp + 4 * i + 1) * PF32_LD + fr] = v.y;
-                Xl[(32 * fp + 4 * i + 2) * PF32_LD + fr] = v.z;
-                Xl[(32 * fp + 4 * i + 3) * PF32_LD + fr] = v.w;
+                Xl[(16 * fp + 4 * i + 0) * PF32_LD + fr] = v.x;
+                Xl[(16 * fp + 4 * i + 1) * PF32_LD + fr] = v.y;
+                Xl[(16 * fp + 4 * i + 2) * PF32_LD + fr] = v.z;
+                Xl[(16 * fp + 4 * i + 3) * PF32_LD + fr] = v.w;
             }
         }
         __syncthreads();
@@ -636,9 +705,13 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
     hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)T), dim3(256), 0, s, X, (_Float16 *)xh, xs, inner);
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
     const int nsplit = prefill_splits(T, inner, outer, device_cus());
-    hipLaunchKernelGGL(k_prefill_q4k, dim3(prefill_grid(mtiles * ntiles, nsplit)), dim3(PF_THREADS), 0, s,
-                       (const uint8_t *)w, (const _Float16 *)xh, (const int *)xs, Y, P, T, inner, outer,
-                       mtiles, ntiles, nsplit);
+    const dim3 grid(prefill_grid(mtiles * ntiles, nsplit));
+    if (inner <= kPrefillExactWMaxK)
+        hipLaunchKernelGGL(k_prefill_q4k<true>, grid, dim3(PF_THREADS), 0, s, (const uint8_t *)w,
+                           (const _Float16 *)xh, (const int *)xs, Y, P, T, inner, outer, mtiles, ntiles, nsplit);
+    else
+        hipLaunchKernelGGL(k_prefill_q4k<false>, grid, dim3(PF_THREADS), 0, s, (const uint8_t *)w,
+                           (const _Float16 *)xh, (const int *)xs, Y, P, T, inner, outer, mtiles, ntiles, nsplit);
     if (nsplit > 1) {
         const int64_t n = (int64_t)T * outer;
         const int64_t units = (n & 3) == 0 ? n >> 2 : n;

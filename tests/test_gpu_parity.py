@@ -719,6 +719,8 @@ def test_prefill_operand_rounding_matches_plain_fp16_in_range():
     (515, 1141, 256),    # short rows (fp32 kernel): seeded shapes whose fp16-operand
     (487, 1645, 512),    #   errors reached 1.5x and 1.05x the row bound
     (66, 130, 768),      # the shortest rows on the fp16 matrix cores
+    (582, 1758, 768),    # a seeded shape whose shared sub-block scale rounding reached 1.14x
+    (100, 300, 2560),    # the first rows past the exactly rounded weights
 ])
 def test_prefill_q4k(T, outer, inner):
     """Every token against the per-token GEMV oracle (src/ModelCPU.jl:1001-1017)

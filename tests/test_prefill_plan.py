@@ -38,7 +38,7 @@ def chk():
 GPU_SHAPES = ((512, 4096, 4096), (70, 300, 2048), (1, 128, 256), (33, 129, 1792), (5, 64, 512),
               (40, 200, 768), (64, 256, 1024), (512, 512, 4096), (100, 384, 4096),
               (17, 1000, 2816), (7, 129, 2048), (48, 320, 2048), (8, 128, 1024),
-              (9, 300, 14336), (3, 130, 8448))
+              (9, 300, 14336), (3, 130, 8448), (582, 1758, 768), (100, 300, 2560), (66, 130, 768))
 
 
 @pytest.mark.parametrize("T,outer,inner", GPU_SHAPES)
