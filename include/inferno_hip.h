@@ -257,8 +257,11 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
  * of ihip_prefill_scratch_bytes(T, inner) bytes: the rounded activations
  * (T*inner fp16 values), one scale exponent per token and room for the
  * partial sums of a weight of few rows, whose K is split over several
- * workgroups (the size does not depend on outer).  w, X, xh and Y are
- * 16-byte aligned; calls that share xh must not overlap on the GPU. */
+ * workgroups (the size does not depend on outer).  Rows of more than 512
+ * columns multiply fp16 operands: any finite X (each token row is scaled by
+ * a power of two), but every dequantized weight below 65504 in magnitude.
+ * w, X, xh and Y are 16-byte aligned; calls that share xh must not overlap
+ * on the GPU. */
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
 size_t ihip_prefill_scratch_bytes(int T, int inner);
@@ -269,8 +272,9 @@ size_t ihip_prefill_scratch_bytes(int T, int inner);
  * ihip_prefill_q4_k_dev (which takes this path for rows of at most 512
  * columns) rounds both operands of longer rows to fp16, which meets that
  * bound for the benchmark's data but not for every X (a token equal to a
- * weight row reaches 2-3x it).  Several times slower than the fp16 path on
- * long rows; no scratch.  w, X and Y are 16-byte aligned; T * outer < 2^31. */
+ * weight row reaches 2-3x it) and needs every dequantized weight below
+ * 65504 in magnitude.  Several times slower than the fp16 path on long rows;
+ * no scratch.  w, X and Y are 16-byte aligned; T * outer < 2^31. */
 int ihip_prefill_q4_k_f32_dev(const void *w, const float *X, float *Y, int T, int inner,
                               int outer, ihip_stream stream);
 

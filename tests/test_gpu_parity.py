@@ -878,3 +878,27 @@ def test_gemv_activations_equal_to_a_weight_row(t, outer, inner):
         y = D.gemv(dw, dev(x)).cpu().numpy()
         assert_within(y, oracle.gemv_f64(t, w, x, inner, outer),
                       oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), f"x = row {r}")
+
+
+def test_prefill_f32_operands_take_weights_past_fp16_range():
+    """Block scales d ~ 200 put dequantized weights past fp16's 65504 (the
+    fp16-operand prefill requires |w| < 65504): the fp32-operand entry point
+    meets the per-token GEMV oracle (src/ModelCPU.jl:285-307) there, and at
+    tiny scales (d ~ 1e-7, fp16 subnormal)."""
+    from inferno_hip import device as D
+    T, outer, inner = 40, 130, 1024
+    for dval in (200.0, 1e-7):
+        say(f"prefill fp32 operands, block scales ~ {dval:g}")
+        rng = synth.rng_for(0xCA)
+        w = synth.weight(rng, synth.Q4_K, outer, inner)
+        b = w.reshape(outer, inner // 256, 144)
+        d = np.abs(rng.standard_normal((outer, inner // 256))) * dval
+        b[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(outer, inner // 256, 2)
+        b[:, :, 2:4] = (d * 0.5).astype(np.float16).view(np.uint8).reshape(outer, inner // 256, 2)
+        X = rng.standard_normal((T, inner)).astype(np.float32)
+        Y = D.prefill_q4_k_f32(dweight(w, synth.Q4_K, inner, outer), dev(X)).cpu().numpy()
+        ref = oracle.gemm_f64(synth.Q4_K, w, X, inner, outer)
+        nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+        xn = np.linalg.norm(X.astype(np.float64), axis=1)
+        assert np.all(np.isfinite(Y))
+        assert np.all(np.abs(Y.astype(np.float64) - ref) <= 1e-4 * nrm[None, :] * xn[:, None])
