@@ -902,3 +902,34 @@ def test_prefill_f32_operands_take_weights_past_fp16_range():
         xn = np.linalg.norm(X.astype(np.float64), axis=1)
         assert np.all(np.isfinite(Y))
         assert np.all(np.abs(Y.astype(np.float64) - ref) <= 1e-4 * nrm[None, :] * xn[:, None])
+
+
+def _set_block_scales(w, t, outer, inner, rng, dval):
+    """Overwrite every block's fp16 scale(s) with |N(0,1)| * dval."""
+    be = {synth.Q4_K: 256, synth.Q5_K: 256, synth.Q6_K: 256, synth.Q8_0: 32, synth.IQ4_NL: 32}[t]
+    bb = {synth.Q4_K: 144, synth.Q5_K: 176, synth.Q6_K: 210, synth.Q8_0: 34, synth.IQ4_NL: 18}[t]
+    b = w.reshape(outer, inner // be, bb)
+    d = (np.abs(rng.standard_normal((outer, inner // be))) * dval).astype(np.float16)
+    off = 208 if t == synth.Q6_K else 0
+    b[:, :, off:off + 2] = d.view(np.uint8).reshape(outer, inner // be, 2)
+    if t in (synth.Q4_K, synth.Q5_K):
+        b[:, :, 2:4] = (d * np.float16(0.5)).view(np.uint8).reshape(outer, inner // be, 2)
+
+
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0, synth.IQ4_NL])
+@pytest.mark.parametrize("dval", [3000.0, 1e-7])
+def test_gemv_extreme_block_scales(t, dval):
+    """Block scales near fp16's top (~3000, weights up to ~3e6) and in its
+    subnormal range (~1e-7): the GEMV's scales and sums are fp32, so the row
+    bound holds for any finite weights (src/ModelCPU.jl:285-379)."""
+    from inferno_hip import device as D
+    outer, inner = 70, 4096
+    say(f"gemv type {t} block scales ~ {dval:g}")
+    rng = synth.rng_for(0xCB + t)
+    w = synth.weight(rng, t, outer, inner)
+    _set_block_scales(w, t, outer, inner, rng, dval)
+    x = synth.activations(rng, inner)
+    y = D.gemv(dweight(w, t, inner, outer), dev(x)).cpu().numpy()
+    assert np.all(np.isfinite(y))
+    assert_within(y, oracle.gemv_f64(t, w, x, inner, outer),
+                  oracle.tolerance(oracle.row_norms(t, w, inner, outer), x), f"type {t} d ~ {dval:g}")
