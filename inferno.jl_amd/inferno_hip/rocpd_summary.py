@@ -34,16 +34,27 @@ def demangle(name: str) -> str:
     except (OSError, subprocess.CalledProcessError):
         pass
     # c++filt does not know every type (e.g. _Float16): keep the nested name
-    m = re.match(r"_ZN((?:\d+\w+?)+)E", name)
-    if not m:
+    # and the literal template arguments (bool / int) of its components
+    if not name.startswith("_ZN"):
         return name
-    parts, rest = [], m.group(1)
-    while rest:
+    parts, rest = [], name[3:]
+    while rest and rest[0].isdigit():
         k = re.match(r"(\d+)", rest)
-        n = int(k.group(1))
-        parts.append(rest[len(k.group(1)):len(k.group(1)) + n])
-        rest = rest[len(k.group(1)) + n:]
-    return "::".join(parts)
+        s, n = len(k.group(1)), int(k.group(1))
+        parts.append(rest[s:s + n])
+        rest = rest[s + n:]
+        if rest.startswith("I"):
+            args, rest = [], rest[1:]
+            while rest and rest[0] != "E":
+                a = re.match(r"L([bij])(n?\d+)E", rest)
+                if not a:
+                    return "::".join(parts) + "<...>"
+                v = a.group(2).replace("n", "-")
+                args.append(("true" if v == "1" else "false") if a.group(1) == "b" else v)
+                rest = rest[a.end():]
+            rest = rest[1:]
+            parts[-1] += "<" + ", ".join(args) + ">"
+    return "::".join(parts) if parts else name
 
 
 def short(name: str, width: int = 90) -> str:
