@@ -146,6 +146,40 @@ def test_gemv_q8k_x_bit_exact(t, outer, inner):
         assert same_bits(y, oracle.ref_gemv(t, w, x, inner, outer))
 
 
+def _random_shape(seed):
+    """Rows of 1..159 Q8_K blocks and 1..9000 of them, capped near 30 M weights."""
+    r = np.random.default_rng(seed)
+    inner = 256 * int(r.integers(1, [16, 64, 160][seed % 3]))
+    outer = int(r.integers(1, [300, 3000, 9000][(seed // 3) % 3]))
+    return max(1, min(outer, 30_000_000 // inner)), inner
+
+
+@pytest.mark.parametrize("seed", range(9))
+def test_gemv_q8k_x_random_shapes(seed):
+    """Random shapes over every launch plan of the int8 path: with q8 given,
+    and in one launch for Q4_K / Q5_K rows of at most 32768 columns (longer
+    rows need q8, and the call says so)."""
+    from inferno_hip import device as D
+    from inferno_hip._lib import IHIPArgumentError
+    outer, inner = _random_shape(seed)
+    for t in K_TYPES:
+        rng = synth.rng_for(0x9A0 + seed * 7 + t)
+        w = synth.weight(rng, t, outer, inner)
+        x = synth.activations(rng, inner) * np.float32(rng.uniform(0.1, 30))
+        say(f"gemv_q8k_x random seed {seed} type {t} {outer}x{inner}")
+        dw = D.DeviceWeight(dev(w), t, inner, outer)
+        want = oracle.gemv_q8k(t, w, x, inner, outer)
+        q8 = torch.empty(inner // 256 * 292, dtype=torch.uint8, device="cuda")
+        assert same_bits(D.gemv_q8k_x(dw, dev(x), q8=q8).cpu().numpy(), want)
+        if t == synth.Q6_K:
+            continue
+        if inner <= 32768:
+            assert same_bits(D.gemv_q8k_x(dw, dev(x)).cpu().numpy(), want)
+        else:
+            with pytest.raises(IHIPArgumentError):
+                D.gemv_q8k_x(dw, dev(x))
+
+
 @pytest.mark.parametrize("t", [synth.Q4_K, synth.Q5_K])
 def test_gemv_q8k_x_quantizer_edge_blocks(t):
     """Zero blocks (d = 0), every .5 tie of both signs, tiny and huge scales,
