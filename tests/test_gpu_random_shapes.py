@@ -9,8 +9,12 @@ oracle. The ranges cover:
 * persistent or not;
 * 1..16 streamed 2048-column segments;
 * prefill tiles with and without the split over K;
-* fused gate/up pairs of every hidden size class, then the down GEMV.
-The bars are those of test_gpu_parity.py:
+* fused gate/up pairs of every hidden size class, then the down GEMV;
+* dequantization of every format, some sources off 16-byte alignment;
+* the fp32-operand prefill, token rows scaled by 2^-60 .. 2^60;
+* the FFN block with its norm and residual, every gate/up and down format.
+The bars are those of test_gpu_parity.py and test_gpu_block.py:
+* bit-exact dequantization (src/Dequant.jl:304-601);
 * the row tolerance 1e-4 * ||w_row|| * ||x|| for GEMV and GEMM outputs
   (src/ModelCPU.jl:285-379, 1001-1017);
 * the exact token wherever the top two logits lie further apart than the
@@ -72,9 +76,32 @@ def _draw(seed):
     return gemv, prefill, lm, ffn
 
 
+def _draw_more(seed):
+    """Dequantization (some sources off 16-byte alignment), the fp32-operand
+    prefill (token rows scaled by 2^-60 .. 2^60) and the FFN block with its
+    norm and residual, from a second stream of the same seed."""
+    r = np.random.default_rng([seed, 2])
+    deq = []
+    for t in FMTS:
+        be = BLOCK[t]
+        inner = be * int(r.integers(1, 32768 // be + 1))
+        outer = max(1, min(int(r.integers(1, 20000)), 12_000_000 // inner))
+        deq.append((t, outer, inner, int(r.choice([0, 0, 0, 2, 4, 8]))))
+    pf32 = [(int(r.integers(1, 700)), int(r.integers(1, 3000)), 256 * int(r.integers(1, 33)))]
+    gt = (synth.Q4_K, synth.Q5_K, synth.Q8_0, synth.IQ4_NL)[int(r.integers(0, 4))]
+    dt = (synth.Q6_K, synth.Q4_K, synth.Q5_K, synth.Q8_0, synth.IQ4_NL)[int(r.integers(0, 5))]
+    hidden, inter = 256 * int(r.integers(1, 49)), 256 * int(r.integers(1, 65))
+    while hidden * inter > 20_000_000:
+        inter = max(256, inter // 512 * 256)
+    return deq, pf32, [(gt, dt, hidden, inter)]
+
+
 GEMV, PREFILL, LM, FFN = [], [], [], []
+DEQ, PF32, BLOCKS = [], [], []
 for _s in SEEDS:
     for _acc, _cases in zip((GEMV, PREFILL, LM, FFN), _draw(_s)):
+        _acc.extend(c for c in _cases if c not in _acc)
+    for _acc, _cases in zip((DEQ, PF32, BLOCKS), _draw_more(_s)):
         _acc.extend(c for c in _cases if c not in _acc)
 
 
@@ -177,3 +204,52 @@ def test_random_ffn(gt, dt, hidden, inter):
     yb = 1e-4 * nd * np.linalg.norm(h_ref) + nd * np.linalg.norm(h - h_ref)
     err = np.abs(y.astype(np.float64) - y_ref)
     assert np.all(err <= yb), f"y: max err/bound {float(np.max(err / yb)):.3g}"
+
+
+@pytest.mark.parametrize("t,outer,inner,off", DEQ)
+def test_random_dequant(t, outer, inner, off):
+    from inferno_hip import device as D
+    say(f"dequant type {t} {outer}x{inner} source offset {off}")
+    rng = synth.rng_for(0x6300 + 3 * outer + inner + t)
+    w = synth.weight(rng, t, outer, inner)
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    buf[off:off + w.size] = torch.from_numpy(w).cuda()
+    got = D.dequantize(D.DeviceWeight(buf[off:off + w.size], t, inner, outer)).cpu().numpy()
+    want = oracle.dequant(t, w, outer * inner)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("T,outer,inner", PF32)
+def test_random_prefill_f32_operands(T, outer, inner):
+    from inferno_hip import device as D
+    say(f"prefill on fp32 operands T={T} {outer}x{inner}")
+    rng = synth.rng_for(0x6400 + T + outer + inner)
+    w = synth.weight(rng, synth.Q4_K, outer, inner)
+    X = rng.standard_normal((T, inner)).astype(np.float32)
+    X *= np.exp2(rng.integers(-60, 61, T)).astype(np.float32)[:, None]
+    Y = D.prefill_q4_k_f32(_dw(w, synth.Q4_K, inner, outer), torch.from_numpy(X).cuda()).cpu().numpy()
+    ref = oracle.gemm_f64(synth.Q4_K, w, X, inner, outer)
+    nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+    xn = np.linalg.norm(X.astype(np.float64), axis=1)
+    ratio = np.abs(Y.astype(np.float64) - ref) / (1e-4 * nrm[None, :] * xn[:, None])
+    assert np.all(np.isfinite(Y))
+    assert np.all(ratio <= 1.0), f"max err/tol {float(np.max(ratio)):.3g}"
+
+
+@pytest.mark.parametrize("gt,dt,hidden,inter", BLOCKS)
+def test_random_ffn_block(gt, dt, hidden, inter):
+    """x += Wd (silu(Wg n) * (Wu n)), n = rmsnorm(x) .* norm_w
+    (src/ModelCPU.jl:913-920), with the bounds of test_gpu_block.py."""
+    from inferno_hip import _lib
+    from inferno_hip import device as D
+    import test_gpu_block as TB
+    say(f"ffn block gate/up {gt} down {dt} hidden {hidden} inter {inter}")
+    eps = 1e-6
+    case = TB._block_case(hidden, inter, gt, dt, 0x6500 + hidden + inter)
+    wg, wu, wd, x, nw = case
+    xd = torch.from_numpy(x).cuda()
+    h = torch.full((_lib.lib().ihip_ffn_block_scratch_floats(gt, gt, hidden, inter),), float("nan"),
+                   device="cuda")
+    D.ffn_block(_dw(wg, gt, hidden, inter), _dw(wu, gt, hidden, inter), _dw(wd, dt, inter, hidden),
+                torch.from_numpy(nw).cuda(), eps, xd, h=h)
+    TB._check_block(xd.cpu().numpy(), h[:inter].cpu().numpy(), x, case, gt, dt, hidden, inter, eps)
