@@ -12,9 +12,12 @@ oracle. The ranges cover:
 * fused gate/up pairs of every hidden size class, then the down GEMV;
 * dequantization of every format, some sources off 16-byte alignment;
 * the fp32-operand prefill, token rows scaled by 2^-60 .. 2^60;
-* the FFN block with its norm and residual, every gate/up and down format.
+* the FFN block with its norm and residual, every gate/up and down format;
+* GEMVs whose weight and x start off 16-byte alignment;
+* the standalone argmax over logits whose maximum appears 1-3 times.
 The bars are those of test_gpu_parity.py and test_gpu_block.py:
 * bit-exact dequantization (src/Dequant.jl:304-601);
+* the first maximal index for the argmax (src/CommonOps.jl:142-163);
 * the row tolerance 1e-4 * ||w_row|| * ||x|| for GEMV and GEMM outputs
   (src/ModelCPU.jl:285-379, 1001-1017);
 * the exact token wherever the top two logits lie further apart than the
@@ -78,8 +81,9 @@ def _draw(seed):
 
 def _draw_more(seed):
     """Dequantization (some sources off 16-byte alignment), the fp32-operand
-    prefill (token rows scaled by 2^-60 .. 2^60) and the FFN block with its
-    norm and residual, from a second stream of the same seed."""
+    prefill (token rows scaled by 2^-60 .. 2^60), the FFN block with its
+    norm and residual, a GEMV on unaligned pointers and the standalone
+    argmax, from a second stream of the same seed."""
     r = np.random.default_rng([seed, 2])
     deq = []
     for t in FMTS:
@@ -93,15 +97,22 @@ def _draw_more(seed):
     hidden, inter = 256 * int(r.integers(1, 49)), 256 * int(r.integers(1, 65))
     while hidden * inter > 20_000_000:
         inter = max(256, inter // 512 * 256)
-    return deq, pf32, [(gt, dt, hidden, inter)]
+    # a GEMV whose weight and x start off 16-byte alignment (byte-granular
+    # kernels), and logits with the maximum planted at 1-3 places
+    t = FMTS[int(r.integers(0, 5))]
+    inner = BLOCK[t] * int(r.integers(1, 34816 // BLOCK[t] + 1))
+    outer = max(1, min(int(r.integers(1, 9000)), 8_000_000 // inner))
+    unal = [(t, outer, inner, int(r.choice([2, 4, 8, 12])), int(r.choice([0, 1, 2, 3])))]
+    am = [(int(r.integers(4, 3_000_000)), int(r.integers(1, 4)), bool(r.integers(0, 2)))]
+    return deq, pf32, [(gt, dt, hidden, inter)], unal, am
 
 
 GEMV, PREFILL, LM, FFN = [], [], [], []
-DEQ, PF32, BLOCKS = [], [], []
+DEQ, PF32, BLOCKS, UNALIGNED, ARGMAX = [], [], [], [], []
 for _s in SEEDS:
     for _acc, _cases in zip((GEMV, PREFILL, LM, FFN), _draw(_s)):
         _acc.extend(c for c in _cases if c not in _acc)
-    for _acc, _cases in zip((DEQ, PF32, BLOCKS), _draw_more(_s)):
+    for _acc, _cases in zip((DEQ, PF32, BLOCKS, UNALIGNED, ARGMAX), _draw_more(_s)):
         _acc.extend(c for c in _cases if c not in _acc)
 
 
@@ -253,3 +264,35 @@ def test_random_ffn_block(gt, dt, hidden, inter):
     D.ffn_block(_dw(wg, gt, hidden, inter), _dw(wu, gt, hidden, inter), _dw(wd, dt, inter, hidden),
                 torch.from_numpy(nw).cuda(), eps, xd, h=h)
     TB._check_block(xd.cpu().numpy(), h[:inter].cpu().numpy(), x, case, gt, dt, hidden, inter, eps)
+
+
+@pytest.mark.parametrize("t,outer,inner,woff,xoff", UNALIGNED)
+def test_random_gemv_unaligned_pointers(t, outer, inner, woff, xoff):
+    from inferno_hip import device as D
+    say(f"gemv type {t} {outer}x{inner}, weight at +{woff} bytes, x at +{4 * xoff} bytes")
+    rng = synth.rng_for(0x6600 + outer + inner + t)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner)
+    wb = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    wb[woff:woff + w.size] = torch.from_numpy(w).cuda()
+    xb = torch.zeros(inner + 4, device="cuda")
+    xb[xoff:xoff + inner] = torch.from_numpy(x).cuda()
+    y = D.gemv(D.DeviceWeight(wb[woff:woff + w.size], t, inner, outer), xb[xoff:xoff + inner]).cpu().numpy()
+    ref = oracle.gemv_f64(t, w, x, inner, outer)
+    tol = oracle.tolerance(oracle.row_norms(t, w, inner, outer), x)
+    assert np.all(np.isfinite(y))
+    assert np.all(np.abs(y.astype(np.float64) - ref) <= tol)
+
+
+@pytest.mark.parametrize("n,ties,neg_prefix", ARGMAX)
+def test_random_argmax_first_of_tied_maxima(n, ties, neg_prefix):
+    from inferno_hip import device as D
+    say(f"argmax n={n} maximum at {ties} places, -inf prefix {neg_prefix}")
+    r = np.random.default_rng(n)
+    lg = r.standard_normal(n).astype(np.float32)
+    lg[np.sort(r.choice(n, size=ties, replace=False))] = np.float32(lg.max() + 1.0)
+    if neg_prefix:
+        lg[: int(r.integers(0, n))] = -np.inf
+    ws = D.ArgmaxWorkspace()
+    D.argmax(torch.from_numpy(lg).cuda(), ws)
+    assert ws.result() == oracle.argmax(lg)[0]
