@@ -112,6 +112,7 @@ export quant_kernels_available
 export q4_k_gemv!, q5_k_gemv!, q6_k_gemv!, q8_0_gemv!
 export quantize_q8_k!, vec_dot_q4_k_q8_k, vec_dot_q5_k_q8_k, vec_dot_q6_k_q8_k
 export q4_k_gemv_q8k!, q5_k_gemv_q8k!, q6_k_gemv_q8k!, EXACT_C_NUMERICS
+export q4_k_gemm!
 
 import ..InfernoHIP: LIBIHIP, check, require, available
 
@@ -234,6 +235,31 @@ function q8_0_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
 end
 
 """
+    q4_k_gemm!(Y, weight_data, X, inner_dim, outer_dim)
+
+The prefill's per-token loop (src/ModelCPU.jl:1001-1017: `q4_k_gemv!` of every
+token column) as one batched product on the matrix cores:
+`Y[:, t] = W X[:, t]` for the `T = size(X, 2)` token columns.  Julia's
+column-major `X` (inner_dim x T) and `Y` (outer_dim x T) are the library's
+row-major T x inner and T x outer.  Within 1e-4 ||w_row|| ||x_t|| of the
+exact sum for any finite X (ihip_prefill_q4_k); the weight is uploaded on
+first use and cached, like `q4_k_gemv!`'s.
+"""
+function q4_k_gemm!(Y::Matrix{Float32}, weight_data::Vector{UInt8}, X::Matrix{Float32},
+                    inner_dim::Int, outer_dim::Int)
+    require()
+    T = size(X, 2)
+    T > 0 || throw(ArgumentError("X has no token columns"))
+    size(X, 1) == inner_dim || throw(DimensionMismatch("X has $(size(X, 1)) rows, inner_dim is $inner_dim"))
+    size(Y) == (outer_dim, T) || throw(DimensionMismatch("Y must be $outer_dim x $T"))
+    check_dims(view(Y, :, 1), weight_data, view(X, :, 1), inner_dim, outer_dim, 256, 144)
+    check(ccall((:ihip_prefill_q4_k, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Cint),
+                weight_data, X, Y, T, inner_dim, outer_dim))
+    return Y
+end
+
+"""
     quantize_q8_k!(q8_buf, x, inner_dim)
 
 src/QuantizedKernels.jl:153-158 with the reference's argument order, passed to
@@ -329,6 +355,7 @@ module FusedKernels
 # the decode path) and the fused decode calls of a device-resident forward.
 export fused_mlp_gate_mul!, fused_silu_gate_mul!, gpu_argmax!
 export ffn_swiglu!, ffn_block!, lm_head_argmax!
+export prefill_scratch_bytes, prefill_q4_k!, prefill_q4_k_f32!
 
 import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
 
@@ -447,6 +474,57 @@ function lm_head_argmax!(logits::Union{Nothing,AbstractVector{Float32}}, w_type:
                  Ptr{Cvoid}, Ptr{Cvoid}),
                 w_type, w, x, lp, token_ptr(ws), flags_ptr(ws), hidden, vocab, ws.ptr, stream))
     return read_token(ws, stream)
+end
+
+"""
+    prefill_scratch_bytes(T, inner) -> Int
+
+Bytes of device scratch `prefill_q4_k!` takes for T tokens of `inner`
+columns (the rounded activations, one scale per token, the partial sums of a
+split over K); independent of the weight's row count.
+"""
+prefill_scratch_bytes(T::Integer, inner::Integer) =
+    Int(ccall((:ihip_prefill_scratch_bytes, LIBIHIP), Csize_t, (Cint, Cint), T, inner))
+
+"""
+    prefill_q4_k!(Y, w, X, xh, T, inner, outer; stream)
+
+The prefill's per-token loop (src/ModelCPU.jl:1001-1017) on device memory:
+`Y[:, t] = W X[:, t]` for T token columns (X: inner x T, Y: outer x T,
+column-major), W a device Q4_K weight pointer.  Rows of more than 512 columns
+multiply fp16 operands (each token column scaled by a power of two first):
+any finite X, every dequantized weight below 65504 in magnitude.  `xh` is
+scratch of `prefill_scratch_bytes(T, inner)` bytes; calls sharing it must not
+overlap on the GPU.  Pointers 16-byte aligned.
+"""
+function prefill_q4_k!(Y::AbstractMatrix{Float32}, w::Ptr{Cvoid}, X::AbstractMatrix{Float32},
+                       xh::Ptr{Cvoid}, T::Integer, inner::Integer, outer::Integer;
+                       stream::Ptr{Cvoid} = C_NULL)
+    require()
+    size(X, 1) == inner && size(X, 2) >= T && size(Y, 1) == outer && size(Y, 2) >= T ||
+        throw(DimensionMismatch("X must be $inner x $T and Y $outer x $T"))
+    check(ccall((:ihip_prefill_q4_k_dev, LIBIHIP), Cint,
+                (Ptr{Cvoid}, Ptr{Float32}, Ptr{Cvoid}, Ptr{Float32}, Cint, Cint, Cint, Ptr{Cvoid}),
+                w, X, xh, Y, T, inner, outer, stream))
+    return Y
+end
+
+"""
+    prefill_q4_k_f32!(Y, w, X, T, inner, outer; stream)
+
+`prefill_q4_k!` on fp32 operands at every row length (no scratch): within
+1e-4 ||w_row|| ||x_t|| for any finite X and any weight, several times slower
+on long rows.
+"""
+function prefill_q4_k_f32!(Y::AbstractMatrix{Float32}, w::Ptr{Cvoid}, X::AbstractMatrix{Float32},
+                           T::Integer, inner::Integer, outer::Integer; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    size(X, 1) == inner && size(X, 2) >= T && size(Y, 1) == outer && size(Y, 2) >= T ||
+        throw(DimensionMismatch("X must be $inner x $T and Y $outer x $T"))
+    check(ccall((:ihip_prefill_q4_k_f32_dev, LIBIHIP), Cint,
+                (Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Cint, Ptr{Cvoid}),
+                w, X, Y, T, inner, outer, stream))
+    return Y
 end
 
 end # module FusedKernels

@@ -16,11 +16,18 @@ HEADER = ROOT / "include" / "inferno_hip.h"
 
 
 def header_arity():
+    return {k: v[1] for k, v in header_decls().items()}
+
+
+def header_decls():
+    """ihip_* name -> (Julia return type, parameter count) from the header."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    jl = {"int": "Cint", "size_t": "Csize_t", "const char *": "Cstring"}
     out = {}
-    for m in re.finditer(r"\b(ihip_\w+)\s*\(([^;{]*?)\)\s*;", text, re.S):
-        params = m.group(2).strip()
-        out[m.group(1)] = 0 if params in ("", "void") else len(_split(params))
+    for m in re.finditer(r"^([A-Za-z_][\w ]*?\s*\**)\s*\b(ihip_\w+)\s*\(([^;{]*?)\)\s*;", text, re.S | re.M):
+        params = m.group(3).strip()
+        ret = re.sub(r"\s+", " ", m.group(1).strip()).replace(" *", " *")
+        out[m.group(2)] = (jl.get(ret, ret), 0 if params in ("", "void") else len(_split(params)))
     return out
 
 
@@ -71,15 +78,14 @@ def ccalls(lib="LIBIHIP"):
 
 
 def test_every_library_ccall_matches_the_header():
-    arity = header_arity()
+    decls = header_decls()
     calls = [c for c in ccalls() if c[1] == "LIBIHIP"]
     assert len(calls) >= 15
     for sym, _, ret, types, args in calls:
-        assert sym in arity, f"{sym} is not declared in include/inferno_hip.h"
-        assert len(types) == arity[sym], f"{sym}: {len(types)} argument types, header has {arity[sym]}"
+        assert sym in decls, f"{sym} is not declared in include/inferno_hip.h"
+        want, n = decls[sym]
+        assert len(types) == n, f"{sym}: {len(types)} argument types, header has {n}"
         assert len(args) == len(types), f"{sym}: {len(args)} arguments for {len(types)} types"
-        want = "Csize_t" if sym == "ihip_ffn_block_scratch_floats" else \
-            "Cstring" if sym == "ihip_last_error" else "Cint"
         assert ret == want, f"{sym} returns {ret}, the header says {want}"
 
 
