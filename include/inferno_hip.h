@@ -125,9 +125,9 @@ int ihip_iq4_nl_gemv(const uint8_t *weight, const float *x, float *out, int inne
 /* ---- GGUF files feeding the weight registry ------------------------------
  * read_gguf (src/GGUF.jl:119-165) and the keep-quantized load
  * (src/LoaderCPU.jl:125-163): the file is memory-mapped and parsed (no GPU
- * needed); tensors are listed by index; a Q4_K/Q5_K/Q6_K/Q8_0 tensor uploads
- * into the registry (inner = ne0, outer = ne1) for ihip_weight_device_ptr and
- * the *_dev entry points. */
+ * needed); tensors are listed by index (from 0); a Q4_K, Q5_K, Q6_K, Q8_0 or
+ * IQ4_NL tensor uploads into the registry (inner = ne0, outer = ne1) for
+ * ihip_weight_device_ptr and the *_dev entry points. */
 int ihip_gguf_open(const char *path, uint64_t *file_handle);
 int ihip_gguf_close(uint64_t file_handle);
 int ihip_gguf_info(uint64_t file_handle, uint32_t *version, uint64_t *alignment,

@@ -17,7 +17,16 @@ meaning, so a caller switches by changing what it `using`s:
   `fused_mlp_gate_mul!`, `fused_silu_gate_mul!`, `gpu_argmax!` on DEVICE
   vectors (AMDGPU.jl `ROCArray`s or anything `pointer` maps to device
   memory), plus the fused decode calls the GPU forward makes
-  (`ffn_swiglu!`, `ffn_block!`, `lm_head_argmax!`).
+  (`ffn_swiglu!`, `ffn_block!`, `lm_head_argmax!`) and the batched prefill
+  (`prefill_q4_k!`, `prefill_q4_k_f32!`).
+
+Beyond the reference's three modules, `QuantizedKernels` also has
+`iq4_nl_gemv!` and the batched prefill `q4_k_gemm!` on host arrays;
+`InfernoHIP.Device` has the unfused device calls of a device-resident forward
+(`gemv!`, `dequantize!`, `rmsnorm!`, `gate_up_swiglu!`,
+`lm_head_argmax_norm!`); `InfernoHIP.GGUF` loads GGUF tensors straight into
+device memory (`open_gguf`, `tensor_count`, `tensor_info`, `upload`,
+`release`, `close_gguf`).
 
 Errors: every library call returns a status; a non-zero status becomes an
 `ArgumentError` for bad arguments and NaN/+Inf/empty logits (the reference's
@@ -112,7 +121,7 @@ export quant_kernels_available
 export q4_k_gemv!, q5_k_gemv!, q6_k_gemv!, q8_0_gemv!
 export quantize_q8_k!, vec_dot_q4_k_q8_k, vec_dot_q5_k_q8_k, vec_dot_q6_k_q8_k
 export q4_k_gemv_q8k!, q5_k_gemv_q8k!, q6_k_gemv_q8k!, EXACT_C_NUMERICS
-export q4_k_gemm!
+export q4_k_gemm!, iq4_nl_gemv!
 
 import ..InfernoHIP: LIBIHIP, check, require, available
 
@@ -229,6 +238,23 @@ function q8_0_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
     require()
     check_dims(out, weight_data, x, inner_dim, outer_dim, 32, 34)
     check(ccall((:ihip_q8_0_gemv, LIBIHIP), Cint,
+                (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Cint, Cint),
+                weight_data, x, out, inner_dim, outer_dim))
+    return out
+end
+
+"""
+    iq4_nl_gemv!(out, weight_data, x, inner_dim, outer_dim)
+
+mul_quant_mat_vec(::IQ4NL_Matrix) (src/ModelCPU.jl:381-408) on the GPU: 18-byte
+blocks of 32 (fp16 d, 16 bytes of 4-bit indices into the IQ4_NL grid), fp32 x,
+within 1e-4 ||w_row|| ||x|| of the exact sum.
+"""
+function iq4_nl_gemv!(out::Vector{Float32}, weight_data::Vector{UInt8},
+                      x::Vector{Float32}, inner_dim::Int, outer_dim::Int)
+    require()
+    check_dims(out, weight_data, x, inner_dim, outer_dim, 32, 18)
+    check(ccall((:ihip_iq4_nl_gemv, LIBIHIP), Cint,
                 (Ptr{UInt8}, Ptr{Float32}, Ptr{Float32}, Cint, Cint),
                 weight_data, x, out, inner_dim, outer_dim))
     return out
@@ -528,5 +554,176 @@ function prefill_q4_k_f32!(Y::AbstractMatrix{Float32}, w::Ptr{Cvoid}, X::Abstrac
 end
 
 end # module FusedKernels
+
+# ============================================================================
+module Device
+# The unfused device calls of a device-resident forward (the role
+# src/Qwen35GPU.jl plays for oneAPI): mul_quant_mat_vec, dequantization,
+# rmsnorm_cpu!, the gate/up pair and the final norm + lm_head on device
+# vectors, asynchronous on `stream` (a hipStream_t).  Weights are device
+# pointers to GGML blocks (e.g. `GGUF.upload`).
+export gemv!, dequantize!, rmsnorm!, gate_up_swiglu!, lm_head_argmax_norm!
+
+import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
+
+"""
+    gemv!(out, w_type, w, x, inner, outer; stream)
+
+mul_quant_mat_vec (src/ModelCPU.jl:285-408) on device memory for GGML type
+`w_type` (Q4_K, Q5_K, Q6_K, Q8_0, IQ4_NL): `out = W x`, within
+1e-4 ||w_row|| ||x|| of the exact sum.
+"""
+function gemv!(out::AbstractVector{Float32}, w_type::Integer, w::Ptr{Cvoid},
+               x::AbstractVector{Float32}, inner::Integer, outer::Integer; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    length(out) >= outer && length(x) >= inner || throw(DimensionMismatch("x or out too short"))
+    check(ccall((:ihip_gemv_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
+                w_type, w, x, out, inner, outer, stream))
+    return out
+end
+
+"""
+    dequantize!(dst, w_type, src, n; stream)
+
+The Dequant.jl routines (src/Dequant.jl:304-693) on device memory: n weights
+of GGML type `w_type` to fp32, bit-exact.
+"""
+function dequantize!(dst::AbstractVector{Float32}, w_type::Integer, src::Ptr{Cvoid}, n::Integer;
+                     stream::Ptr{Cvoid} = C_NULL)
+    require()
+    length(dst) >= n || throw(DimensionMismatch("dst holds fewer than $n floats"))
+    check(ccall((:ihip_dequantize_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Ptr{Float32}, Int64, Ptr{Cvoid}), w_type, src, dst, n, stream))
+    return dst
+end
+
+"""
+    rmsnorm!(out, x, w, eps; stream)
+
+rmsnorm_cpu! (src/ModelCPU.jl:111-123): `out = x * (1/sqrt(mean(x^2) + eps)) .* w`
+(out may be x).
+"""
+function rmsnorm!(out::AbstractVector{Float32}, x::AbstractVector{Float32},
+                  w::AbstractVector{Float32}, eps::Real; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    n = length(x)
+    length(out) >= n && length(w) >= n || throw(DimensionMismatch("out or w too short"))
+    check(ccall((:ihip_rmsnorm_dev, LIBIHIP), Cint,
+                (Ptr{Float32}, Ptr{Float32}, Cfloat, Ptr{Float32}, Cint, Ptr{Cvoid}),
+                x, w, Float32(eps), out, n, stream))
+    return out
+end
+
+"""
+    gate_up_swiglu!(h, gate_type, wg, up_type, wu, x, hidden, inter; stream)
+
+The first half of mlp_forward (src/ModelCPU.jl:482-505):
+`h = silu(Wg x) .* (Wu x)`, one pass over both weights for a matching
+16-byte aligned Q4_K or Q5_K pair.
+"""
+function gate_up_swiglu!(h::AbstractVector{Float32}, gate_type::Integer, wg::Ptr{Cvoid},
+                         up_type::Integer, wu::Ptr{Cvoid}, x::AbstractVector{Float32},
+                         hidden::Integer, inter::Integer; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    length(h) >= inter && length(x) >= hidden || throw(DimensionMismatch("x or h too short"))
+    check(ccall((:ihip_gate_up_swiglu_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
+                gate_type, wg, up_type, wu, x, h, hidden, inter, stream))
+    return h
+end
+
+"""
+    lm_head_argmax_norm!(xn, logits, w_type, w, norm_w, eps, x, hidden, vocab; ws, stream) -> Int
+
+The last step of the forward (src/ModelCPU.jl:1014-1015, src/CommonOps.jl:142-163):
+`xn = rmsnorm(x) .* norm_w`, then the lm_head and the greedy token, 1-based.
+`logits` may be `nothing` where the argmax is fused into the GEMV.
+"""
+function lm_head_argmax_norm!(xn::AbstractVector{Float32}, logits::Union{Nothing,AbstractVector{Float32}},
+                              w_type::Integer, w::Ptr{Cvoid}, norm_w::AbstractVector{Float32},
+                              eps::Real, x::AbstractVector{Float32}, hidden::Integer, vocab::Integer;
+                              ws::ArgmaxWorkspace = ArgmaxWorkspace(), stream::Ptr{Cvoid} = C_NULL)
+    require()
+    lp = logits === nothing ? Ptr{Float32}(C_NULL) : Base.unsafe_convert(Ptr{Float32}, logits)
+    check(ccall((:ihip_lm_head_argmax_norm_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Ptr{Float32}, Cfloat, Ptr{Float32}, Ptr{Float32}, Ptr{Float32},
+                 Ptr{Int32}, Ptr{UInt32}, Cint, Cint, Ptr{Cvoid}, Ptr{Cvoid}),
+                w_type, w, norm_w, Float32(eps), x, xn, lp, token_ptr(ws), flags_ptr(ws), hidden,
+                vocab, ws.ptr, stream))
+    return read_token(ws, stream)
+end
+
+end # module Device
+
+# ============================================================================
+module GGUF
+# read_gguf (src/GGUF.jl:119-165) and the keep-quantized load
+# (src/LoaderCPU.jl:125-163) straight into device memory: the file is
+# memory-mapped and parsed by the library, and each quantized tensor is
+# uploaded once into the weight registry.
+export open_gguf, close_gguf, tensor_count, tensor_info, upload, release
+
+import ..InfernoHIP: LIBIHIP, check
+
+"""`open_gguf(path) -> UInt64`: parse the header and tensor table (no GPU needed)."""
+function open_gguf(path::AbstractString)
+    fh = Ref{UInt64}(0)
+    check(ccall((:ihip_gguf_open, LIBIHIP), Cint, (Cstring, Ref{UInt64}), path, fh))
+    return fh[]
+end
+
+close_gguf(fh::UInt64) = check(ccall((:ihip_gguf_close, LIBIHIP), Cint, (UInt64,), fh))
+
+"""`tensor_count(fh) -> Int`, from the header (src/GGUF.jl:125-130)."""
+function tensor_count(fh::UInt64)
+    version = Ref{UInt32}(0)
+    alignment = Ref{UInt64}(0)
+    data_offset = Ref{UInt64}(0)
+    n = Ref{Int64}(0)
+    check(ccall((:ihip_gguf_info, LIBIHIP), Cint,
+                (UInt64, Ref{UInt32}, Ref{UInt64}, Ref{UInt64}, Ref{Int64}),
+                fh, version, alignment, data_offset, n))
+    return Int(n[])
+end
+
+"""
+    tensor_info(fh, i) -> (name, ggml_type, dims, offset, nbytes)
+
+Tensor `i` (1-based) of the table: dims with ne0 first, the offset relative
+to the data section, and the byte count its type's blocks take.
+"""
+function tensor_info(fh::UInt64, i::Integer)
+    name = Vector{UInt8}(undef, 1024)
+    t = Ref{Cint}(0)
+    nd = Ref{Cint}(0)
+    dims = zeros(Int64, 4)
+    off = Ref{UInt64}(0)
+    nb = Ref{UInt64}(0)
+    check(ccall((:ihip_gguf_tensor_info, LIBIHIP), Cint,
+                (UInt64, Int64, Ptr{UInt8}, Csize_t, Ref{Cint}, Ref{Cint}, Ptr{Int64}, Ref{UInt64},
+                 Ref{UInt64}),
+                fh, i - 1, name, length(name), t, nd, dims, off, nb))
+    s = unsafe_string(pointer(name))
+    return s, Int(t[]), dims[1:nd[]], off[], nb[]
+end
+
+"""
+    upload(fh, name) -> (handle, device_pointer)
+
+Upload a Q4_K / Q5_K / Q6_K / Q8_0 / IQ4_NL tensor into the registry; the
+pointer feeds the `Device` and `FusedKernels` calls until `release(handle)`.
+"""
+function upload(fh::UInt64, name::AbstractString)
+    h = Ref{UInt64}(0)
+    check(ccall((:ihip_gguf_upload, LIBIHIP), Cint, (UInt64, Cstring, Ref{UInt64}), fh, name, h))
+    p = Ref{Ptr{Cvoid}}(C_NULL)
+    check(ccall((:ihip_weight_device_ptr, LIBIHIP), Cint, (UInt64, Ref{Ptr{Cvoid}}), h[], p))
+    return h[], p[]
+end
+
+release(h::UInt64) = check(ccall((:ihip_weight_release, LIBIHIP), Cint, (UInt64,), h))
+
+end # module GGUF
 
 end # module InfernoHIP

@@ -97,7 +97,7 @@ def test_hip_runtime_calls_are_the_documented_ones():
 def test_modules_export_the_reference_names():
     text = JL.read_text()
     mods = {}
-    for name in ("QuantizedKernels", "Dequant", "FusedKernels"):
+    for name in ("QuantizedKernels", "Dequant", "FusedKernels", "Device", "GGUF"):
         m = re.search(r"^module " + name + r"\n(.*?)^end # module " + name, text, re.S | re.M)
         assert m, name
         mods[name] = m.group(1)
