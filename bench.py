@@ -437,9 +437,24 @@ def prefill(torch, stream, synth, D):
     us, us_graph, us_stream = both_ways_us(torch, stream, lambda i: D.prefill_q4_k(dw, Xd, Y, xh),
                                            10, 5, 4)
     flops = 2.0 * T * outer * inner
+    # three weights on one input (the attention's wq, wk, wv,
+    # src/ModelCPU.jl:789-791): one rounding of X, three products
+    dws = [dw] + [D.DeviceWeight(dw.data.clone(), synth.Q4_K, inner, outer) for _ in range(2)]
+    Ys = [Y] + [torch.empty_like(Y) for _ in range(2)]
+
+    def shared(i):
+        D.prefill_convert(Xd, xh)
+        for k in range(3):
+            D.prefill_q4_k_xh(dws[k], xh, T, Ys[k])
+
+    def separate(i):
+        for k in range(3):
+            D.prefill_q4_k(dws[k], Xd, Ys[k], xh)
+    us3_shared = both_ways_us(torch, stream, shared, 4, 5, 2)[0]
+    us3_separate = both_ways_us(torch, stream, separate, 4, 5, 2)[0]
     return dict(us=us, tflops=flops / (us * 1e-6) / 1e12,
                 mfma_frac=flops / (us * 1e-6) / 1e12 / PEAK_FP16_TFLOPS, graph_us=us_graph,
-                stream_us=us_stream)
+                stream_us=us_stream, shared3_us=us3_shared, separate3_us=us3_separate)
 
 
 def write_gguf(path, tensors, alignment=32):
@@ -862,8 +877,12 @@ def main():
         log("prefill 512x4096x4096")
         p = prefill(torch, stream, synth, D)
         log(f"  {p['us']:.1f} us, {p['tflops']:.1f} TFLOP/s (graph {p['graph_us']:.2f}, stream {p['stream_us']:.2f})")
+        log(f"  three weights on one X: {p['shared3_us']:.1f} us with one rounding, "
+            f"{p['separate3_us']:.1f} us as three calls")
         extras.update(prefill_us=p["us"], prefill_tflops=p["tflops"], prefill_mfma_frac=p["mfma_frac"],
-                      prefill_graph_us=p["graph_us"], prefill_stream_us=p["stream_us"])
+                      prefill_graph_us=p["graph_us"], prefill_stream_us=p["stream_us"],
+                      prefill_3_weights_shared_x_us=p["shared3_us"],
+                      prefill_3_weights_separate_us=p["separate3_us"])
 
     cpu = None
     if not args.no_cpu:

@@ -265,6 +265,21 @@ int ihip_fused_silu_gate_mul_dev(float *out, const float *x, const float *gate, 
 int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int T,
                           int inner, int outer, ihip_stream stream);
 size_t ihip_prefill_scratch_bytes(int T, int inner);
+/* ihip_prefill_q4_k_dev in two halves, for weights that multiply the same
+ * activations: the attention's wq, wk and wv (src/ModelCPU.jl:789-791), the
+ * MLP's gate and up (:490, 498), the SSM's in and gate projections
+ * (:570-571).  ihip_prefill_convert_dev rounds X into xh (as
+ * ihip_prefill_q4_k_dev does); each ihip_prefill_q4_k_xh_dev then multiplies
+ * one weight by the rounded rows, with outputs bit-identical to
+ * ihip_prefill_q4_k_dev's for that weight.  The product reuses xh's
+ * partial-sum area and leaves the rounded rows as they were, so any number
+ * of products (same T and inner) may follow one conversion; none of them may
+ * overlap another call that uses xh on the GPU.  Rows of at most 512 columns
+ * are IHIP_ERR_INVALID here: ihip_prefill_q4_k_dev multiplies them on fp32
+ * operands straight from X. */
+int ihip_prefill_convert_dev(const float *X, void *xh, int T, int inner, ihip_stream stream);
+int ihip_prefill_q4_k_xh_dev(const void *w, void *xh, float *Y, int T, int inner, int outer,
+                             ihip_stream stream);
 /* The per-token prefill loop (src/ModelCPU.jl:1001-1017 over
  * mul_quant_mat_vec, :285-307) on fp32 operands: the weights dequantized to
  * fp32 exactly and X as given, multiplied on the fp32 matrix cores.  The

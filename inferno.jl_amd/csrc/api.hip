@@ -1108,6 +1108,53 @@ int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int
     return IHIP_OK;
 }
 
+int ihip_prefill_convert_dev(const float *X, void *xh, int T, int inner, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(kQ4_K, inner, 1));
+    if (T <= 0)
+        return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if (inner <= kPrefillF32MaxK)
+        return fail(IHIP_ERR_INVALID, "rows of at most %d columns are multiplied on fp32 operands "
+                    "straight from X: call ihip_prefill_q4_k_dev", kPrefillF32MaxK);
+    if (!prefill_fits(T, inner, 1))
+        return fail(IHIP_ERR_INVALID, "T*inner*2 must stay below 4 GiB");
+    if (!X || !xh)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (!al16(X) || !al16(xh))
+        return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    hipError_t e = launch_prefill_convert(X, xh, T, inner, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "prefill conversion launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
+int ihip_prefill_q4_k_xh_dev(const void *w, void *xh, float *Y, int T, int inner, int outer,
+                             ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(kQ4_K, inner, outer));
+    if (T <= 0)
+        return fail(IHIP_ERR_INVALID, "T=%d must be positive", T);
+    if (inner <= kPrefillF32MaxK)
+        return fail(IHIP_ERR_INVALID, "rows of at most %d columns are multiplied on fp32 operands "
+                    "straight from X: call ihip_prefill_q4_k_dev", kPrefillF32MaxK);
+    if (!prefill_fits(T, inner, outer))
+        return fail(IHIP_ERR_INVALID, "prefill operands must stay below 4 GiB (T*inner*2 and W bytes) and T*outer below 2^31");
+    if (!w || !xh || !Y)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (!al16(w) || !al16(xh) || !al16(Y))
+        return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    hipError_t e = launch_prefill_gemm(w, xh, Y, T, inner, outer, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
+    return IHIP_OK;
+}
+
 int ihip_prefill_q4_k_f32_dev(const void *w, const float *X, float *Y, int T, int inner,
                               int outer, ihip_stream stream)
 {

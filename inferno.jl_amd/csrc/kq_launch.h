@@ -153,6 +153,13 @@ inline int prefill_splits(int T, int inner, int outer, int ncu)
 }
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s);
+// Its two halves for rows of more than kPrefillF32MaxK columns: X rounded into
+// xh (fp16 rows and one scale exponent per token), then the product from xh
+// (which also takes the partial sums of a split over K, leaving the rounded
+// rows as they were), so several weights can share one rounding.
+hipError_t launch_prefill_convert(const float *X, void *xh, int T, int inner, hipStream_t s);
+hipError_t launch_prefill_gemm(const void *w, void *xh, float *Y, int T, int inner, int outer,
+                               hipStream_t s);
 // The same product on fp32 operands (k_prefill_q4k_f32), any inner; needs
 // T * outer <= INT32_MAX.
 hipError_t launch_prefill_q4k_f32(const void *w, const float *X, float *Y, int T, int inner,

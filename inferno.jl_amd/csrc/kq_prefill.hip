@@ -693,6 +693,15 @@ hipError_t launch_prefill_q4k_f32(const void *w, const float *X, float *Y, int T
     return hipGetLastError();
 }
 
+hipError_t launch_prefill_convert(const float *X, void *xh, int T, int inner, hipStream_t s)
+{
+    if (T <= 0 || inner <= 0 || inner % 256)
+        return hipErrorInvalidValue;
+    int *xs = reinterpret_cast<int *>(static_cast<uint8_t *>(xh) + prefill_scale_offset(T, inner));
+    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)T), dim3(256), 0, s, X, (_Float16 *)xh, xs, inner);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y, int T,
                               int inner, int outer, hipStream_t s)
 {
@@ -700,9 +709,19 @@ hipError_t launch_prefill_q4k(const void *w, const float *X, void *xh, float *Y,
         return hipErrorInvalidValue;
     if (inner <= kPrefillF32MaxK)
         return launch_prefill_q4k_f32(w, X, Y, T, inner, outer, s);
+    const hipError_t e = launch_prefill_convert(X, xh, T, inner, s);
+    if (e != hipSuccess)
+        return e;
+    return launch_prefill_gemm(w, xh, Y, T, inner, outer, s);
+}
+
+hipError_t launch_prefill_gemm(const void *w, void *xh, float *Y, int T, int inner, int outer,
+                               hipStream_t s)
+{
+    if (T <= 0 || inner <= kPrefillF32MaxK || inner % 256 || !prefill_fits(T, inner, outer))
+        return hipErrorInvalidValue;
     int *xs = reinterpret_cast<int *>(static_cast<uint8_t *>(xh) + prefill_scale_offset(T, inner));
     float *P = reinterpret_cast<float *>(static_cast<uint8_t *>(xh) + prefill_part_offset(T, inner));
-    hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)T), dim3(256), 0, s, X, (_Float16 *)xh, xs, inner);
     const int mtiles = (T + PF_BM - 1) / PF_BM, ntiles = (outer + PF_BN - 1) / PF_BN;
     const int nsplit = prefill_splits(T, inner, outer, device_cus());
     const dim3 grid(prefill_grid(mtiles * ntiles, nsplit));

@@ -104,6 +104,8 @@ SIGNATURES = {
     "ihip_prefill_q4_k_dev": ([_vp, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "ihip_prefill_scratch_bytes": ([_i, _i], _sz),
     "ihip_prefill_q4_k_f32_dev": ([_vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "ihip_prefill_convert_dev": ([_vp, _vp, _i, _i, _vp], _i),
+    "ihip_prefill_q4_k_xh_dev": ([_vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "ihip_quantize_row_q8_k_dev": ([_vp, _vp, _i64, _vp], _i),
     "ihip_gemv_q8k_dev": ([_i, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_gemv_q8k_x_dev": ([_i, _vp, _vp, _vp, _vp, _i, _i, _vp], _i),

@@ -164,6 +164,32 @@ def prefill_q4_k(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, xh: t
     return Y
 
 
+def prefill_convert(X: torch.Tensor, xh: torch.Tensor = None, stream=None) -> torch.Tensor:
+    """The rounding half of prefill_q4_k (ihip_prefill_convert_dev): X (T x
+    inner, inner > 512) into xh, which prefill_q4_k_xh then multiplies by any
+    number of weights."""
+    T, inner = X.shape
+    if xh is None:
+        xh = prefill_scratch(T, inner, device=X.device)
+    check(lib().ihip_prefill_convert_dev(_ptr(X, torch.float32, "X"), _ptr(xh, torch.uint8, "xh"),
+                                         T, inner, _stream(stream)))
+    return xh
+
+
+def prefill_q4_k_xh(w: DeviceWeight, xh: torch.Tensor, T: int, Y: torch.Tensor = None,
+                    stream=None) -> torch.Tensor:
+    """The product half (ihip_prefill_q4_k_xh_dev): Y = W X from rows that
+    prefill_convert rounded into xh; bit-identical to prefill_q4_k."""
+    if w.ggml_type != Q4_K:
+        raise IHIPArgumentError(_lib.IHIP_ERR_INVALID, "prefill takes a Q4_K weight")
+    if Y is None:
+        Y = torch.empty(T, w.outer, dtype=torch.float32, device=xh.device)
+    check(lib().ihip_prefill_q4_k_xh_dev(_ptr(w.data), _ptr(xh, torch.uint8, "xh"),
+                                         _ptr(Y, torch.float32, "Y"), T, w.inner, w.outer,
+                                         _stream(stream)))
+    return Y
+
+
 def prefill_q4_k_f32(w: DeviceWeight, X: torch.Tensor, Y: torch.Tensor = None, stream=None):
     """The prefill on fp32 operands (ihip_prefill_q4_k_f32_dev): within the row
     bound for any finite X, slower than prefill_q4_k on long rows."""

@@ -18,7 +18,8 @@ meaning, so a caller switches by changing what it `using`s:
   vectors (AMDGPU.jl `ROCArray`s or anything `pointer` maps to device
   memory), plus the fused decode calls the GPU forward makes
   (`ffn_swiglu!`, `ffn_block!`, `lm_head_argmax!`) and the batched prefill
-  (`prefill_q4_k!`, `prefill_q4_k_f32!`).
+  (`prefill_q4_k!`, `prefill_q4_k_f32!`, and `prefill_convert!` with
+  `prefill_q4_k_xh!` for weights that share an input).
 
 Beyond the reference's three modules, `QuantizedKernels` also has
 `iq4_nl_gemv!` and the batched prefill `q4_k_gemm!` on host arrays;
@@ -381,7 +382,7 @@ module FusedKernels
 # the decode path) and the fused decode calls of a device-resident forward.
 export fused_mlp_gate_mul!, fused_silu_gate_mul!, gpu_argmax!
 export ffn_swiglu!, ffn_block!, lm_head_argmax!
-export prefill_scratch_bytes, prefill_q4_k!, prefill_q4_k_f32!
+export prefill_scratch_bytes, prefill_q4_k!, prefill_q4_k_f32!, prefill_convert!, prefill_q4_k_xh!
 
 import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
 
@@ -532,6 +533,40 @@ function prefill_q4_k!(Y::AbstractMatrix{Float32}, w::Ptr{Cvoid}, X::AbstractMat
     check(ccall((:ihip_prefill_q4_k_dev, LIBIHIP), Cint,
                 (Ptr{Cvoid}, Ptr{Float32}, Ptr{Cvoid}, Ptr{Float32}, Cint, Cint, Cint, Ptr{Cvoid}),
                 w, X, xh, Y, T, inner, outer, stream))
+    return Y
+end
+
+"""
+    prefill_convert!(xh, X, T, inner; stream)
+
+The rounding half of `prefill_q4_k!` (rows of more than 512 columns): X
+(inner x T) into the scratch `xh`, which `prefill_q4_k_xh!` then multiplies by
+every weight that shares this input -- wq, wk and wv
+(src/ModelCPU.jl:789-791), gate and up (:490, 498).
+"""
+function prefill_convert!(xh::Ptr{Cvoid}, X::AbstractMatrix{Float32}, T::Integer, inner::Integer;
+                          stream::Ptr{Cvoid} = C_NULL)
+    require()
+    size(X, 1) == inner && size(X, 2) >= T || throw(DimensionMismatch("X must be $inner x $T"))
+    check(ccall((:ihip_prefill_convert_dev, LIBIHIP), Cint,
+                (Ptr{Float32}, Ptr{Cvoid}, Cint, Cint, Ptr{Cvoid}), X, xh, T, inner, stream))
+    return xh
+end
+
+"""
+    prefill_q4_k_xh!(Y, w, xh, T, inner, outer; stream)
+
+The product half: `Y[:, t] = W X[:, t]` from the rows `prefill_convert!`
+rounded into `xh`, bit-identical to `prefill_q4_k!`; any number of products
+may follow one conversion.
+"""
+function prefill_q4_k_xh!(Y::AbstractMatrix{Float32}, w::Ptr{Cvoid}, xh::Ptr{Cvoid}, T::Integer,
+                          inner::Integer, outer::Integer; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    size(Y, 1) == outer && size(Y, 2) >= T || throw(DimensionMismatch("Y must be $outer x $T"))
+    check(ccall((:ihip_prefill_q4_k_xh_dev, LIBIHIP), Cint,
+                (Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Float32}, Cint, Cint, Cint, Ptr{Cvoid}),
+                w, xh, Y, T, inner, outer, stream))
     return Y
 end
 

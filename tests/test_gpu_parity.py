@@ -750,6 +750,54 @@ def test_prefill_q4k(T, outer, inner):
         assert float(np.max(ratio32)) < 0.25
 
 
+@pytest.mark.parametrize("inner", [2048, 4096])
+def test_prefill_shared_activations_match_the_one_call_entry_point(inner):
+    """One rounding of X, then products with several weights, as the
+    attention's wq, wk and wv share their input (src/ModelCPU.jl:789-791):
+    each output bit-identical to prefill_q4_k's for that weight, within the
+    row bound of the oracle, and the rounded rows in xh untouched by the
+    products (the 320-row weight splits K and writes partial sums into xh)."""
+    from inferno_hip import device as D
+    T = 300
+    rng = synth.rng_for(0x5E0 + inner)
+    X = rng.standard_normal((T, inner)).astype(np.float32)
+    X[7] *= np.float32(3e5)  # a row past fp16's range: its own scale
+    Xd = dev(X)
+    say(f"prefill shared activations T={T} inner={inner}: rows 4096, 320, 1000")
+    xh = D.prefill_convert(Xd)
+    kept = (2 * T * inner + 15) // 16 * 16 + 4 * T  # rounded rows and per-token scales
+    rounded = xh[:kept].clone()
+    for outer in (4096, 320, 1000):
+        w = synth.weight(rng, synth.Q4_K, outer, inner)
+        dw = dweight(w, synth.Q4_K, inner, outer)
+        Y = D.prefill_q4_k_xh(dw, xh, T).cpu().numpy()
+        want = D.prefill_q4_k(dw, Xd).cpu().numpy()
+        assert np.array_equal(Y.view(np.uint32), want.view(np.uint32)), f"outer {outer}"
+        assert torch.equal(xh[:kept], rounded), f"the product with outer {outer} changed the rounded rows"
+        ref = oracle.gemm_f64(synth.Q4_K, w, X, inner, outer)
+        nrm = oracle.row_norms(synth.Q4_K, w, inner, outer)
+        xn = np.linalg.norm(X.astype(np.float64), axis=1)
+        ratio = np.abs(Y.astype(np.float64) - ref) / (1e-4 * nrm[None, :] * xn[:, None])
+        assert np.all(ratio <= 1.0), f"outer {outer}: max err/tol {float(np.max(ratio)):.3g}"
+
+
+def test_prefill_shared_activations_refuse_short_rows():
+    """Rows of at most 512 columns run on fp32 operands straight from X, so
+    the two halves refuse them."""
+    from inferno_hip import device as D
+    from inferno_hip._lib import IHIPArgumentError
+    say("prefill halves refuse 512-column rows")
+    T, outer, inner = 16, 64, 512
+    rng = synth.rng_for(0x5E9)
+    Xd = dev(rng.standard_normal((T, inner)).astype(np.float32))
+    dw = dweight(synth.weight(rng, synth.Q4_K, outer, inner), synth.Q4_K, inner, outer)
+    xh = D.prefill_scratch(T, inner)
+    with pytest.raises(IHIPArgumentError):
+        D.prefill_convert(Xd, xh)
+    with pytest.raises(IHIPArgumentError):
+        D.prefill_q4_k_xh(dw, xh, T)
+
+
 @pytest.mark.parametrize("scale", [1e5, 1e-6, 1e30, 1e-38])
 def test_prefill_any_finite_activations(scale):
     """Token rows scaled to 1e5 (past fp16's 65504) and to 1e-6 (below its
