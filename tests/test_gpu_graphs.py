@@ -211,6 +211,36 @@ def test_prefill_graph(T, outer, inner, other_work):
     replay_matches_eager(lambda: D.prefill_q4_k(dw, X, Y, xh), [Y], other_work)
 
 
+def test_prefill_shared_rounding_graph(other_work):
+    """One rounding of X, then two products (one of them splitting K)."""
+    from inferno_hip import device as D
+    T, inner = 64, 4096
+    say(f"graph prefill halves T={T} inner={inner}: rows 4096 and 320")
+    rng = synth.rng_for(0x6AB)
+    _, dw1 = dweight(rng, synth.Q4_K, 4096, inner)
+    _, dw2 = dweight(rng, synth.Q4_K, 320, inner)
+    X = dev(rng.standard_normal((T, inner)).astype(np.float32))
+    Y1, Y2 = torch.empty(T, 4096, device="cuda"), torch.empty(T, 320, device="cuda")
+    xh = D.prefill_scratch(T, inner)
+
+    def call():
+        D.prefill_convert(X, xh)
+        D.prefill_q4_k_xh(dw1, xh, T, Y1)
+        D.prefill_q4_k_xh(dw2, xh, T, Y2)
+    replay_matches_eager(call, [Y1, Y2], other_work)
+
+
+def test_prefill_f32_operands_graph(other_work):
+    from inferno_hip import device as D
+    T, outer, inner = 96, 1000, 2048
+    say(f"graph prefill on fp32 operands T={T} {outer}x{inner}")
+    rng = synth.rng_for(0x6AC)
+    _, dw = dweight(rng, synth.Q4_K, outer, inner)
+    X = dev(rng.standard_normal((T, inner)).astype(np.float32))
+    Y = torch.empty(T, outer, device="cuda")
+    replay_matches_eager(lambda: D.prefill_q4_k_f32(dw, X, Y), [Y], other_work)
+
+
 @pytest.mark.parametrize("t", [synth.Q4_K, synth.Q6_K])
 def test_int8_activation_gemv_graph(t, other_work):
     from inferno_hip import device as D
