@@ -390,6 +390,37 @@ def q8k_gemv(torch, stream, synth, D):
     return dict(us=us, gbs=nbytes / (us * 1e-6) / 1e9)
 
 
+def qkv_group(torch, stream, synth, D):
+    """The attention's input projections of one decode step
+    (src/ModelCPU.jl:789-791): Q4_K wq 4096x4096, wk and wv 1024x4096 on one
+    x, as three GEMVs and as one GEMV over the three uploaded back to back
+    (ihip_weight_register_group); 16 rotated copies."""
+    inner, outers = 4096, (4096, 1024, 1024)
+    rng = synth.rng_for(0xC7)
+    ws = [synth.weight(rng, synth.Q4_K, o, inner) for o in outers]
+    x = torch.from_numpy(synth.activations(rng, inner)).cuda()
+    ncopy = 16
+    groups = [D.WeightGroup(ws, synth.Q4_K, inner, outers) for _ in range(ncopy)]
+    singles = [[D.DeviceWeight(torch.from_numpy(w).cuda(), synth.Q4_K, inner, o)
+                for w, o in zip(ws, outers)] for _ in range(ncopy)]
+    total = sum(outers)
+    ys = torch.empty(ncopy, total, device="cuda")
+    offs = groups[0].offsets
+
+    def one(i):
+        groups[i % ncopy].gemv(x, ys[i % ncopy])
+
+    def three(i):
+        for w, o, r in zip(singles[i % ncopy], offs, outers):
+            D.gemv(w, x, ys[i % ncopy, o:o + r])
+    us1 = both_ways_us(torch, stream, one, ncopy, 20, 3)[0]
+    us3 = both_ways_us(torch, stream, three, ncopy, 20, 3)[0]
+    for g in groups:
+        g.release()
+    nbytes = sum(w.size for w in ws) + 4 * inner + 4 * total
+    return dict(group_us=us1, separate_us=us3, group_gbs=nbytes / (us1 * 1e-6) / 1e9)
+
+
 def lm_head(torch, stream, synth, D):
     vocab, hidden = 151936, 2048
     rng = synth.rng_for(0xC2)
@@ -862,6 +893,12 @@ def main():
         k8 = q8k_gemv(torch, stream, synth, D)
         log(f"  {k8['us']:.2f} us, {k8['gbs']:.0f} GB/s")
         extras.update(q4k_gemv_q8k_us=k8["us"], q4k_gemv_q8k_gbs=k8["gbs"])
+        log("attention input projections, Q4_K 4096+1024+1024 rows x 4096")
+        qk = qkv_group(torch, stream, synth, D)
+        log(f"  one grouped GEMV {qk['group_us']:.2f} us ({qk['group_gbs']:.0f} GB/s), "
+            f"three GEMVs {qk['separate_us']:.2f} us")
+        extras.update(qkv_group_gemv_us=qk["group_us"], qkv_group_gemv_gbs=qk["group_gbs"],
+                      qkv_three_gemvs_us=qk["separate_us"])
         log("Q6_K lm_head 151936x2048 + argmax")
         lm = lm_head(torch, stream, synth, D)
         log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s (graph {lm['graph_us']:.2f}, stream {lm['stream_us']:.2f})")

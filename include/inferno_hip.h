@@ -102,6 +102,20 @@ int ihip_weight_forget(const void *host);
 int ihip_weight_fingerprint(const void *host, size_t bytes, uint64_t *fp);
 /* Device address of a registered weight (for the *_dev entry points). */
 int ihip_weight_device_ptr(uint64_t handle, const void **dev);
+/* Weights that multiply the same input -- the attention's wq, wk and wv
+ * (src/ModelCPU.jl:789-791), the SSM's in and gate projections (:570-571) --
+ * uploaded back to back as ONE registered weight of outers[0] + ... +
+ * outers[n-1] rows (1 <= n <= 64, one GGML type, one row length inner).
+ * ihip_gemv_dev over it computes every member's outputs in one launch:
+ * member i's are out[o_i .. o_i + outers[i] - 1] with o_i the rows before it,
+ * and its blocks start ihip_weight_bytes(type, inner, o_i) bytes into the
+ * group (Q4_K 4096 + 1024 + 1024 rows x 4096 columns: 5.3 us as one launch
+ * against 10.3 us as three). */
+int ihip_weight_register_group(const void *const *hosts, const int *outers, int n, int ggml_type,
+                               int inner, uint64_t *handle);
+/* Bytes of an outer x inner weight of a GGML type (0 for an unknown type or
+ * an inner that is not a whole number of blocks). */
+size_t ihip_weight_bytes(int ggml_type, int inner, int outer);
 
 /* ---- drop-in mirrors of src/kernels/quant_kernels.c ------------------- */
 /* Same arguments as q{4,5,6}_k_gemv (quant_kernels.c:602, 620, 638); the
@@ -142,6 +156,10 @@ int ihip_gguf_tensor_info(uint64_t file_handle, int64_t index, char *name, size_
  * rather than 4 bytes per element: copies nbytes into dst. */
 int ihip_gguf_tensor_bytes(uint64_t file_handle, const char *name, void *dst, size_t dst_bytes);
 int ihip_gguf_upload(uint64_t file_handle, const char *name, uint64_t *weight_handle);
+/* ihip_weight_register_group from the file: the named tensors (one type, one
+ * ne0) back to back as one registered weight, in the order given. */
+int ihip_gguf_upload_group(uint64_t file_handle, const char *const *names, int n,
+                           uint64_t *weight_handle);
 
 /* ---- int8-activation variant: the reference C numerics, bit for bit ---- */
 /* Q8_K block: float d, int8 qs[256], int16 bsums[16] (292 bytes,

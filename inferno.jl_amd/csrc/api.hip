@@ -64,6 +64,7 @@ struct Weight {
 // mixed by a 64-bit multiply / xor-shift hash.  About 1 KB is read whatever
 // the size, so it is checked on every host-pointer call.
 constexpr int kFpWindows = 64;
+constexpr int kMaxGroup = 64; // weights in one group upload
 
 uint64_t fp_mix(uint64_t h, uint64_t v)
 {
@@ -281,6 +282,55 @@ int upload_locked(const void *host, size_t bytes, int type, int inner, int outer
     c.by_handle[h] = w;
     if (cache_by_host)
         c.by_host[host] = h;
+    *handle = h;
+    return IHIP_OK;
+}
+
+// Several weights of one type and row length uploaded back to back as one
+// registered weight of sum(outers) rows (member i's bytes at its rows'
+// offset): one GEMV over it computes every member's outputs.  bytes[i], when
+// given, is what member i's source holds.
+int upload_group_locked(const void *const *hosts, const size_t *bytes, const int *outers, int n,
+                        int type, int inner, uint64_t *handle)
+{
+    Ctx &c = ctx();
+    if (!hosts || !outers || !handle)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (n <= 0 || n > kMaxGroup)
+        return fail(IHIP_ERR_INVALID, "a group holds 1 to %d weights, not %d", kMaxGroup, n);
+    int64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!hosts[i])
+            return fail(IHIP_ERR_INVALID, "null pointer (member %d)", i);
+        RET_IF(check_shape(type, inner, outers[i]));
+        if (bytes && bytes[i] < weight_bytes(type, inner, outers[i]))
+            return fail(IHIP_ERR_INVALID, "member %d: %zu bytes < %zu needed for %dx%d type %d", i,
+                        bytes[i], weight_bytes(type, inner, outers[i]), outers[i], inner, type);
+        total += outers[i];
+    }
+    if (total > INT32_MAX)
+        return fail(IHIP_ERR_INVALID, "a group's rows must stay below 2^31");
+    Weight w;
+    w.bytes = weight_bytes(type, inner, (int)total);
+    w.type = type;
+    w.inner = inner;
+    w.outer = (int)total;
+    w.host = nullptr;
+    w.fp = 0;
+    HIPCHK(hipMalloc(&w.dev, w.bytes));
+    size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+        const size_t b = weight_bytes(type, inner, outers[i]);
+        const hipError_t e = hipMemcpy(static_cast<uint8_t *>(w.dev) + off, hosts[i], b,
+                                       hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(w.dev);
+            return fail(IHIP_ERR_HIP, "weight upload failed: %s", hipGetErrorString(e));
+        }
+        off += b;
+    }
+    const uint64_t h = c.next_handle++;
+    c.by_handle[h] = w;
     *handle = h;
     return IHIP_OK;
 }
@@ -588,6 +638,14 @@ int ihip_register_device_copy(const void *host, size_t bytes, int type, int inne
     return upload_locked(host, weight_bytes(type, inner, outer), type, inner, outer, false, handle);
 }
 
+int ihip_register_device_group(const void *const *hosts, const size_t *bytes, const int *outers,
+                               int n, int type, int inner, uint64_t *handle)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    RET_IF(ready_locked());
+    return upload_group_locked(hosts, bytes, outers, n, type, inner, handle);
+}
+
 extern "C" {
 
 const char *ihip_last_error(void) { return t_err.c_str(); }
@@ -677,6 +735,21 @@ int ihip_weight_register(const void *host, size_t bytes, int ggml_type, int inne
                     weight_bytes(ggml_type, inner, outer), outer, inner, ggml_type);
     return upload_locked(host, weight_bytes(ggml_type, inner, outer), ggml_type, inner, outer,
                          false, handle);
+}
+
+int ihip_weight_register_group(const void *const *hosts, const int *outers, int n, int ggml_type,
+                               int inner, uint64_t *handle)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    RET_IF(ready_locked());
+    return upload_group_locked(hosts, nullptr, outers, n, ggml_type, inner, handle);
+}
+
+size_t ihip_weight_bytes(int ggml_type, int inner, int outer)
+{
+    if (!known_type(ggml_type) || inner <= 0 || outer < 0 || inner % block_elems(ggml_type))
+        return 0;
+    return weight_bytes(ggml_type, inner, outer);
 }
 
 int ihip_weight_release(uint64_t handle)

@@ -272,6 +272,8 @@ int parse(File &f, std::string &err)
 int ihip_fail_msg(int code, const char *msg);
 int ihip_register_device_copy(const void *host, size_t bytes, int type, int inner, int outer,
                               uint64_t *handle);
+int ihip_register_device_group(const void *const *hosts, const size_t *bytes, const int *outers,
+                               int n, int type, int inner, uint64_t *handle);
 
 using namespace ihip_gguf;
 
@@ -404,6 +406,50 @@ int ihip_gguf_upload(uint64_t file_handle, const char *name, uint64_t *weight_ha
     // src/LoaderCPU.jl:130-132: inner = ne0, outer = ne1
     return ihip_register_device_copy(f.map + f.data_offset + t.offset, (size_t)t.nbytes, t.type,
                                      (int)t.dims[0], (int)t.dims[1], weight_handle);
+}
+
+int ihip_gguf_upload_group(uint64_t file_handle, const char *const *names, int n,
+                           uint64_t *weight_handle)
+{
+    if (!names || !weight_handle)
+        return ihip_fail_msg(IHIP_ERR_INVALID, "null pointer");
+    if (n <= 0 || n > 64)
+        return ihip_fail_msg(IHIP_ERR_INVALID, "a group holds 1 to 64 tensors");
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_files.find(file_handle);
+    if (it == g_files.end())
+        return ihip_fail_msg(IHIP_ERR_INVALID, "unknown GGUF handle");
+    const File &f = it->second;
+    std::vector<const void *> hosts((size_t)n);
+    std::vector<size_t> bytes((size_t)n);
+    std::vector<int> outers((size_t)n);
+    int type = -1;
+    int64_t inner = -1;
+    for (int i = 0; i < n; ++i) {
+        if (!names[i])
+            return ihip_fail_msg(IHIP_ERR_INVALID, "null tensor name");
+        auto ti = f.by_name.find(names[i]);
+        if (ti == f.by_name.end())
+            return ihip_fail_msg(IHIP_ERR_INVALID, (std::string("tensor not found: ") + names[i]).c_str());
+        const Tensor &t = f.tensors[ti->second];
+        if (t.type != 8 && t.type != 12 && t.type != 13 && t.type != 14 && t.type != 20)
+            return ihip_fail_msg(IHIP_ERR_INVALID, "only Q4_K, Q5_K, Q6_K, Q8_0 and IQ4_NL tensors are "
+                                                   "kept quantized on the device");
+        if (t.ndim > 2 || t.dims[0] > INT32_MAX || t.dims[1] > INT32_MAX)
+            return ihip_fail_msg(IHIP_ERR_INVALID, "a weight tensor has rank 1 or 2 and int-sized dims");
+        if (i == 0) {
+            type = t.type;
+            inner = t.dims[0];
+        } else if (t.type != type || t.dims[0] != inner) {
+            return ihip_fail_msg(IHIP_ERR_INVALID, "the tensors of a group share one type and one row "
+                                                   "length (ne0)");
+        }
+        hosts[(size_t)i] = f.map + f.data_offset + t.offset;
+        bytes[(size_t)i] = (size_t)t.nbytes;
+        outers[(size_t)i] = (int)t.dims[1];
+    }
+    return ihip_register_device_group(hosts.data(), bytes.data(), outers.data(), n, type, (int)inner,
+                                      weight_handle);
 }
 
 } // extern "C"

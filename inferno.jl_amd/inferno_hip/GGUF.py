@@ -84,6 +84,16 @@ def upload(file: GGUFFile, name: str) -> int:
     return h.value
 
 
+def upload_group(file: GGUFFile, names) -> int:
+    """Registry handle of the named tensors (one type, one ne0) uploaded back
+    to back as one weight of their summed rows: one GEMV over it computes
+    every member's outputs (ihip_gguf_upload_group)."""
+    arr = (C.c_char_p * len(names))(*[n.encode() for n in names])
+    h = C.c_uint64(0)
+    check(lib().ihip_gguf_upload_group(file.handle, arr, len(names), C.byref(h)))
+    return h.value
+
+
 def device_ptr(handle: int) -> int:
     p = C.c_void_p(0)
     check(lib().ihip_weight_device_ptr(handle, C.byref(p)))

@@ -60,6 +60,8 @@ SIGNATURES = {
     "ihip_weight_release": ([_u64], _i),
     "ihip_weight_forget": ([_vp], _i),
     "ihip_weight_device_ptr": ([_u64, C.POINTER(_vp)], _i),
+    "ihip_weight_register_group": ([C.POINTER(_vp), C.POINTER(_i), _i, _i, _i, C.POINTER(_u64)], _i),
+    "ihip_weight_bytes": ([_i, _i, _i], _sz),
     "ihip_weight_fingerprint": ([_vp, _sz, C.POINTER(_u64)], _i),
     "ihip_q4_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
     "ihip_q5_k_gemv": ([_vp, _vp, _vp, _vp, _i, _i], _i),
@@ -74,6 +76,7 @@ SIGNATURES = {
                                C.POINTER(_i64), C.POINTER(_u64), C.POINTER(_u64)], _i),
     "ihip_gguf_tensor_bytes": ([_u64, C.c_char_p, _vp, _sz], _i),
     "ihip_gguf_upload": ([_u64, C.c_char_p, C.POINTER(_u64)], _i),
+    "ihip_gguf_upload_group": ([_u64, C.POINTER(C.c_char_p), _i, C.POINTER(_u64)], _i),
     "ihip_quantize_row_q8_k": ([_vp, _vp, _i64], _i),
     "ihip_vec_dot_q4_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),
     "ihip_vec_dot_q5_k_q8_k": ([_vp, _vp, _i, C.POINTER(C.c_float)], _i),

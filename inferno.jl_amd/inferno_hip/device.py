@@ -6,6 +6,7 @@ torch's current stream (or ``stream``) and returns without synchronizing.
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
 
 import torch
@@ -84,6 +85,46 @@ class ArgmaxWorkspace:
         if fl & _lib.FLAG_POSINF:
             raise IHIPArgumentError(_lib.IHIP_ERR_NONFINITE, "logits must not contain +Inf")
         return int(self.token.item())
+
+
+class WeightGroup:
+    """Host weights of one GGML type and row length uploaded back to back as
+    one registered weight (ihip_weight_register_group), e.g. wq, wk and wv:
+    `whole` is the group as one DeviceWeight of the summed rows, `members[i]`
+    member i's rows inside it, `offsets[i]` its first output row.  Freed by
+    release()."""
+
+    def __init__(self, hosts, ggml_type: int, inner: int, outers):
+        import numpy as np
+        self._keep = [np.ascontiguousarray(h, dtype=np.uint8) for h in hosts]
+        n = len(self._keep)
+        ptrs = (C.c_void_p * n)(*[h.ctypes.data for h in self._keep])
+        rows = (C.c_int * n)(*outers)
+        h = C.c_uint64(0)
+        check(lib().ihip_weight_register_group(ptrs, rows, n, ggml_type, inner, C.byref(h)))
+        self.handle = h.value
+        p = C.c_void_p(0)
+        check(lib().ihip_weight_device_ptr(self.handle, C.byref(p)))
+        self.ptr = p.value
+        self.ggml_type, self.inner, self.outers = ggml_type, inner, list(outers)
+        self.offsets = [sum(outers[:i]) for i in range(n)]
+
+    def member_ptr(self, i: int) -> int:
+        return self.ptr + lib().ihip_weight_bytes(self.ggml_type, self.inner, self.offsets[i])
+
+    def gemv(self, x: torch.Tensor, out: torch.Tensor = None, stream=None) -> torch.Tensor:
+        """Every member's outputs in one launch: out[offsets[i]:][:outers[i]]."""
+        total = sum(self.outers)
+        if out is None:
+            out = torch.empty(total, dtype=torch.float32, device=x.device)
+        check(lib().ihip_gemv_dev(self.ggml_type, self.ptr, _ptr(x, torch.float32, "x"),
+                                  _ptr(out, torch.float32, "out"), self.inner, total, _stream(stream)))
+        return out
+
+    def release(self):
+        if self.handle:
+            check(lib().ihip_weight_release(self.handle))
+            self.handle = 0
 
 
 def gemv(w: DeviceWeight, x: torch.Tensor, out: torch.Tensor = None, stream=None):

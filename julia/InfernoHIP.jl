@@ -25,8 +25,9 @@ Beyond the reference's three modules, `QuantizedKernels` also has
 `iq4_nl_gemv!` and the batched prefill `q4_k_gemm!` on host arrays;
 `InfernoHIP.Device` has the unfused device calls of a device-resident forward
 (`gemv!`, `dequantize!`, `rmsnorm!`, `gate_up_swiglu!`,
-`lm_head_argmax_norm!`); `InfernoHIP.GGUF` loads GGUF tensors straight into
-device memory (`open_gguf`, `tensor_count`, `tensor_info`, `upload`,
+`lm_head_argmax_norm!`, and `register_group` for weights that share an
+input); `InfernoHIP.GGUF` loads GGUF tensors straight into device memory
+(`open_gguf`, `tensor_count`, `tensor_info`, `upload`, `upload_group`,
 `release`, `close_gguf`).
 
 Errors: every library call returns a status; a non-zero status becomes an
@@ -598,6 +599,7 @@ module Device
 # vectors, asynchronous on `stream` (a hipStream_t).  Weights are device
 # pointers to GGML blocks (e.g. `GGUF.upload`).
 export gemv!, dequantize!, rmsnorm!, gate_up_swiglu!, lm_head_argmax_norm!
+export register_group, weight_bytes
 
 import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
 
@@ -689,6 +691,41 @@ function lm_head_argmax_norm!(xn::AbstractVector{Float32}, logits::Union{Nothing
     return read_token(ws, stream)
 end
 
+"""`weight_bytes(w_type, inner, outer) -> Int`: bytes of an outer x inner weight."""
+weight_bytes(w_type::Integer, inner::Integer, outer::Integer) =
+    Int(ccall((:ihip_weight_bytes, LIBIHIP), Csize_t, (Cint, Cint, Cint), w_type, inner, outer))
+
+"""
+    register_group(datas, w_type, inner, outers) -> (handle, device_pointer)
+
+Host weights that share an input -- wq, wk and wv (src/ModelCPU.jl:789-791)
+-- uploaded back to back as one weight of `sum(outers)` rows: `gemv!` over it
+with `outer = sum(outers)` computes every member's outputs in one launch
+(member i's rows follow the rows of the members before it, and its blocks
+start `weight_bytes(w_type, inner, rows before it)` into the group).
+Free it with `GGUF.release(handle)`.
+"""
+function register_group(datas::Vector{Vector{UInt8}}, w_type::Integer, inner::Integer,
+                        outers::Vector{<:Integer})
+    require()
+    n = length(datas)
+    n == length(outers) || throw(DimensionMismatch("one row count per weight"))
+    for (d, o) in zip(datas, outers)
+        length(d) >= weight_bytes(w_type, inner, o) || throw(ArgumentError("a weight is too short"))
+    end
+    ptrs = [pointer(d) for d in datas]
+    rows = Cint.(outers)
+    h = Ref{UInt64}(0)
+    GC.@preserve datas begin
+        check(ccall((:ihip_weight_register_group, LIBIHIP), Cint,
+                    (Ptr{Ptr{UInt8}}, Ptr{Cint}, Cint, Cint, Cint, Ref{UInt64}),
+                    ptrs, rows, n, w_type, inner, h))
+    end
+    p = Ref{Ptr{Cvoid}}(C_NULL)
+    check(ccall((:ihip_weight_device_ptr, LIBIHIP), Cint, (UInt64, Ref{Ptr{Cvoid}}), h[], p))
+    return h[], p[]
+end
+
 end # module Device
 
 # ============================================================================
@@ -697,7 +734,7 @@ module GGUF
 # (src/LoaderCPU.jl:125-163) straight into device memory: the file is
 # memory-mapped and parsed by the library, and each quantized tensor is
 # uploaded once into the weight registry.
-export open_gguf, close_gguf, tensor_count, tensor_info, upload, release
+export open_gguf, close_gguf, tensor_count, tensor_info, upload, upload_group, release
 
 import ..InfernoHIP: LIBIHIP, check
 
@@ -752,6 +789,24 @@ pointer feeds the `Device` and `FusedKernels` calls until `release(handle)`.
 function upload(fh::UInt64, name::AbstractString)
     h = Ref{UInt64}(0)
     check(ccall((:ihip_gguf_upload, LIBIHIP), Cint, (UInt64, Cstring, Ref{UInt64}), fh, name, h))
+    p = Ref{Ptr{Cvoid}}(C_NULL)
+    check(ccall((:ihip_weight_device_ptr, LIBIHIP), Cint, (UInt64, Ref{Ptr{Cvoid}}), h[], p))
+    return h[], p[]
+end
+
+"""
+    upload_group(fh, names) -> (handle, device_pointer)
+
+The named tensors (one type, one ne0), e.g. a layer's attn_q, attn_k and
+attn_v, uploaded back to back as one weight (see `Device.register_group`).
+"""
+function upload_group(fh::UInt64, names::Vector{String})
+    h = Ref{UInt64}(0)
+    ptrs = [pointer(n) for n in names]  # Julia strings end in a NUL byte
+    GC.@preserve names begin
+        check(ccall((:ihip_gguf_upload_group, LIBIHIP), Cint,
+                    (UInt64, Ptr{Ptr{UInt8}}, Cint, Ref{UInt64}), fh, ptrs, length(names), h))
+    end
     p = Ref{Ptr{Cvoid}}(C_NULL)
     check(ccall((:ihip_weight_device_ptr, LIBIHIP), Cint, (UInt64, Ref{Ptr{Cvoid}}), h[], p))
     return h[], p[]

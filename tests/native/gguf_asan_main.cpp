@@ -2,7 +2,7 @@
 // compiled as plain C++ with AddressSanitizer and UndefinedBehaviorSanitizer
 // by tests/test_gguf_asan.py) over every file named on the command line: open,
 // header info, every tensor's info, its bytes into an exact and a short buffer,
-// the upload hook, close.  Accepting or refusing a file are both fine; an
+// the upload hooks (one tensor, then groups of them), close.  Accepting or refusing a file are both fine; an
 // out-of-bounds read, a leak-free use after free or undefined behaviour makes
 // the sanitizers end the process with a report.  CPU only.
 #include "inferno_hip.h"
@@ -27,6 +27,19 @@ int ihip_register_device_copy(const void *host, size_t bytes, int, int, int, uin
     unsigned acc = 0;
     for (size_t i = 0; i < bytes; ++i)
         acc += p[i];
+    *handle = acc | 1u;
+    return IHIP_ERR_NO_DEVICE;
+}
+
+int ihip_register_device_group(const void *const *hosts, const size_t *bytes, const int *, int n,
+                               int, int, uint64_t *handle)
+{
+    unsigned acc = 0;
+    for (int m = 0; m < n; ++m) {
+        const unsigned char *p = (const unsigned char *)hosts[m];
+        for (size_t i = 0; i < bytes[m]; ++i)
+            acc += p[i];
+    }
     *handle = acc | 1u;
     return IHIP_ERR_NO_DEVICE;
 }
@@ -68,6 +81,24 @@ int main(int argc, char **argv)
             uint64_t wh = 0;
             ihip_gguf_upload(fh, name, &wh);
         }
+        // group uploads: every tensor at once, then each neighbouring pair
+        std::vector<std::string> names;
+        for (int64_t i = 0; i < count; ++i) {
+            char name[512];
+            int type = 0, ndim = 0;
+            int64_t dims[4];
+            uint64_t offset = 0, nbytes = 0;
+            if (ihip_gguf_tensor_info(fh, i, name, sizeof name, &type, &ndim, dims, &offset, &nbytes) == IHIP_OK)
+                names.push_back(name);
+        }
+        std::vector<const char *> np;
+        for (const std::string &n : names)
+            np.push_back(n.c_str());
+        uint64_t gh = 0;
+        if (!np.empty())
+            ihip_gguf_upload_group(fh, np.data(), (int)np.size(), &gh);
+        for (size_t i = 0; i + 1 < np.size(); ++i)
+            ihip_gguf_upload_group(fh, np.data() + i, 2, &gh);
         ihip_gguf_tensor_info(fh, count, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr);
         ihip_gguf_close(fh);
         ++accepted;

@@ -185,6 +185,77 @@ def test_uploaded_tensors_feed_the_gemv(tmp_path):
             _lib.check(_lib.lib().ihip_weight_release(h))
 
 
+@pytest.mark.gpu
+def test_grouped_tensors_feed_one_gemv(tmp_path):
+    """wq, wk and wv (src/ModelCPU.jl:789-791) uploaded back to back, from
+    the file and from host arrays: one GEMV over the group gives every
+    member's outputs, bit-identical to each member's own GEMV; each member's
+    blocks sit at ihip_weight_bytes of the rows before it; tensors of another
+    type or row length, and unknown names, are refused."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import oracle
+    from inferno_hip import GGUF, _lib
+    from inferno_hip import device as D
+    from inferno_hip._lib import IHIPArgumentError
+    rng = synth.rng_for(0x6609)
+    inner = 2048
+    specs = (("blk.0.attn_q.weight", 2048), ("blk.0.attn_k.weight", 256), ("blk.0.attn_v.weight", 256))
+    for gt in (synth.Q4_K, synth.Q6_K):
+        tensors = [(n, (inner, o), gt, synth.weight(rng, gt, o, inner).tobytes()) for n, o in specs]
+        tensors.append(("blk.0.ffn_up.weight", (1024, 64), gt, synth.weight(rng, gt, 64, 1024).tobytes()))
+        other = synth.Q8_0 if gt != synth.Q8_0 else synth.Q4_K
+        tensors.append(("blk.0.attn_o.weight", (inner, 32), other, synth.weight(rng, other, 32, inner).tobytes()))
+        blob, _, _ = gguf_bytes([("general.alignment", U32, 32)], tensors, 32)
+        x = synth.activations(rng, inner)
+        xd = torch.from_numpy(x).cuda()
+        names = [n for n, _ in specs]
+        outers = [o for _, o in specs]
+        with open_file(tmp_path, blob, f"g{gt}.gguf") as f:
+            print(f"[case] GGUF group upload type {gt}: rows {outers} x {inner}", flush=True)
+            h = GGUF.upload_group(f, names)
+            ws = [GGUF.get_tensor_raw_bytes(f, n) for n in names]
+            total = sum(outers)
+            y = torch.empty(total, device="cuda")
+            _lib.check(_lib.lib().ihip_gemv_dev(gt, GGUF.device_ptr(h), xd.data_ptr(), y.data_ptr(),
+                                                inner, total, D._stream(None)))
+            grp = D.WeightGroup(ws, gt, inner, outers)
+            y2 = grp.gemv(xd)
+            o = 0
+            for i, (w, r) in enumerate(zip(ws, outers)):
+                own = D.gemv(D.DeviceWeight(torch.from_numpy(w).cuda(), gt, inner, r), xd).cpu().numpy()
+                got = y[o:o + r].cpu().numpy()
+                ref = oracle.gemv_f64(gt, w, x, inner, r)
+                tol = oracle.tolerance(oracle.row_norms(gt, w, inner, r), x)
+                assert np.all(np.abs(got.astype(np.float64) - ref) <= tol), f"member {i}"
+                assert np.array_equal(got.view(np.uint32), own.view(np.uint32)), f"member {i} (file group)"
+                assert np.array_equal(y2[o:o + r].cpu().numpy().view(np.uint32), own.view(np.uint32))
+                # the member's blocks inside the group
+                assert _lib.lib().ihip_weight_bytes(gt, inner, o) == o * w.size // r
+                torch.cuda.synchronize()
+                assert torch.equal(torch.from_numpy(w).cuda(), _device_bytes(torch, grp.member_ptr(i), w.size))
+                o += r
+            grp.release()
+            _lib.check(_lib.lib().ihip_weight_release(h))
+            with pytest.raises(IHIPArgumentError, match="share one type"):
+                GGUF.upload_group(f, names + ["blk.0.attn_o.weight"])
+            with pytest.raises(IHIPArgumentError, match="share one type"):
+                GGUF.upload_group(f, names + ["blk.0.ffn_up.weight"])
+            with pytest.raises(IHIPArgumentError, match="not found"):
+                GGUF.upload_group(f, names + ["blk.9.attn_q.weight"])
+
+
+def _device_bytes(torch, ptr, n):
+    """n bytes at a device address, copied into a fresh device tensor."""
+    import ctypes as C
+    out = torch.empty(n, dtype=torch.uint8, device="cuda")
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    assert hip.hipMemcpy(out.data_ptr(), ptr, n, 3) == 0  # device to device
+    return out
+
+
 def test_bench_writer_round_trips(tmp_path):
     """bench.py's GGUF writer (the file its registry-load leg times) is read
     back by the native reader: names, types, dimensions and bytes."""

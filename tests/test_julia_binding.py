@@ -130,5 +130,6 @@ def test_julia_source_is_structurally_balanced():
     opens = len(re.findall(r"^\s*(module|function|if|for|while|begin|let|struct|mutable struct)\b",
                            code, re.M))
     opens += len(re.findall(r"^\s*\w[^=\n]*=\s*(if|begin|let)\b", code, re.M))
+    opens += len(re.findall(r"^\s*(?:\w+\.)?@\w+[^\n]*\bbegin\s*$", code, re.M))  # GC.@preserve x begin
     ends = len(re.findall(r"^\s*end\b", code, re.M))
     assert opens == ends, (opens, ends)
