@@ -221,6 +221,12 @@ int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inn
 /* ---- device-pointer entry points (asynchronous on `stream`) -------------- */
 int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int inner,
                   int outer, ihip_stream stream);
+/* out = resid + W x, the residual add folded into the GEMV's epilogue: the
+ * attention's output projection (src/ModelCPU.jl:885) and the layer's
+ * x .+= residual (:909) as one launch.  resid may be out (in place); x may
+ * not overlap out. */
+int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float *resid,
+                      float *out, int inner, int outer, ihip_stream stream);
 int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n,
                         ihip_stream stream);
 /* h = silu(Wg x) .* (Wu x) (h: inter floats).  A matching Q4_K or Q5_K pair

@@ -1030,6 +1030,22 @@ int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int 
     return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream);
 }
 
+int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float *resid, float *out,
+                      int inner, int outer, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    if (!resid)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    // every workgroup reads all of x while rows of out are written
+    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out;
+    if (x && out && inner > 0 && outer > 0 && xa < oa + 4 * (uintptr_t)outer &&
+        oa < xa + 4 * (uintptr_t)inner)
+        return fail(IHIP_ERR_INVALID, "x overlaps out");
+    return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream, resid, kEpiAdd);
+}
+
 int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n, ihip_stream stream)
 {
     std::lock_guard<std::recursive_mutex> lk(ctx().mu);

@@ -135,6 +135,18 @@ def gemv(w: DeviceWeight, x: torch.Tensor, out: torch.Tensor = None, stream=None
     return out
 
 
+def gemv_add(w: DeviceWeight, x: torch.Tensor, resid: torch.Tensor, out: torch.Tensor = None,
+             stream=None) -> torch.Tensor:
+    """out = resid + W x in one launch (ihip_gemv_add_dev); out defaults to
+    resid (in place), as the layer's x .+= residual (src/ModelCPU.jl:909)."""
+    if out is None:
+        out = resid
+    check(lib().ihip_gemv_add_dev(w.ggml_type, _ptr(w.data), _ptr(x, torch.float32, "x"),
+                                  _ptr(resid, torch.float32, "resid"), _ptr(out, torch.float32, "out"),
+                                  w.inner, w.outer, _stream(stream)))
+    return out
+
+
 def dequantize(w: DeviceWeight, out: torch.Tensor = None, stream=None):
     n = w.inner * w.outer
     if out is None:

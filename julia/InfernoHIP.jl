@@ -24,7 +24,7 @@ meaning, so a caller switches by changing what it `using`s:
 Beyond the reference's three modules, `QuantizedKernels` also has
 `iq4_nl_gemv!` and the batched prefill `q4_k_gemm!` on host arrays;
 `InfernoHIP.Device` has the unfused device calls of a device-resident forward
-(`gemv!`, `dequantize!`, `rmsnorm!`, `gate_up_swiglu!`,
+(`gemv!`, `gemv_add!`, `dequantize!`, `rmsnorm!`, `gate_up_swiglu!`,
 `lm_head_argmax_norm!`, and `register_group` for weights that share an
 input); `InfernoHIP.GGUF` loads GGUF tensors straight into device memory
 (`open_gguf`, `tensor_count`, `tensor_info`, `upload`, `upload_group`,
@@ -598,7 +598,7 @@ module Device
 # rmsnorm_cpu!, the gate/up pair and the final norm + lm_head on device
 # vectors, asynchronous on `stream` (a hipStream_t).  Weights are device
 # pointers to GGML blocks (e.g. `GGUF.upload`).
-export gemv!, dequantize!, rmsnorm!, gate_up_swiglu!, lm_head_argmax_norm!
+export gemv!, gemv_add!, dequantize!, rmsnorm!, gate_up_swiglu!, lm_head_argmax_norm!
 export register_group, weight_bytes
 
 import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
@@ -617,6 +617,25 @@ function gemv!(out::AbstractVector{Float32}, w_type::Integer, w::Ptr{Cvoid},
     check(ccall((:ihip_gemv_dev, LIBIHIP), Cint,
                 (Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
                 w_type, w, x, out, inner, outer, stream))
+    return out
+end
+
+"""
+    gemv_add!(out, w_type, w, x, resid, inner, outer; stream)
+
+`out = resid + W x` in one launch: the attention's output projection
+(src/ModelCPU.jl:885) with the layer's `x .+= residual` (:909) folded into the
+GEMV's epilogue.  `resid` may be `out` (in place); x may not overlap out.
+"""
+function gemv_add!(out::AbstractVector{Float32}, w_type::Integer, w::Ptr{Cvoid},
+                   x::AbstractVector{Float32}, resid::AbstractVector{Float32}, inner::Integer,
+                   outer::Integer; stream::Ptr{Cvoid} = C_NULL)
+    require()
+    length(out) >= outer && length(resid) >= outer && length(x) >= inner ||
+        throw(DimensionMismatch("x, resid or out too short"))
+    check(ccall((:ihip_gemv_add_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
+                w_type, w, x, resid, out, inner, outer, stream))
     return out
 end
 

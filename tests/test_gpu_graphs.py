@@ -120,6 +120,17 @@ def test_gemv_graph(t, outer, inner, other_work):
         assert np.all(np.abs(e.cpu().numpy().astype(np.float64) - ref) <= tol)
 
 
+def test_gemv_add_graph(other_work):
+    from inferno_hip import device as D
+    say("graph gemv_add Q4_K 4096x4096")
+    rng = synth.rng_for(0x6AD)
+    _, dw = dweight(rng, synth.Q4_K, 4096, 4096)
+    xd = dev(synth.activations(rng, 4096))
+    resid = dev(rng.standard_normal(4096).astype(np.float32))
+    out = torch.empty(4096, device="cuda")
+    replay_matches_eager(lambda: D.gemv_add(dw, xd, resid, out), [out], other_work)
+
+
 def test_dequantize_graph(other_work):
     from inferno_hip import device as D
     say("graph dequantize Q6_K 512x2048")

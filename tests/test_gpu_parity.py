@@ -750,6 +750,41 @@ def test_prefill_q4k(T, outer, inner):
         assert float(np.max(ratio32)) < 0.25
 
 
+@pytest.mark.parametrize("t,outer,inner,woff", [
+    (synth.Q4_K, 4096, 4096, 0),    # the attention output projection's shape
+    (synth.Q5_K, 1000, 2048, 0),
+    (synth.Q6_K, 777, 12288, 0),    # streamed rows
+    (synth.Q8_0, 515, 4096, 0),
+    (synth.IQ4_NL, 300, 2048, 0),
+    (synth.Q4_K, 129, 1024, 2),     # weight off 16-byte alignment: byte-granular kernel
+])
+def test_gemv_add_folds_the_residual(t, outer, inner, woff):
+    """out = resid + W x (the attention output projection and the layer's
+    residual add, src/ModelCPU.jl:885, 909) in one launch: bit-identical to
+    the GEMV followed by an fp32 add, in place and not; x overlapping out is
+    refused."""
+    from inferno_hip import device as D
+    from inferno_hip._lib import IHIPArgumentError
+    say(f"gemv_add type={t} {outer}x{inner} weight offset {woff}")
+    rng = synth.rng_for(0x5F0 + t + outer)
+    w = synth.weight(rng, t, outer, inner)
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
+    buf[woff:woff + w.size] = dev(w)
+    dw = D.DeviceWeight(buf[woff:woff + w.size], t, inner, outer)
+    x = dev(synth.activations(rng, inner))
+    resid = dev(rng.standard_normal(outer).astype(np.float32))
+    want = (D.gemv(dw, x) + resid).cpu().numpy()
+    out = torch.full((outer,), float("nan"), device="cuda")
+    got = D.gemv_add(dw, x, resid, out).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    inplace = resid.clone()
+    D.gemv_add(dw, x, inplace)
+    assert np.array_equal(inplace.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    both = torch.zeros(inner + outer, device="cuda")
+    with pytest.raises(IHIPArgumentError, match="overlaps"):
+        D.gemv_add(dw, both[:inner], resid, both[inner - 1:inner - 1 + outer])
+
+
 @pytest.mark.parametrize("inner", [2048, 4096])
 def test_prefill_shared_activations_match_the_one_call_entry_point(inner):
     """One rounding of X, then products with several weights, as the
