@@ -96,12 +96,13 @@ class WeightGroup:
 
     def __init__(self, hosts, ggml_type: int, inner: int, outers):
         import numpy as np
-        self._keep = [np.ascontiguousarray(h, dtype=np.uint8) for h in hosts]
-        n = len(self._keep)
-        ptrs = (C.c_void_p * n)(*[h.ctypes.data for h in self._keep])
+        src = [np.ascontiguousarray(h, dtype=np.uint8) for h in hosts]  # alive through the upload
+        n = len(src)
+        ptrs = (C.c_void_p * n)(*[a.ctypes.data for a in src])
         rows = (C.c_int * n)(*outers)
         h = C.c_uint64(0)
         check(lib().ihip_weight_register_group(ptrs, rows, n, ggml_type, inner, C.byref(h)))
+        del src
         self.handle = h.value
         p = C.c_void_p(0)
         check(lib().ihip_weight_device_ptr(self.handle, C.byref(p)))
