@@ -421,6 +421,51 @@ def qkv_group(torch, stream, synth, D):
     return dict(group_us=us1, separate_us=us3, group_gbs=nbytes / (us1 * 1e-6) / 1e9)
 
 
+def decode_layer(torch, stream, synth, D):
+    """The quantized work of one decoder layer's decode step
+    (src/ModelCPU.jl:900-920) at hidden 4096, K/V projections of 1024 rows,
+    intermediate 12288: the input rmsnorm, one grouped GEMV for wq/wk/wv
+    (Q4_K), the output projection wo (Q4_K) with the residual add folded in --
+    its input is the q rows, standing in for the attention core, which is
+    outside this path -- and the FFN block (post-norm folded into the fused
+    Q4_K gate/up pass, Q6_K down with the residual).  Five launches; 4 rotated
+    copies of the layer's 121 MB of weights."""
+    hid, kv, inter = 4096, 1024, 12288
+    rng = synth.rng_for(0xC8)
+    ncopy = 4
+    qkv_w = [synth.weight(rng, synth.Q4_K, o, hid) for o in (hid, kv, kv)]
+    wo = synth.weight(rng, synth.Q4_K, hid, hid)
+    wg = synth.weight(rng, synth.Q4_K, inter, hid)
+    wu = synth.weight(rng, synth.Q4_K, inter, hid)
+    wd = synth.weight(rng, synth.Q6_K, hid, inter)
+    layers = []
+    for _ in range(ncopy):
+        layers.append(dict(
+            qkv=D.WeightGroup(qkv_w, synth.Q4_K, hid, (hid, kv, kv)),
+            wo=D.DeviceWeight(torch.from_numpy(wo).cuda(), synth.Q4_K, hid, hid),
+            wg=D.DeviceWeight(torch.from_numpy(wg).cuda(), synth.Q4_K, hid, inter),
+            wu=D.DeviceWeight(torch.from_numpy(wu).cuda(), synth.Q4_K, hid, inter),
+            wd=D.DeviceWeight(torch.from_numpy(wd).cuda(), synth.Q6_K, inter, hid)))
+    wbytes = sum(w.size for w in qkv_w) + wo.size + wg.size + wu.size + wd.size
+    x0 = torch.from_numpy(synth.activations(rng, hid)).cuda()
+    n1 = torch.from_numpy(rng.uniform(0.5, 1.5, hid).astype(np.float32)).cuda()
+    n2 = torch.from_numpy(rng.uniform(0.5, 1.5, hid).astype(np.float32)).cuda()
+    xn, x1 = torch.empty(hid, device="cuda"), torch.empty(hid, device="cuda")
+    qkv = torch.empty(hid + 2 * kv, device="cuda")
+    h = torch.empty(inter + hid, device="cuda")
+
+    def step(i):
+        L = layers[i % ncopy]
+        D.rmsnorm(x0, n1, 1e-6, out=xn)
+        L["qkv"].gemv(xn, qkv)
+        D.gemv_add(L["wo"], qkv[:hid], x0, out=x1)
+        D.ffn_block(L["wg"], L["wu"], L["wd"], n2, 1e-6, x1, h=h)
+    us = both_ways_us(torch, stream, step, ncopy, 20, 3)[0]
+    for L in layers:
+        L["qkv"].release()
+    return dict(us=us, gbs=wbytes / (us * 1e-6) / 1e9, weight_bytes=wbytes)
+
+
 def lm_head(torch, stream, synth, D):
     vocab, hidden = 151936, 2048
     rng = synth.rng_for(0xC2)
@@ -899,6 +944,10 @@ def main():
             f"three GEMVs {qk['separate_us']:.2f} us")
         extras.update(qkv_group_gemv_us=qk["group_us"], qkv_group_gemv_gbs=qk["group_gbs"],
                       qkv_three_gemvs_us=qk["separate_us"])
+        log("decode layer: norm, grouped wq/wk/wv, wo + residual, FFN block (hidden 4096)")
+        dl = decode_layer(torch, stream, synth, D)
+        log(f"  {dl['us']:.2f} us per layer, {dl['gbs']:.0f} GB/s over {dl['weight_bytes'] / 1e6:.0f} MB of weights")
+        extras.update(decode_layer_us=dl["us"], decode_layer_gbs=dl["gbs"])
         log("Q6_K lm_head 151936x2048 + argmax")
         lm = lm_head(torch, stream, synth, D)
         log(f"  {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s (graph {lm['graph_us']:.2f}, stream {lm['stream_us']:.2f})")
