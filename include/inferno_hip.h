@@ -223,8 +223,8 @@ int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int 
                   int outer, ihip_stream stream);
 /* out = resid + W x, the residual add folded into the GEMV's epilogue: the
  * attention's output projection (src/ModelCPU.jl:885) and the layer's
- * x .+= residual (:909) as one launch.  resid may be out (in place); x may
- * not overlap out. */
+ * x .+= residual (:909) as one launch.  resid may be out (in place) but not
+ * overlap it otherwise; x may not overlap out. */
 int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float *resid,
                       float *out, int inner, int outer, ihip_stream stream);
 int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n,

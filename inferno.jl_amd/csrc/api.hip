@@ -1039,10 +1039,13 @@ int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float 
     if (!resid)
         return fail(IHIP_ERR_INVALID, "null pointer");
     // every workgroup reads all of x while rows of out are written
-    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out;
+    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out, ra = (uintptr_t)resid;
     if (x && out && inner > 0 && outer > 0 && xa < oa + 4 * (uintptr_t)outer &&
         oa < xa + 4 * (uintptr_t)inner)
         return fail(IHIP_ERR_INVALID, "x overlaps out");
+    // row r reads resid[r] and writes out[r]: in place is fine, a shifted overlap races
+    if (out && outer > 0 && ra != oa && ra < oa + 4 * (uintptr_t)outer && oa < ra + 4 * (uintptr_t)outer)
+        return fail(IHIP_ERR_INVALID, "resid overlaps out without being out");
     return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream, resid, kEpiAdd);
 }
 

@@ -783,6 +783,9 @@ def test_gemv_add_folds_the_residual(t, outer, inner, woff):
     both = torch.zeros(inner + outer, device="cuda")
     with pytest.raises(IHIPArgumentError, match="overlaps"):
         D.gemv_add(dw, both[:inner], resid, both[inner - 1:inner - 1 + outer])
+    shifted = torch.zeros(outer + 4, device="cuda")
+    with pytest.raises(IHIPArgumentError, match="resid overlaps out"):
+        D.gemv_add(dw, x, shifted[4:4 + outer], shifted[:outer])
 
 
 @pytest.mark.parametrize("inner", [2048, 4096])
