@@ -380,6 +380,10 @@ int gemv_dev_locked(int type, const void *w, const float *x, float *out, int inn
     RET_IF(check_shape(type, inner, outer));
     if (!w || !x || !out)
         return fail(IHIP_ERR_INVALID, "null pointer");
+    // every workgroup reads all of x while rows of out are written
+    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out;
+    if (xa < oa + 4 * (uintptr_t)outer && oa < xa + 4 * (uintptr_t)inner)
+        return fail(IHIP_ERR_INVALID, "x overlaps out");
     hipError_t e = fast_ok(type, w, x, inner)
                        ? launch_gemv(type, w, x, out, inner, outer, s, resid, epi)
                        : launch_gemv_generic(type, w, x, out, inner, outer, s, resid, epi);
@@ -1039,10 +1043,7 @@ int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float 
     if (!resid)
         return fail(IHIP_ERR_INVALID, "null pointer");
     // every workgroup reads all of x while rows of out are written
-    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out, ra = (uintptr_t)resid;
-    if (x && out && inner > 0 && outer > 0 && xa < oa + 4 * (uintptr_t)outer &&
-        oa < xa + 4 * (uintptr_t)inner)
-        return fail(IHIP_ERR_INVALID, "x overlaps out");
+    const uintptr_t oa = (uintptr_t)out, ra = (uintptr_t)resid;
     // row r reads resid[r] and writes out[r]: in place is fine, a shifted overlap races
     if (out && outer > 0 && ra != oa && ra < oa + 4 * (uintptr_t)outer && oa < ra + 4 * (uintptr_t)outer)
         return fail(IHIP_ERR_INVALID, "resid overlaps out without being out");

@@ -101,6 +101,25 @@ def test_prefill_operands_past_32_bit_offsets_are_refused():
     assert rc == _lib.IHIP_ERR_INVALID
 
 
+def test_gemv_operands_that_race_are_refused():
+    """Every workgroup of a device GEMV reads all of x while rows of out are
+    written, so x overlapping out is refused, as is a residual that overlaps
+    out without being out; checked before any device work (the pointers are
+    never dereferenced, and every call here is refused before a launch)."""
+    import ctypes as C
+    from inferno_hip import _lib
+    L = _lib.lib()
+    w = C.c_void_p(1 << 20)
+    base = 1 << 24
+    x, out = C.c_void_p(base), C.c_void_p(base + 4 * 100)  # 256-float x covers out[0..155]
+    assert L.ihip_gemv_dev(12, w, x, out, 256, 64, None) == _lib.IHIP_ERR_INVALID
+    assert b"overlaps" in L.ihip_last_error()
+    r = C.c_void_p(base + 4 * 1000)
+    o = C.c_void_p(base + 4 * 1004)  # out shifted by 4 floats from resid
+    assert L.ihip_gemv_add_dev(12, w, x, r, o, 256, 64, None) == _lib.IHIP_ERR_INVALID
+    assert b"resid overlaps out" in L.ihip_last_error()
+
+
 def test_no_device_is_an_error_not_a_fallback():
     import torch
     if torch.cuda.is_available():
