@@ -219,8 +219,11 @@ int ihip_prefill_q4_k(const uint8_t *w, const float *X, float *Y, int T, int inn
                       int outer);
 
 /* ---- device-pointer entry points (asynchronous on `stream`) -------------- */
-/* out = W x on device pointers; x may not overlap out (every GEMV entry
- * point refuses that with IHIP_ERR_INVALID). */
+/* out = W x on device pointers.  Device entry points refuse, with
+ * IHIP_ERR_INVALID, inputs that overlap the outputs their kernels write while
+ * every workgroup reads the inputs (x and out here; x and h of the gate/up
+ * pair; x and logits; src and dst of a dequantization; X, xh and Y of the
+ * prefill). */
 int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int inner,
                   int outer, ihip_stream stream);
 /* out = resid + W x, the residual add folded into the GEMV's epilogue: the

@@ -183,6 +183,14 @@ int check_shape(int type, int inner, int outer)
 
 bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Whether [a, a + an) and [b, b + bn) share a byte.  A kernel that reads one
+// buffer in every workgroup while it writes the other races on any overlap.
+bool overlap(const void *a, size_t an, const void *b, size_t bn)
+{
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return an && bn && x < y + bn && y < x + an;
+}
+
 // Grow a host-path staging buffer.  Only the host-pointer entry points use
 // these buffers, on the library stream; work still queued there (an earlier
 // call that failed half-way) finishes before the old buffer is freed.
@@ -381,8 +389,7 @@ int gemv_dev_locked(int type, const void *w, const float *x, float *out, int inn
     if (!w || !x || !out)
         return fail(IHIP_ERR_INVALID, "null pointer");
     // every workgroup reads all of x while rows of out are written
-    const uintptr_t xa = (uintptr_t)x, oa = (uintptr_t)out;
-    if (xa < oa + 4 * (uintptr_t)outer && oa < xa + 4 * (uintptr_t)inner)
+    if (overlap(x, 4 * (size_t)inner, out, 4 * (size_t)outer))
         return fail(IHIP_ERR_INVALID, "x overlaps out");
     hipError_t e = fast_ok(type, w, x, inner)
                        ? launch_gemv(type, w, x, out, inner, outer, s, resid, epi)
@@ -412,6 +419,11 @@ int gate_up_dev_locked(int gt, const void *wg, int ut, const void *wu, const flo
     RET_IF(check_shape(ut, hidden, inter));
     if (!wg || !wu || !x || !h)
         return fail(IHIP_ERR_INVALID, "null pointer");
+    if (overlap(x, 4 * (size_t)hidden, h, 4 * (size_t)inter))
+        return fail(IHIP_ERR_INVALID, "x overlaps h");
+    if (xn && (overlap(x, 4 * (size_t)hidden, xn, 4 * (size_t)hidden) ||
+               overlap(h, 4 * (size_t)inter, xn, 4 * (size_t)hidden)))
+        return fail(IHIP_ERR_INVALID, "the norm scratch overlaps x or h");
     if (gate_up_fused(gt, wg, ut, wu, x, hidden, norm_w)) {
         hipError_t e = launch_gate_up_swiglu(gt, wg, wu, x, h, hidden, inter, s, norm_w, eps);
         if (e != hipSuccess)
@@ -448,6 +460,8 @@ int lm_head_dev_locked(int type, const void *w, const float *x, float *logits, i
     RET_IF(check_shape(type, hidden, vocab));
     if (!w || !x || !token || !flags || !ws)
         return fail(IHIP_ERR_INVALID, "null pointer");
+    if (logits && overlap(x, 4 * (size_t)hidden, logits, 4 * (size_t)vocab))
+        return fail(IHIP_ERR_INVALID, "x overlaps logits");
     if (lm_head_fused(type, w, x, hidden, vocab)) {
         hipError_t e = launch_lm_head_argmax(type, w, x, logits, token, flags, hidden, vocab, ws, s);
         if (e != hipSuccess)
@@ -1043,9 +1057,8 @@ int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float 
     if (!resid)
         return fail(IHIP_ERR_INVALID, "null pointer");
     // every workgroup reads all of x while rows of out are written
-    const uintptr_t oa = (uintptr_t)out, ra = (uintptr_t)resid;
     // row r reads resid[r] and writes out[r]: in place is fine, a shifted overlap races
-    if (out && outer > 0 && ra != oa && ra < oa + 4 * (uintptr_t)outer && oa < ra + 4 * (uintptr_t)outer)
+    if (out && outer > 0 && resid != out && overlap(resid, 4 * (size_t)outer, out, 4 * (size_t)outer))
         return fail(IHIP_ERR_INVALID, "resid overlaps out without being out");
     return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream, resid, kEpiAdd);
 }
@@ -1064,6 +1077,9 @@ int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n, i
         return IHIP_OK;
     if (!src || !dst)
         return fail(IHIP_ERR_INVALID, "null pointer");
+    if (overlap(src, (size_t)(n / block_elems(ggml_type)) * (size_t)block_bytes(ggml_type), dst,
+                4 * (size_t)n))
+        return fail(IHIP_ERR_INVALID, "src overlaps dst");
     hipError_t e = launch_dequant(ggml_type, src, dst, n, al16(src) && al16(dst), (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "dequant launch failed: %s", hipGetErrorString(e));
@@ -1195,6 +1211,12 @@ int ihip_prefill_q4_k_dev(const void *w, const float *X, void *xh, float *Y, int
         return fail(IHIP_ERR_INVALID, "null pointer");
     if (!al16(w) || !al16(X) || !al16(xh) || !al16(Y))
         return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    {
+        const size_t xb = 4 * (size_t)T * (size_t)inner, yb = 4 * (size_t)T * (size_t)outer;
+        const size_t sb = prefill_scratch_bytes(T, inner);
+        if (overlap(X, xb, Y, yb) || overlap(xh, sb, X, xb) || overlap(xh, sb, Y, yb))
+            return fail(IHIP_ERR_INVALID, "X, xh and Y must not overlap");
+    }
     hipError_t e = launch_prefill_q4k(w, X, xh, Y, T, inner, outer, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
@@ -1218,6 +1240,8 @@ int ihip_prefill_convert_dev(const float *X, void *xh, int T, int inner, ihip_st
         return fail(IHIP_ERR_INVALID, "null pointer");
     if (!al16(X) || !al16(xh))
         return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    if (overlap(X, 4 * (size_t)T * (size_t)inner, xh, prefill_scratch_bytes(T, inner)))
+        return fail(IHIP_ERR_INVALID, "X and xh must not overlap");
     hipError_t e = launch_prefill_convert(X, xh, T, inner, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill conversion launch failed: %s", hipGetErrorString(e));
@@ -1242,6 +1266,8 @@ int ihip_prefill_q4_k_xh_dev(const void *w, void *xh, float *Y, int T, int inner
         return fail(IHIP_ERR_INVALID, "null pointer");
     if (!al16(w) || !al16(xh) || !al16(Y))
         return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    if (overlap(xh, prefill_scratch_bytes(T, inner), Y, 4 * (size_t)T * (size_t)outer))
+        return fail(IHIP_ERR_INVALID, "xh and Y must not overlap");
     hipError_t e = launch_prefill_gemm(w, xh, Y, T, inner, outer, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));
@@ -1263,6 +1289,8 @@ int ihip_prefill_q4_k_f32_dev(const void *w, const float *X, float *Y, int T, in
         return fail(IHIP_ERR_INVALID, "null pointer");
     if (!al16(w) || !al16(X) || !al16(Y))
         return fail(IHIP_ERR_INVALID, "prefill pointers must be 16-byte aligned");
+    if (overlap(X, 4 * (size_t)T * (size_t)inner, Y, 4 * (size_t)T * (size_t)outer))
+        return fail(IHIP_ERR_INVALID, "X and Y must not overlap");
     hipError_t e = launch_prefill_q4k_f32(w, X, Y, T, inner, outer, (hipStream_t)stream);
     if (e != hipSuccess)
         return fail(IHIP_ERR_HIP, "prefill launch failed: %s", hipGetErrorString(e));

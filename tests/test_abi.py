@@ -118,6 +118,13 @@ def test_gemv_operands_that_race_are_refused():
     o = C.c_void_p(base + 4 * 1004)  # out shifted by 4 floats from resid
     assert L.ihip_gemv_add_dev(12, w, x, r, o, 256, 64, None) == _lib.IHIP_ERR_INVALID
     assert b"resid overlaps out" in L.ihip_last_error()
+    h = C.c_void_p(base + 4 * 100)  # 64 floats inside x's 256
+    assert L.ihip_gate_up_swiglu_dev(12, w, 12, w, x, h, 256, 64, None) == _lib.IHIP_ERR_INVALID
+    assert b"x overlaps h" in L.ihip_last_error()
+    assert L.ihip_dequantize_dev(12, x, C.c_void_p(base + 64), 256, None) == _lib.IHIP_ERR_INVALID
+    assert b"src overlaps dst" in L.ihip_last_error()
+    assert L.ihip_prefill_q4_k_f32_dev(w, x, C.c_void_p(base + 16), 2, 256, 64, None) == _lib.IHIP_ERR_INVALID
+    assert b"must not overlap" in L.ihip_last_error()
 
 
 def test_no_device_is_an_error_not_a_fallback():
