@@ -3,9 +3,11 @@
 The reference's kernels are plain C functions behind `ccall`
 (src/QuantizedKernels.jl:84-148), so a Julia engine may call them from
 several threads at once.  Here:
-* the device entry points run from three host threads at once, each on its
+* the device entry points run from four host threads at once, each on its
   own stream with its own buffers and workspaces (an FFN, an lm_head with its
-  argmax, a prefill whose K is split over workgroups), 12 calls each; every
+  argmax, a prefill whose K is split over workgroups, and the composite calls:
+  a grouped wq/wk/wv GEMV, wo with its residual, one prefill rounding for two
+  weights), 12 calls each; every
   call's outputs are copied aside on the caller's stream and must equal an
   eager call's bit for bit (nothing a `*_dev` call touches is shared between
   callers);
@@ -99,10 +101,30 @@ def test_device_entry_points_from_threads_on_their_own_streams():
     X = dev(rng.standard_normal((T, inner)).astype(np.float32))
     Y, xh = torch.empty(T, outer, device="cuda"), D.prefill_scratch(T, inner)
 
+    # the composite calls: wq/wk/wv as one group, wo with the residual, and
+    # the prefill's two halves over two weights
+    qkv = D.WeightGroup([synth.weight(rng, synth.Q4_K, o, 2048) for o in (2048, 512, 512)],
+                        synth.Q4_K, 2048, (2048, 512, 512))
+    wo = dweight(rng, synth.Q4_K, 2048, 2048)
+    ax, ar = dev(synth.activations(rng, 2048)), dev(synth.activations(rng, 2048))
+    qout, aout = torch.empty(3072, device="cuda"), torch.empty(2048, device="cuda")
+    wp2 = dweight(rng, synth.Q4_K, 1024, inner)
+    X2 = dev(rng.standard_normal((T, inner)).astype(np.float32))
+    Y2a, Y2b, xh2 = torch.empty(T, outer, device="cuda"), torch.empty(T, 1024, device="cuda"), \
+        D.prefill_scratch(T, inner)
+
+    def composite(s):
+        qkv.gemv(ax, qout, stream=s)
+        D.gemv_add(wo, ax, ar, aout, stream=s)
+        D.prefill_convert(X2, xh2, stream=s)
+        D.prefill_q4_k_xh(wp, xh2, T, Y2a, stream=s)
+        D.prefill_q4_k_xh(wp2, xh2, T, Y2b, stream=s)
+
     jobs = [
         (lambda s: D.ffn_swiglu(wg, wu, wd, fx, h=fh, y=fy, stream=s), [fh, fy]),
         (lambda s: D.lm_head_argmax(wl, lx, ws, logits=logits, stream=s), [logits, ws.token, ws.flags]),
         (lambda s: D.prefill_q4_k(wp, X, Y, xh, stream=s), [Y]),
+        (composite, [qout, aout, Y2a, Y2b]),
     ]
     eager = []
     for call, outs in jobs:
@@ -130,6 +152,7 @@ def test_device_entry_points_from_threads_on_their_own_streams():
         for r in range(REPS):
             for i, (k, e) in enumerate(zip(kept[j][r], eager[j])):
                 assert same_bits(k, e), f"job {j} call {r} output {i} differs from the eager call"
+    qkv.release()
 
 
 def test_host_entry_points_from_threads():
