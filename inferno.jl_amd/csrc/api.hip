@@ -1056,8 +1056,8 @@ int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float 
         return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
     if (!resid)
         return fail(IHIP_ERR_INVALID, "null pointer");
-    // every workgroup reads all of x while rows of out are written
     // row r reads resid[r] and writes out[r]: in place is fine, a shifted overlap races
+    // (x against out is checked with every GEMV)
     if (out && outer > 0 && resid != out && overlap(resid, 4 * (size_t)outer, out, 4 * (size_t)outer))
         return fail(IHIP_ERR_INVALID, "resid overlaps out without being out");
     return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream, resid, kEpiAdd);
