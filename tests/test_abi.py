@@ -127,6 +127,21 @@ def test_gemv_operands_that_race_are_refused():
     assert b"must not overlap" in L.ihip_last_error()
 
 
+def test_weight_bytes_follow_the_block_layouts():
+    """ihip_weight_bytes (the offsets of a weight group's members) against the
+    block sizes of the formats (src/QuantsCPU.jl:22-26); no device
+    needed."""
+    from inferno_hip import _lib, synth
+    L = _lib.lib()
+    for t in (synth.Q4_K, synth.Q5_K, synth.Q6_K, synth.Q8_0, synth.IQ4_NL):
+        e, b = synth.BLOCK_ELEMS[t], synth.BLOCK_BYTES[t]
+        for inner, outer in ((e, 1), (4096, 1024), (8 * e, 0), (12288, 4096)):
+            assert L.ihip_weight_bytes(t, inner, outer) == outer * (inner // e) * b
+        assert L.ihip_weight_bytes(t, e + 1, 4) == 0      # not a whole number of blocks
+        assert L.ihip_weight_bytes(t, e, -1) == 0
+    assert L.ihip_weight_bytes(99, 256, 4) == 0             # unknown type
+
+
 def test_no_device_is_an_error_not_a_fallback():
     import torch
     if torch.cuda.is_available():
