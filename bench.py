@@ -424,11 +424,11 @@ def qkv_group(torch, stream, synth, D):
 def decode_layer(torch, stream, synth, D):
     """The quantized work of one decoder layer's decode step
     (src/ModelCPU.jl:900-920) at hidden 4096, K/V projections of 1024 rows,
-    intermediate 12288: the input rmsnorm, one grouped GEMV for wq/wk/wv
-    (Q4_K), the output projection wo (Q4_K) with the residual add folded in --
+    intermediate 12288: one grouped GEMV for wq/wk/wv (Q4_K) with the input
+    rmsnorm folded in, the output projection wo (Q4_K) with the residual add folded in --
     its input is the q rows, standing in for the attention core, which is
     outside this path -- and the FFN block (post-norm folded into the fused
-    Q4_K gate/up pass, Q6_K down with the residual).  Five launches; 4 rotated
+    Q4_K gate/up pass, Q6_K down with the residual).  Four launches; 4 rotated
     copies of the layer's 121 MB of weights."""
     hid, kv, inter = 4096, 1024, 12288
     rng = synth.rng_for(0xC8)
@@ -456,8 +456,7 @@ def decode_layer(torch, stream, synth, D):
 
     def step(i):
         L = layers[i % ncopy]
-        D.rmsnorm(x0, n1, 1e-6, out=xn)
-        L["qkv"].gemv(xn, qkv)
+        L["qkv"].gemv_norm(n1, 1e-6, x0, qkv, xn=xn)  # the input norm folded in
         D.gemv_add(L["wo"], qkv[:hid], x0, out=x1)
         D.ffn_block(L["wg"], L["wu"], L["wd"], n2, 1e-6, x1, h=h)
     us = both_ways_us(torch, stream, step, ncopy, 20, 3)[0]
@@ -944,7 +943,7 @@ def main():
             f"three GEMVs {qk['separate_us']:.2f} us")
         extras.update(qkv_group_gemv_us=qk["group_us"], qkv_group_gemv_gbs=qk["group_gbs"],
                       qkv_three_gemvs_us=qk["separate_us"])
-        log("decode layer: norm, grouped wq/wk/wv, wo + residual, FFN block (hidden 4096)")
+        log("decode layer: grouped wq/wk/wv with the norm, wo + residual, FFN block (hidden 4096)")
         dl = decode_layer(torch, stream, synth, D)
         log(f"  {dl['us']:.2f} us per layer, {dl['gbs']:.0f} GB/s over {dl['weight_bytes'] / 1e6:.0f} MB of weights")
         extras.update(decode_layer_us=dl["us"], decode_layer_gbs=dl["gbs"])

@@ -232,6 +232,15 @@ int ihip_gemv_dev(int ggml_type, const void *w, const float *x, float *out, int 
  * overlap it otherwise; x may not overlap out. */
 int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float *resid,
                       float *out, int inner, int outer, ihip_stream stream);
+/* out = W (rmsnorm(x) .* norm_w): a layer's input norm (src/ModelCPU.jl:903,
+ * rmsnorm_cpu! at :111-123) folded into the GEMV that consumes it, e.g. the
+ * grouped wq/wk/wv (:789-791).  One launch for 16-byte aligned Q4_K / Q5_K
+ * rows of at most 4096 columns and fewer than 8192 rows.  Otherwise xn
+ * (inner floats of caller scratch) receives the normed input and the plain
+ * GEMV follows; xn may be NULL only where the norm folds. */
+int ihip_gemv_norm_dev(int ggml_type, const void *w, const float *norm_w, float eps,
+                       const float *x, float *xn, float *out, int inner, int outer,
+                       ihip_stream stream);
 int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n,
                         ihip_stream stream);
 /* h = silu(Wg x) .* (Wu x) (h: inter floats).  A matching Q4_K or Q5_K pair

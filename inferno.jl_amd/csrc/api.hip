@@ -1063,6 +1063,35 @@ int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float 
     return gemv_dev_locked(ggml_type, w, x, out, inner, outer, (hipStream_t)stream, resid, kEpiAdd);
 }
 
+int ihip_gemv_norm_dev(int ggml_type, const void *w, const float *norm_w, float eps, const float *x,
+                       float *xn, float *out, int inner, int outer, ihip_stream stream)
+{
+    std::lock_guard<std::recursive_mutex> lk(ctx().mu);
+    if (disabled())
+        return fail(IHIP_ERR_DISABLED, "IHIP_DISABLE is set");
+    RET_IF(check_shape(ggml_type, inner, outer));
+    if (!w || !norm_w || !x || !out)
+        return fail(IHIP_ERR_INVALID, "null pointer");
+    if (overlap(x, 4 * (size_t)inner, out, 4 * (size_t)outer))
+        return fail(IHIP_ERR_INVALID, "x overlaps out");
+    if (gemv_norm_fusable(ggml_type, inner, outer) && fast_ok(ggml_type, w, x, inner) && al16(norm_w)) {
+        hipError_t e = launch_gemv_norm(ggml_type, w, x, norm_w, eps, out, inner, outer, (hipStream_t)stream);
+        if (e != hipSuccess)
+            return fail(IHIP_ERR_HIP, "gemv launch failed: %s", hipGetErrorString(e));
+        return IHIP_OK;
+    }
+    // the norm first, into the caller's scratch, then the plain GEMV
+    if (!xn)
+        return fail(IHIP_ERR_INVALID, "this GEMV (type %d, %d x %d) cannot fold the norm: pass xn",
+                    ggml_type, outer, inner);
+    if (overlap(xn, 4 * (size_t)inner, out, 4 * (size_t)outer))
+        return fail(IHIP_ERR_INVALID, "xn overlaps out");
+    hipError_t e = launch_rmsnorm(x, norm_w, eps, xn, inner, (hipStream_t)stream);
+    if (e != hipSuccess)
+        return fail(IHIP_ERR_HIP, "rmsnorm launch failed: %s", hipGetErrorString(e));
+    return gemv_dev_locked(ggml_type, w, xn, out, inner, outer, (hipStream_t)stream);
+}
+
 int ihip_dequantize_dev(int ggml_type, const void *src, float *dst, int64_t n, ihip_stream stream)
 {
     std::lock_guard<std::recursive_mutex> lk(ctx().mu);

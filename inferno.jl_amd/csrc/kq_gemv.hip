@@ -368,17 +368,17 @@ __device__ __forceinline__ float kdig_dot(const KBytes &B, int j, const XDig &X)
 //     1/sqrt(mean(x^2) + eps) at the end, so the norm costs no extra pass.
 //   plain: y[r] = resid[r] + (W x)[r], the residual add of
 //     src/ModelCPU.jl:913-920 (resid may be y itself).
-template <int FMT, int R, bool GATEUP, bool EXT, int NWV>
-__global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restrict__ W,
-                                                    const uint8_t *__restrict__ W2,
-                                                    const float *__restrict__ x,
-                                                    float *y, int outer, int nblk,
-                                                    const float *__restrict__ nw, float eps,
-                                                    const float *resid, int epi)
+//
+// The body is shared with k_gemv_kwide_norm (a plain GEMV whose input is the
+// normed x) through kwide_body, which takes NORM and RESID directly.
+template <int FMT, int R, bool GATEUP, bool NORM, bool RESID, int NWV>
+__device__ __forceinline__ void kwide_body(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
+                                           const float *__restrict__ x, float *y, int outer, int nblk,
+                                           const float *__restrict__ nw, float eps, const float *resid,
+                                           int epi)
 {
     using F = KFmt<FMT>;
     constexpr int NW = GATEUP ? 2 : 1;
-    constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
     constexpr int NT = NWV * 64, NXV = xnv(NT);
     // x's three digit planes, its sub-block sums and exponents
     __shared__ __attribute__((aligned(16))) uint32_t xbuf[3 * kDigPlaneDw];
@@ -484,6 +484,31 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restri
         if (lane == 0 && row < outer)
             y[row] = RESID ? epi_apply(rv[r], v, epi) : v;
     }
+}
+
+template <int FMT, int R, bool GATEUP, bool EXT, int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kwide(const uint8_t *__restrict__ W,
+                                                    const uint8_t *__restrict__ W2,
+                                                    const float *__restrict__ x,
+                                                    float *y, int outer, int nblk,
+                                                    const float *__restrict__ nw, float eps,
+                                                    const float *resid, int epi)
+{
+    kwide_body<FMT, R, GATEUP, GATEUP && EXT, !GATEUP && EXT, NWV>(W, W2, x, y, outer, nblk, nw, eps,
+                                                                   resid, epi);
+}
+
+// y = W (rmsnorm(x) .* nw) for one weight: the gate/up pass's folded norm
+// (x .* nw staged, the row sums scaled by 1/sqrt(mean(x^2) + eps)) in front of
+// a plain GEMV, e.g. the grouped wq/wk/wv behind a layer's input norm
+// (src/ModelCPU.jl:903, 789-791).
+template <int FMT, int R, int NWV>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kwide_norm(const uint8_t *__restrict__ W,
+                                                         const float *__restrict__ x, float *y,
+                                                         int outer, int nblk,
+                                                         const float *__restrict__ nw, float eps)
+{
+    kwide_body<FMT, R, false, true, false, NWV>(W, nullptr, x, y, outer, nblk, nw, eps, nullptr, 0);
 }
 
 // Persistent form of the digit kernel for matrices of many rows and at most
@@ -1681,6 +1706,40 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
                    : launch_sdig<kIQ4_NL, false>(w, x, y, inner, outer, nullptr, s, resid, epi);
     default: return hipErrorInvalidValue;
     }
+}
+
+bool gemv_norm_fusable(int type, int inner, int outer)
+{
+    const int nblk = inner / 256;
+    return (type == kQ4_K || type == kQ5_K) && inner % 256 == 0 && nblk <= 16 &&
+           !kwide_takes_kpers(nblk, outer);
+}
+
+template <int FMT>
+static void launch_kwide_norm(const void *w, const float *x, const float *nw, float eps, float *y,
+                              int inner, int outer, hipStream_t s)
+{
+    constexpr int NWV = 8;
+    const int nblk = inner / 256;
+    const uint8_t *W = (const uint8_t *)w;
+    if (kwide_one_row(outer))
+        hipLaunchKernelGGL((k_gemv_kwide_norm<FMT, 1, NWV>), dim3((outer + NWV - 1) / NWV), dim3(NWV * 64),
+                           0, s, W, x, y, outer, nblk, nw, eps);
+    else
+        hipLaunchKernelGGL((k_gemv_kwide_norm<FMT, 2, NWV>), dim3((outer + 2 * NWV - 1) / (2 * NWV)),
+                           dim3(NWV * 64), 0, s, W, x, y, outer, nblk, nw, eps);
+}
+
+hipError_t launch_gemv_norm(int type, const void *w, const float *x, const float *nw, float eps,
+                            float *y, int inner, int outer, hipStream_t s)
+{
+    if (!gemv_norm_fusable(type, inner, outer))
+        return hipErrorNotSupported;
+    if (type == kQ4_K)
+        launch_kwide_norm<kQ4_K>(w, x, nw, eps, y, inner, outer, s);
+    else
+        launch_kwide_norm<kQ5_K>(w, x, nw, eps, y, inner, outer, s);
+    return hipGetLastError();
 }
 
 bool gate_up_fusable(int gate_type, int up_type)

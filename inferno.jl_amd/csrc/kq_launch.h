@@ -11,6 +11,12 @@ namespace ihip {
 // residual add, or the SwiGLU of an unfused gate/up pair); resid may be y.
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
                        hipStream_t s, const float *resid = nullptr, int epi = 0);
+// y = W (rmsnorm(x) .* nw) in one launch (the wide kernel's folded norm) for
+// Q4_K / Q5_K rows of at most 16 blocks below the persistent kernel's row
+// count; hipErrorNotSupported otherwise.
+bool gemv_norm_fusable(int type, int inner, int outer);
+hipError_t launch_gemv_norm(int type, const void *w, const float *x, const float *nw, float eps,
+                            float *y, int inner, int outer, hipStream_t s);
 bool gate_up_fusable(int gate_type, int up_type);
 // norm_w != nullptr: the input is rmsnorm(x) .* norm_w (eps inside the root).
 hipError_t launch_gate_up_swiglu(int type, const void *wg, const void *wu, const float *x,

@@ -95,6 +95,7 @@ SIGNATURES = {
                                       _vp, _vp], _i),
     "ihip_gemv_dev": ([_i, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_gemv_add_dev": ([_i, _vp, _vp, _vp, _vp, _i, _i, _vp], _i),
+    "ihip_gemv_norm_dev": ([_i, _vp, _vp, C.c_float, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_dequantize_dev": ([_i, _vp, _vp, _i64, _vp], _i),
     "ihip_gate_up_swiglu_dev": ([_i, _vp, _i, _vp, _vp, _vp, _i, _i, _vp], _i),
     "ihip_ffn_swiglu_dev": ([_i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _vp], _i),

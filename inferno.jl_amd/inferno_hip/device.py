@@ -113,6 +113,20 @@ class WeightGroup:
     def member_ptr(self, i: int) -> int:
         return self.ptr + lib().ihip_weight_bytes(self.ggml_type, self.inner, self.offsets[i])
 
+    def gemv_norm(self, norm_w: torch.Tensor, eps: float, x: torch.Tensor, out: torch.Tensor = None,
+                  xn: torch.Tensor = None, stream=None) -> torch.Tensor:
+        """Every member's outputs of the normed x in one launch where the norm
+        folds (ihip_gemv_norm_dev over the group)."""
+        total = sum(self.outers)
+        if out is None:
+            out = torch.empty(total, dtype=torch.float32, device=x.device)
+        if xn is None:
+            xn = torch.empty(self.inner, dtype=torch.float32, device=x.device)
+        check(lib().ihip_gemv_norm_dev(self.ggml_type, self.ptr, _ptr(norm_w, torch.float32, "norm_w"), eps,
+                                       _ptr(x, torch.float32, "x"), _ptr(xn, torch.float32, "xn"),
+                                       _ptr(out, torch.float32, "out"), self.inner, total, _stream(stream)))
+        return out
+
     def gemv(self, x: torch.Tensor, out: torch.Tensor = None, stream=None) -> torch.Tensor:
         """Every member's outputs in one launch: out[offsets[i]:][:outers[i]]."""
         total = sum(self.outers)
@@ -145,6 +159,21 @@ def gemv_add(w: DeviceWeight, x: torch.Tensor, resid: torch.Tensor, out: torch.T
     check(lib().ihip_gemv_add_dev(w.ggml_type, _ptr(w.data), _ptr(x, torch.float32, "x"),
                                   _ptr(resid, torch.float32, "resid"), _ptr(out, torch.float32, "out"),
                                   w.inner, w.outer, _stream(stream)))
+    return out
+
+
+def gemv_norm(w: DeviceWeight, norm_w: torch.Tensor, eps: float, x: torch.Tensor,
+              out: torch.Tensor = None, xn: torch.Tensor = None, stream=None) -> torch.Tensor:
+    """out = W (rmsnorm(x) .* norm_w) (ihip_gemv_norm_dev): one launch where
+    the norm folds into the GEMV, else the norm into xn (allocated here when
+    not given) and the plain GEMV."""
+    if out is None:
+        out = torch.empty(w.outer, dtype=torch.float32, device=x.device)
+    if xn is None:
+        xn = torch.empty(w.inner, dtype=torch.float32, device=x.device)
+    check(lib().ihip_gemv_norm_dev(w.ggml_type, _ptr(w.data), _ptr(norm_w, torch.float32, "norm_w"),
+                                   eps, _ptr(x, torch.float32, "x"), _ptr(xn, torch.float32, "xn"),
+                                   _ptr(out, torch.float32, "out"), w.inner, w.outer, _stream(stream)))
     return out
 
 

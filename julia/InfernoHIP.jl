@@ -24,9 +24,9 @@ meaning, so a caller switches by changing what it `using`s:
 Beyond the reference's three modules, `QuantizedKernels` also has
 `iq4_nl_gemv!` and the batched prefill `q4_k_gemm!` on host arrays;
 `InfernoHIP.Device` has the unfused device calls of a device-resident forward
-(`gemv!`, `gemv_add!`, `dequantize!`, `rmsnorm!`, `gate_up_swiglu!`,
-`lm_head_argmax_norm!`, and `register_group` for weights that share an
-input); `InfernoHIP.GGUF` loads GGUF tensors straight into device memory
+(`gemv!`, `gemv_add!`, `gemv_norm!`, `dequantize!`, `rmsnorm!`,
+`gate_up_swiglu!`, `lm_head_argmax_norm!`, and `register_group` for weights
+that share an input); `InfernoHIP.GGUF` loads GGUF tensors straight into device memory
 (`open_gguf`, `tensor_count`, `tensor_info`, `upload`, `upload_group`,
 `release`, `close_gguf`).
 
@@ -598,7 +598,7 @@ module Device
 # rmsnorm_cpu!, the gate/up pair and the final norm + lm_head on device
 # vectors, asynchronous on `stream` (a hipStream_t).  Weights are device
 # pointers to GGML blocks (e.g. `GGUF.upload`).
-export gemv!, gemv_add!, dequantize!, rmsnorm!, gate_up_swiglu!, lm_head_argmax_norm!
+export gemv!, gemv_add!, gemv_norm!, dequantize!, rmsnorm!, gate_up_swiglu!, lm_head_argmax_norm!
 export register_group, weight_bytes
 
 import ..InfernoHIP: LIBIHIP, check, require, ArgmaxWorkspace, token_ptr, flags_ptr, read_token
@@ -636,6 +636,30 @@ function gemv_add!(out::AbstractVector{Float32}, w_type::Integer, w::Ptr{Cvoid},
     check(ccall((:ihip_gemv_add_dev, LIBIHIP), Cint,
                 (Cint, Ptr{Cvoid}, Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Cint, Cint, Ptr{Cvoid}),
                 w_type, w, x, resid, out, inner, outer, stream))
+    return out
+end
+
+"""
+    gemv_norm!(out, w_type, w, norm_w, eps, x, xn, inner, outer; stream)
+
+`out = W (rmsnorm(x) .* norm_w)`: a layer's input norm (src/ModelCPU.jl:903)
+folded into the GEMV that consumes it, e.g. a `register_group` of wq, wk and
+wv (:789-791).  One launch for aligned Q4_K / Q5_K rows of at most 4096
+columns and fewer than 8192 rows; otherwise `xn` (inner floats, may be
+`nothing` where the norm folds) receives the normed x first.
+"""
+function gemv_norm!(out::AbstractVector{Float32}, w_type::Integer, w::Ptr{Cvoid},
+                    norm_w::AbstractVector{Float32}, eps::Real, x::AbstractVector{Float32},
+                    xn::Union{Nothing,AbstractVector{Float32}}, inner::Integer, outer::Integer;
+                    stream::Ptr{Cvoid} = C_NULL)
+    require()
+    length(out) >= outer && length(x) >= inner && length(norm_w) >= inner ||
+        throw(DimensionMismatch("x, norm_w or out too short"))
+    xp = xn === nothing ? Ptr{Float32}(C_NULL) : Base.unsafe_convert(Ptr{Float32}, xn)
+    check(ccall((:ihip_gemv_norm_dev, LIBIHIP), Cint,
+                (Cint, Ptr{Cvoid}, Ptr{Float32}, Cfloat, Ptr{Float32}, Ptr{Float32}, Ptr{Float32}, Cint,
+                 Cint, Ptr{Cvoid}),
+                w_type, w, norm_w, Float32(eps), x, xp, out, inner, outer, stream))
     return out
 end
 

@@ -114,6 +114,32 @@ def _check_block(x_out, h, x, case, gt, dt, hidden, inter, eps):
     check_within(x_out, y_ref, tol, "x + Wd h")
 
 
+@pytest.mark.parametrize("t,outer,inner", [
+    (synth.Q4_K, 6144, 4096),   # wq + wk + wv rows: the norm folded, two rows per wave
+    (synth.Q5_K, 1000, 2048),   # folded, one row per wave
+    (synth.Q4_K, 8192, 4096),   # the persistent kernel's rows: the norm first
+    (synth.Q6_K, 777, 2048),    # another format: the norm first
+    (synth.Q4_K, 300, 5120),    # rows of two passes: the norm first
+])
+def test_gemv_norm(t, outer, inner):
+    """out = W (rmsnorm(x) .* norm_w) (src/ModelCPU.jl:903 then :789-791)
+    within the row bound of the fp64 oracle's normed input, the norm folded
+    into the GEMV or run first into xn."""
+    from inferno_hip import device as D
+    eps = 1e-6
+    rng = synth.rng_for(0xB20 + outer + inner)
+    w = synth.weight(rng, t, outer, inner)
+    x = synth.activations(rng, inner) * np.float32(2.5)
+    nw = rng.uniform(0.5, 1.5, inner).astype(np.float32)
+    say(f"gemv of the normed x type={t} {outer}x{inner}")
+    xn = torch.full((inner,), float("nan"), device="cuda")
+    y = D.gemv_norm(dweight(w, t, inner, outer), dev(nw), eps, dev(x), xn=xn).cpu().numpy()
+    n = oracle.rmsnorm_f64(x, nw, eps)
+    ref = oracle.gemv_f64(t, w, n, inner, outer)
+    nrm = oracle.row_norms(t, w, inner, outer)
+    check_within(y, ref, 1e-4 * nrm * np.linalg.norm(n) + 1e-6 * nrm * np.linalg.norm(n), "W rmsnorm(x)")
+
+
 @pytest.mark.parametrize("hidden,inter,gt,dt", FFN_CASES)
 def test_ffn_block_with_norm_and_residual(hidden, inter, gt, dt):
     from inferno_hip import device as D

@@ -131,6 +131,17 @@ def test_gemv_add_graph(other_work):
     replay_matches_eager(lambda: D.gemv_add(dw, xd, resid, out), [out], other_work)
 
 
+def test_gemv_norm_graph(other_work):
+    from inferno_hip import device as D
+    say("graph gemv of the normed x, Q4_K 6144x4096 (folded)")
+    rng = synth.rng_for(0x6AE)
+    _, dw = dweight(rng, synth.Q4_K, 6144, 4096)
+    xd = dev(synth.activations(rng, 4096))
+    nw = dev(rng.uniform(0.5, 1.5, 4096).astype(np.float32))
+    out, xn = torch.empty(6144, device="cuda"), torch.empty(4096, device="cuda")
+    replay_matches_eager(lambda: D.gemv_norm(dw, nw, 1e-6, xd, out, xn), [out], other_work)
+
+
 def test_dequantize_graph(other_work):
     from inferno_hip import device as D
     say("graph dequantize Q6_K 512x2048")
