@@ -235,7 +235,7 @@ int ihip_gemv_add_dev(int ggml_type, const void *w, const float *x, const float 
 /* out = W (rmsnorm(x) .* norm_w): a layer's input norm (src/ModelCPU.jl:903,
  * rmsnorm_cpu! at :111-123) folded into the GEMV that consumes it, e.g. the
  * grouped wq/wk/wv (:789-791).  One launch for 16-byte aligned Q4_K / Q5_K
- * rows of at most 4096 columns and fewer than 8192 rows.  Otherwise xn
+ * rows of at most 4096 columns.  Otherwise xn
  * (inner floats of caller scratch) receives the normed input and the plain
  * GEMV follows; xn may be NULL only where the norm folds. */
 int ihip_gemv_norm_dev(int ggml_type, const void *w, const float *norm_w, float eps,

@@ -521,7 +521,7 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kwide_norm(const uint8_t *__r
 // k_gemv_kwide<FMT, R, GATEUP, EXT, NWV>.
 // The walk itself over LDS the caller declares (xbuf: 3 * kDigPlaneDw
 // dwords, xsum / xexp: 128 each, ssw: NWV floats).
-template <int FMT, int R, bool GATEUP, bool EXT, int NWV, int NB>
+template <int FMT, int R, bool GATEUP, bool NORM, bool RESID, int NWV, int NB>
 __device__ __forceinline__ void kpers_run(const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2,
                                           const float *__restrict__ x, float *y, int outer, int nblk,
                                           const float *__restrict__ nw, float eps, const float *resid,
@@ -529,7 +529,6 @@ __device__ __forceinline__ void kpers_run(const uint8_t *__restrict__ W, const u
 {
     using F = KFmt<FMT>;
     constexpr int NM = GATEUP ? 2 : 1;
-    constexpr bool NORM = GATEUP && EXT, RESID = !GATEUP && EXT;
     constexpr int NT = NWV * 64, NXV = xnv(NT);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -654,8 +653,25 @@ __global__ __launch_bounds__(NWV * 64) void k_gemv_kpers(const uint8_t *__restri
     __shared__ __attribute__((aligned(16))) float xsum[128];
     __shared__ __attribute__((aligned(8))) int xexp[128];
     __shared__ float ssw[NWV];
-    kpers_run<FMT, R, GATEUP, EXT, NWV, NB>(W, W2, x, y, outer, nblk, nw, eps, resid, epi, xbuf, xsum,
-                                            xexp, ssw);
+    kpers_run<FMT, R, GATEUP, GATEUP && EXT, !GATEUP && EXT, NWV, NB>(W, W2, x, y, outer, nblk, nw, eps,
+                                                                      resid, epi, xbuf, xsum, xexp, ssw);
+}
+
+// The persistent kernel with the folded norm on a single weight,
+// y = W (rmsnorm(x) .* nw) (as k_gemv_kwide_norm, for rows of at most 16
+// blocks past the per-workgroup kernel's row count).
+template <int FMT, int R, int NWV, int NB>
+__global__ __launch_bounds__(NWV * 64) void k_gemv_kpers_norm(const uint8_t *__restrict__ W,
+                                                         const float *__restrict__ x, float *y,
+                                                         int outer, int nblk,
+                                                         const float *__restrict__ nw, float eps)
+{
+    __shared__ __attribute__((aligned(16))) uint32_t xbuf[3 * kDigPlaneDw];
+    __shared__ __attribute__((aligned(16))) float xsum[128];
+    __shared__ __attribute__((aligned(8))) int xexp[128];
+    __shared__ float ssw[NWV];
+    kpers_run<FMT, R, false, true, false, NWV, NB>(W, nullptr, x, y, outer, nblk, nw, eps, nullptr, 0,
+                                                   xbuf, xsum, xexp, ssw);
 }
 
 // Persistent form for rows of more than 16 blocks (2..MP passes of 4096
@@ -1708,11 +1724,9 @@ hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int in
     }
 }
 
-bool gemv_norm_fusable(int type, int inner, int outer)
+bool gemv_norm_fusable(int type, int inner, int)
 {
-    const int nblk = inner / 256;
-    return (type == kQ4_K || type == kQ5_K) && inner % 256 == 0 && nblk <= 16 &&
-           !kwide_takes_kpers(nblk, outer);
+    return (type == kQ4_K || type == kQ5_K) && inner % 256 == 0 && inner / 256 <= 16;
 }
 
 template <int FMT>
@@ -1722,7 +1736,11 @@ static void launch_kwide_norm(const void *w, const float *x, const float *nw, fl
     constexpr int NWV = 8;
     const int nblk = inner / 256;
     const uint8_t *W = (const uint8_t *)w;
-    if (kwide_one_row(outer))
+    if (kwide_takes_kpers(nblk, outer))
+        hipLaunchKernelGGL((k_gemv_kpers_norm<FMT, 1, NWV, 2>),
+                           dim3(std::max(1, std::min(device_cus(), (outer + NWV - 1) / NWV))),
+                           dim3(NWV * 64), 0, s, W, x, y, outer, nblk, nw, eps);
+    else if (kwide_one_row(outer))
         hipLaunchKernelGGL((k_gemv_kwide_norm<FMT, 1, NWV>), dim3((outer + NWV - 1) / NWV), dim3(NWV * 64),
                            0, s, W, x, y, outer, nblk, nw, eps);
     else

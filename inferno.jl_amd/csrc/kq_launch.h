@@ -11,9 +11,9 @@ namespace ihip {
 // residual add, or the SwiGLU of an unfused gate/up pair); resid may be y.
 hipError_t launch_gemv(int type, const void *w, const float *x, float *y, int inner, int outer,
                        hipStream_t s, const float *resid = nullptr, int epi = 0);
-// y = W (rmsnorm(x) .* nw) in one launch (the wide kernel's folded norm) for
-// Q4_K / Q5_K rows of at most 16 blocks below the persistent kernel's row
-// count; hipErrorNotSupported otherwise.
+// y = W (rmsnorm(x) .* nw) in one launch (the wide kernels' folded norm, per
+// workgroup or persistent by row count) for Q4_K / Q5_K rows of at most 16
+// blocks; hipErrorNotSupported otherwise.
 bool gemv_norm_fusable(int type, int inner, int outer);
 hipError_t launch_gemv_norm(int type, const void *w, const float *x, const float *nw, float eps,
                             float *y, int inner, int outer, hipStream_t s);

@@ -645,7 +645,7 @@ end
 `out = W (rmsnorm(x) .* norm_w)`: a layer's input norm (src/ModelCPU.jl:903)
 folded into the GEMV that consumes it, e.g. a `register_group` of wq, wk and
 wv (:789-791).  One launch for aligned Q4_K / Q5_K rows of at most 4096
-columns and fewer than 8192 rows; otherwise `xn` (inner floats, may be
+columns; otherwise `xn` (inner floats, may be
 `nothing` where the norm folds) receives the normed x first.
 """
 function gemv_norm!(out::AbstractVector{Float32}, w_type::Integer, w::Ptr{Cvoid},

@@ -117,7 +117,8 @@ def _check_block(x_out, h, x, case, gt, dt, hidden, inter, eps):
 @pytest.mark.parametrize("t,outer,inner", [
     (synth.Q4_K, 6144, 4096),   # wq + wk + wv rows: the norm folded, two rows per wave
     (synth.Q5_K, 1000, 2048),   # folded, one row per wave
-    (synth.Q4_K, 8192, 4096),   # the persistent kernel's rows: the norm first
+    (synth.Q4_K, 8192, 4096),   # the persistent kernel's rows: folded there too
+    (synth.Q5_K, 10240, 2048),  # wq 8192 + wk/wv 1024 rows of a larger model, persistent
     (synth.Q6_K, 777, 2048),    # another format: the norm first
     (synth.Q4_K, 300, 5120),    # rows of two passes: the norm first
 ])
